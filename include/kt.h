@@ -1,0 +1,123 @@
+/* kt.h - C ABI of libkt_gfx950.so, the MI355X (gfx950) kernel library for Kindi's quantized linear layer.
+
+   It replaces the kernel module Kindi compiles at run time (cp.RawModule over kindi.cu + tc_hip.cu + ...,
+   spec.py:144-151, 187-195; engine.py:88-92) and launches through gpudrv.driver() (gpudrv.py:24-101): a prebuilt
+   shared library, loaded with ctypes, exporting host launchers with plain pointers and sizes.
+
+   Conventions (all entry points):
+   - every pointer argument is a device pointer owned by the caller (as Kindi's CuPy buffers, engine.py:193-204,
+     spec.py:523-593); the library never allocates, frees or synchronizes, and keeps no device state;
+   - `stream` is a hipStream_t (NULL = the null stream); launches are asynchronous and graph-capturable;
+   - the return value is a hipError_t as int: 0 on success, hipErrorInvalidValue (1) for a shape, stride or
+     alignment the kernels do not take (Kindi raises SystemExit / RuntimeError there: spec.py:195-196,
+     layout.py:38-39, tp.py:944-945), else the launch error;
+   - M = 0 tokens is a no-op returning 0.
+
+   Numbers (the reference's, tc.cu:1-18, tc_hip.cu:8-15): activations are int8 per 128-column group (XS = amax/127,
+   q = round-to-nearest-even(x * 127 / amax), XA = sum q); a group's value v = sum t q over its 128 columns is an
+   exact int32 (t in {-1, 0, +1}); the fp32 output adds fmaf((float)v, XS * d, acc) group after group. A K split of a
+   product (fixed per shape, never per M) adds its parts in a fixed order, so a token's result does not depend on
+   how many tokens share the pass and is the same on every run. */
+#ifndef KT_H
+#define KT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#define KT_VERSION 1
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+int kt_version(void);
+/* hipSetDevice(device). gpudrv.py:83-85 (cuCtxSetCurrent) */
+int kt_init(int device);
+const char* kt_error_string(int rc);
+
+/* ---------------------------------------------------------------- ternary weights
+   Device layout "kt2": 2-bit digits + fp16 scale per 128 columns, the same 2.125 bits per weight as the pack.
+   kt_tern_weight_bytes: the size of one matrix (rows padded to a multiple of 64), 0 if C % 128 != 0.
+   kt_tern_pack: the reference pack of one tensor, unchanged (bcodes [C/4][R]: byte = d0 + 3 d1 + 9 d2 + 27 d3 of
+   4 columns, convert.py:49-52, 144-159; dpm [C/128][R] fp16 bits, convert.py:155) -> W (16-byte aligned).
+   Replaces layout.repack (layout.py:32-48) and spec.repack / k_tc_pack (spec.py:327-383, tc_hip.cu:31-40). */
+size_t kt_tern_weight_bytes(int R, int C);
+int kt_tern_pack(const uint8_t* bcodes, const uint16_t* dpm, int R, int C, void* W, void* stream);
+
+/* ---------------------------------------------------------------- activations
+   X fp32 [M][ldx] -> XQ int8 [M][ldq] (natural column order, ldq % 16 == 0), XS f32 / XA i32 [M][C/128].
+   per_row = 0: the reference's per-128-group scale (k_tc_q8, tc_hip.cu:43-74; tcq128 tc.cu:160-194; k_q8x_T
+   chunk.cu:781-802). per_row = 1: one amax per token row (the same formula; XS repeated per group). */
+int kt_quant_q8(const float* X, int ldx, int M, int C, int per_row, int8_t* XQ, int ldq, float* XS, int32_t* XA,
+                void* stream);
+
+/* ---------------------------------------------------------------- decode products (1 .. 16 tokens a pass)
+   Y[n][ldy] = W x_n for tokens n < M. dbg (nullable): the exact group values v, int32 [M][R][C/128].
+   ws: workspace of kt_tern_gemv_workspace(R, C, M) bytes (NULL when that is 0). Its first 64 KB hold the arrival
+   counters of the K split's last-block reduction: zero-fill them once when the workspace is allocated; every
+   launch leaves them zero, so one workspace serves every shape and M (sized for the largest). Launches that share
+   a workspace must not run concurrently (same stream, or ordered).
+   Replaces k_tc_mv{2,4,8} + k_tc_sum (tc_hip.cu:180-199, 236-240, 271-279; spec.py:619-657). */
+int kt_tern_gemv_splits(int R, int C);
+size_t kt_tern_gemv_workspace(int R, int C, int M);
+int kt_tern_gemv(const void* W, int R, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M,
+                 float* Y, int ldy, int32_t* dbg, void* ws, void* stream);
+
+/* up to three matrices sharing one input (q/k/v, gate/up) in one launch; Y_i is [M][R_i]; R_i <= 0 ends the list.
+   Replaces k_tc_mv3_{2,4,8} (tc_hip.cu:201-234; spec.py:659-673). */
+size_t kt_tern_gemv3_workspace(int R0, int R1, int R2, int C, int M);
+int kt_tern_gemv3(const void* W0, int R0, float* Y0, const void* W1, int R1, float* Y1, const void* W2, int R2,
+                  float* Y2, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M, void* ws,
+                  void* stream);
+
+/* y[n R + r] = sum over parts p < sp of P[(n sp + p) R + r], in part order. k_tc_sum (tc_hip.cu:271-279). */
+int kt_tern_sum(const float* P, float* y, int R, int M, int sp, void* stream);
+
+/* ---------------------------------------------------------------- prefill product (any M, matrix cores)
+   Y and/or Y16 [M][ldy] (fp32 / fp16 bits); dbg as kt_tern_gemv. XA is accepted for the reference's argument list
+   and not read (the matrix cores take signed trits). Replaces k_tc_mm2 / k_tc_mm{4,8,16} (tc_hip.cu:243-269,
+   chunk.py:273-296) and k_mm_g5q (chunk.cu:858-918, chunk.py:245-271). */
+int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M,
+                 float* Y, uint16_t* Y16, int ldy, int32_t* dbg, void* stream);
+
+/* ---------------------------------------------------------------- q8_0
+   Device layout "kq8": int8 codes + fp16 scale per 32 columns (1.0625 B/w, as GGUF Q8_0).
+   kt_q8_pack: GGUF Q8_0 rows (34-byte blocks: fp16 d, 32 int8; dsv41_cpu.c:77-78) -> W. Replaces dg_mat_q8
+   (dsv41_gpu.cu:66-88) and the Q8_0 repack of lightning.py.
+   kt_q8_quant: X fp32 -> Q int8 [M][ldq] + D f32 [M][ldd] per 32 columns, llama.cpp's CPU rounding
+   (d = fp16(amax/127), q = rne(x * 127 / amax); quant_q8 dsv41_cpu.c:251-280, moe_cpu.c:84-112); act = 1 applies
+   relu^2 first (lt_quant2, lightning.cu:470).
+   kt_q8_gemv: Y = W x for M tokens: per block v = sum w q exact, acc = fmaf((float)v, dw * dx, acc) (lt_mv_q8
+   lightning.cu:258-284, k_q8 dsv41_gpu.cu:131-296); dbg int32 [M][R][C/32]; ws as kt_tern_gemv. */
+size_t kt_q8_weight_bytes(int R, int C);
+int kt_q8_pack(const uint8_t* rows, int R, int C, void* W, void* stream);
+int kt_q8_quant(const float* X, int ldx, int M, int C, int act, int8_t* Q, int ldq, float* D, int ldd, void* stream);
+int kt_q8_gemv_splits(int R, int C);
+size_t kt_q8_gemv_workspace(int R, int C, int M);
+int kt_q8_gemv(const void* W, int R, int C, const int8_t* Q, int ldq, const float* D, int ldd, int M, float* Y,
+               int ldy, int32_t* dbg, void* ws, void* stream);
+
+/* ---------------------------------------------------------------- MoE
+   kt_moe_topk: logits [M][E] -> ids / gw [M][k]: softmax, the k largest (ties to the lower index), weights
+   normalized over the chosen k (the reference's Lightning router lt_topk / lt_router_topk,
+   lightning.cu:373-468, is sigmoid + bias: same interface, other scoring). E <= 1024, k <= 16.
+   kt_moe_sort: lt_moe_lists (lightning.cu:1318-1349): cnt / off [E], xrow / where [M k], plus act [E] (experts with
+   cnt > 0, ascending) and nact [1]; entries of an expert in ascending t k + j. One block; E <= 1024.
+   kt_q8_grouped: per active expert e, Y[p] = W_e x[xrow[p]] for its entries p (xrow NULL: x[p]); Wexp = device
+   table of E kq8 buffers (the pointer tables of lt_mv_q2 / lt_mm_*, lightning.cu:154-195, 958-961); M = tokens
+   (bounds an expert's list); dbg int32 [entries][R][C/32].
+   kt_moe_combine: x[t] += sum_j fmaf(gw[t k + j], yd[where[t k + j]], .) (+ ysh[t]) (lt_moe_combine,
+   lightning.cu:1352-1361). */
+int kt_moe_topk(const float* logits, int M, int E, int k, int* ids, float* gw, void* stream);
+int kt_moe_sort(const int* ids, int M, int k, int E, int* cnt, int* off, int* xrow, int* where, int* act, int* nact,
+                void* stream);
+int kt_q8_grouped(const void* const* Wexp, int R, int C, int E, const int* cnt, const int* off, const int* act,
+                  const int* nact, const int* xrow, int nentries, int M, const int8_t* Q, int ldq, const float* D,
+                  int ldd, float* Y, int ldy, int32_t* dbg, void* stream);
+int kt_moe_combine(const float* yd, const float* ysh, const int* where, const float* gw, int M, int k, int cols,
+                   float* x, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

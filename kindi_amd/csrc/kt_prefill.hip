@@ -1,0 +1,149 @@
+/* kt_prefill.hip - the prefill product on the matrix cores (k_tc_mm2 tc_hip.cu:243-269, k_mm_g5q chunk.cu:858-918).
+
+   Y[t][r] = sum_g fmaf((float)v(t, r, g), XS[t][g] * d[r][g], .) over the 128-column groups g in order, where
+   v(t, r, g) = sum of t(r, c) q(t, c) over the group is an exact int32 from V_MFMA_I32_32X32X32_I8.
+
+   Block: 256 threads (4 waves) own 128 tokens x 128 weight rows; wave (wt, wr) owns tokens 64 wt .., rows 64 wr ..
+   as 2 x 2 MFMA tiles of 32 x 32. Per group: the block loads the 128 rows' packed trits (4 KB: one 16-byte load
+   per thread, straight from the kt2 layout), unpacks them to signed int8 once (shift, mask, v_perm byte lookup)
+   into LDS, stages the 128 tokens' int8 activations in LDS, and each wave runs 4 k-steps of 2 x 2 MFMAs. The
+   MFMA A operand is the activations (rows = tokens), B the weights (columns = weight rows), so a lane's 16
+   accumulators share one weight row: its group scale is one register. After the group the int32 accumulators are
+   scaled into fp32 accumulators in the reference expression and cleared.
+
+   MFMA 32x32x32 i8 register layouts on gfx950 (measured): A lane l holds row l % 32, k = 16 (l / 32) .. +15;
+   B lane l holds column l % 32, the same k; D lane l register i holds column l % 32, row (i % 4) + 8 (i / 4) +
+   4 (l / 32). */
+#include "kt_common.h"
+
+typedef int kt_v4i __attribute__((ext_vector_type(4)));
+typedef int kt_v16i __attribute__((ext_vector_type(16)));
+
+#define PF_BT 128                     /* tokens per block */
+#define PF_BR 128                     /* weight rows per block */
+#define PF_LD 144                     /* LDS row stride in bytes (128 + 16: rows land on different banks) */
+
+/* 4 digits (0/1/2, one per byte) -> 4 signed trits (-1/0/+1): byte lookup in 0x000100FF */
+__device__ __forceinline__ uint32_t kt_trits(uint32_t dig){ return __builtin_amdgcn_perm(0x000100FFu, 0x000100FFu, dig); }
+
+extern "C" __global__ void __launch_bounds__(256) k_tern_gemm(const uint32_t* __restrict__ codes,
+    const uint16_t* __restrict__ scales, int R, int NG, int ntiles, const int8_t* __restrict__ XQ, int ldq,
+    const float* __restrict__ XS, int M, float* __restrict__ Y, uint16_t* __restrict__ Y16, int ldy,
+    int32_t* __restrict__ dbg){
+  __shared__ __attribute__((aligned(16))) uint8_t Xl[PF_BT * PF_LD];
+  __shared__ __attribute__((aligned(16))) uint8_t Wl[PF_BR * PF_LD];
+  __shared__ float xs_l[PF_BT];
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wt = wv >> 1, wr = wv & 1;
+  const int r0 = blockIdx.x * PF_BR, n0 = blockIdx.y * PF_BT;
+
+  /* this thread's weight chunk: tile (r0/64 + tid/128), half (tid/64)&1, lane tid&63 */
+  const int ltile = tid >> 7, lh = (tid >> 6) & 1, ll = tid & 63;
+  const int gtile = (r0 >> 6) + ltile;
+  const bool wvalid = gtile < ntiles;
+  const uint4* __restrict__ wsrc = (const uint4*)codes + (long long)gtile * NG * 128 + lh * 64 + ll;
+  uint8_t* wdst = Wl + (ltile * 64 + ll) * PF_LD + lh * 64;
+
+  /* this thread's activation chunk: token tid/2, 64 bytes at (tid&1)*64 */
+  const int xt = tid >> 1, xh = tid & 1;
+  const bool xvalid = n0 + xt < M;
+  const int8_t* __restrict__ xsrc = XQ + (long long)(n0 + xt) * ldq + xh * 64;
+  uint8_t* xdst = Xl + xt * PF_LD + xh * 64;
+
+  /* scales of this lane's two weight rows (columns of the 2 B tiles) */
+  const int cr0 = r0 + wr * 64 + (lane & 31), cr1 = cr0 + 32;
+  const uint16_t* __restrict__ s0p = scales + (long long)(cr0 >> 6) * NG * 64 + (cr0 & 63);
+  const uint16_t* __restrict__ s1p = scales + (long long)(cr1 >> 6) * NG * 64 + (cr1 & 63);
+  const bool c0v = (cr0 >> 6) < ntiles, c1v = (cr1 >> 6) < ntiles;
+
+  float acc[2][2][16];
+#pragma unroll
+  for(int i = 0; i < 2; ++i)
+#pragma unroll
+    for(int j = 0; j < 2; ++j)
+#pragma unroll
+      for(int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  for(int g = 0; g < NG; ++g){
+    /* global -> registers */
+    uint4 wc = make_uint4(0x55555555u, 0x55555555u, 0x55555555u, 0x55555555u);
+    if(wvalid) wc = kt_ldnt(wsrc + (long long)g * 128);
+    uint4 xv[4];
+#pragma unroll
+    for(int k = 0; k < 4; ++k) xv[k] = xvalid ? ((const uint4*)(xsrc + g * 128))[k] : make_uint4(0u, 0u, 0u, 0u);
+    const float d0 = c0v ? kt_h2f(s0p[(long long)g * 64]) : 0.0f;
+    const float d1 = c1v ? kt_h2f(s1p[(long long)g * 64]) : 0.0f;
+
+    __syncthreads();                                          /* the previous group's operands are consumed */
+    /* unpack: word j of the chunk = columns 16j .. +15 of the half; slot s = columns 16j + 4s .. +3 */
+    const uint32_t ww[4] = {wc.x, wc.y, wc.z, wc.w};
+#pragma unroll
+    for(int j = 0; j < 4; ++j){
+      uint4 o;
+      o.x = kt_trits(ww[j] & 0x03030303u);
+      o.y = kt_trits((ww[j] >> 2) & 0x03030303u);
+      o.z = kt_trits((ww[j] >> 4) & 0x03030303u);
+      o.w = kt_trits((ww[j] >> 6) & 0x03030303u);
+      *(uint4*)(wdst + 16 * j) = o;
+    }
+#pragma unroll
+    for(int k = 0; k < 4; ++k) *(uint4*)(xdst + 16 * k) = xv[k];
+    if(tid < PF_BT) xs_l[tid] = n0 + tid < M ? XS[(long long)(n0 + tid) * NG + g] : 0.0f;
+    __syncthreads();
+
+    kt_v16i c[2][2];
+#pragma unroll
+    for(int i = 0; i < 2; ++i)
+#pragma unroll
+      for(int j = 0; j < 2; ++j)
+#pragma unroll
+        for(int e = 0; e < 16; ++e) c[i][j][e] = 0;
+#pragma unroll
+    for(int ks = 0; ks < 4; ++ks){
+      const int koff = ks * 32 + (lane >> 5) * 16;
+      kt_v4i A[2], B[2];
+#pragma unroll
+      for(int i = 0; i < 2; ++i) A[i] = *(const kt_v4i*)(Xl + (wt * 64 + i * 32 + (lane & 31)) * PF_LD + koff);
+#pragma unroll
+      for(int j = 0; j < 2; ++j) B[j] = *(const kt_v4i*)(Wl + (wr * 64 + j * 32 + (lane & 31)) * PF_LD + koff);
+#pragma unroll
+      for(int i = 0; i < 2; ++i)
+#pragma unroll
+        for(int j = 0; j < 2; ++j) c[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[i], B[j], c[i][j], 0, 0, 0);
+    }
+    /* group epilogue: acc += (float)v * (XS[t][g] * d[r][g]) */
+#pragma unroll
+    for(int i = 0; i < 2; ++i)
+#pragma unroll
+      for(int e = 0; e < 16; ++e){
+        const int tl = wt * 64 + i * 32 + (e & 3) + 8 * (e >> 2) + 4 * (lane >> 5);
+        const float xs = xs_l[tl];
+        acc[i][0][e] = fmaf((float)c[i][0][e], xs * d0, acc[i][0][e]);
+        acc[i][1][e] = fmaf((float)c[i][1][e], xs * d1, acc[i][1][e]);
+        if(dbg){
+          const int t = n0 + tl;
+          if(t < M){
+            if(cr0 < R) dbg[((long long)t * R + cr0) * NG + g] = c[i][0][e];
+            if(cr1 < R) dbg[((long long)t * R + cr1) * NG + g] = c[i][1][e];
+          }
+        }
+      }
+  }
+  /* store: lanes of one register write 32 consecutive rows of one token */
+#pragma unroll
+  for(int i = 0; i < 2; ++i)
+#pragma unroll
+    for(int e = 0; e < 16; ++e){
+      const int t = n0 + wt * 64 + i * 32 + (e & 3) + 8 * (e >> 2) + 4 * (lane >> 5);
+      if(t < M){
+        if(cr0 < R){
+          if(Y) Y[(long long)t * ldy + cr0] = acc[i][0][e];
+          if(Y16) Y16[(long long)t * ldy + cr0] = __half_as_ushort(__float2half_rn(acc[i][0][e]));
+        }
+        if(cr1 < R){
+          if(Y) Y[(long long)t * ldy + cr1] = acc[i][1][e];
+          if(Y16) Y16[(long long)t * ldy + cr1] = __half_as_ushort(__float2half_rn(acc[i][1][e]));
+        }
+      }
+    }
+}

@@ -1,0 +1,190 @@
+"""Ternary linear layers on MI355X: the host side of Kindi's linear-call surface over libkt_gfx950.so.
+
+Kindi's callers and what each maps to here:
+  Engine.gemv(names, x, outs, parts_ok)       engine.py:254-274      Linear.gemv          (<= 3 tensors, one input)
+  build_plan gemm / gemm3 (k_tc_q8 + k_tc_mv) spec.py:619-672        quantize + Linear.gemv_q / gemv3_q
+  chunk gemm_tc (k_tc_q8 + k_tc_mm2)          chunk.py:273-296       quantize + Linear.gemm
+  layout.repack / spec.repack                 layout.py:32-48, spec.py:327-383   TernaryMatrix (kt_tern_pack)
+
+Torch provides device memory and the current stream only; every product runs in the HIP library. Tensors are
+CUDA (HIP) tensors on one device; activations fp32 [M, C] row-major.
+"""
+import ctypes
+from collections import namedtuple
+
+import numpy as np
+import torch
+
+from . import gpudrv
+
+VP = ctypes.c_void_p
+
+
+def ptr(t):
+    return VP(t.data_ptr()) if t is not None else None
+
+
+def stream():
+    return VP(torch.cuda.current_stream().cuda_stream)
+
+
+def _dev_u8(a, device):
+    if isinstance(a, torch.Tensor):
+        return a.to(device=device, dtype=torch.uint8).contiguous()
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint8)).to(device)
+
+
+def _dev_u16(a, device):
+    """uint16 bits (numpy uint16 / torch int16 or uint16) -> a device int16 tensor with the same bits"""
+    if isinstance(a, torch.Tensor):
+        return a.to(device=device).view(torch.int16).contiguous()
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint16).view(np.int16)).to(device)
+
+
+class TernaryMatrix(object):
+    """One ternary tensor resident in HBM in the kt2 layout (2.125 bits per weight).
+
+    bcodes: the reference pack's codes [C/4, R] (byte = d0 + 3 d1 + 9 d2 + 27 d3, convert.py:49-52);
+    dpm: its fp16 scales [C/128, R] as uint16 bits. Numpy arrays are uploaded; device tensors are used as they are."""
+
+    def __init__(self, bcodes, dpm, R, C, device="cuda"):
+        lib = gpudrv.load()
+        self.R, self.C = int(R), int(C)
+        nbytes = lib.kt_tern_weight_bytes(self.R, self.C)
+        if nbytes == 0:
+            raise ValueError("ternary tensor %d x %d does not fit the kt2 layout (C %% 128 != 0)" % (R, C))
+        bc = _dev_u8(bcodes, device).reshape(-1)
+        dp = _dev_u16(dpm, device).reshape(-1)
+        if bc.numel() != self.R * self.C // 4 or dp.numel() != self.R * (self.C // 128):
+            raise ValueError("pack arrays do not match %d x %d" % (R, C))
+        self.W = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        gpudrv.check(lib.kt_tern_pack(ptr(bc), ptr(dp), self.R, self.C, ptr(self.W), stream()), "kt_tern_pack")
+
+    @property
+    def nbytes(self):
+        return self.W.numel()
+
+
+Act = namedtuple("Act", "XQ XS XA M C per_row")
+
+
+def quantize(X, per_row=False, out=None):
+    """fp32 [M, C] -> int8 rows per 128-column group (k_tc_q8, tc_hip.cu:43-74) or per row. Returns Act."""
+    if X.dim() == 1:
+        X = X.reshape(1, -1)
+    M, C = X.shape
+    if X.dtype != torch.float32 or X.stride(1) != 1:
+        raise ValueError("quantize takes fp32 rows with unit column stride")
+    if out is None:
+        out = Act(torch.empty((M, C), dtype=torch.int8, device=X.device),
+                  torch.empty((M, C // 128), dtype=torch.float32, device=X.device),
+                  torch.empty((M, C // 128), dtype=torch.int32, device=X.device), M, C, per_row)
+    lib = gpudrv.load()
+    gpudrv.check(lib.kt_quant_q8(ptr(X), X.stride(0), M, C, 1 if per_row else 0, ptr(out.XQ), out.XQ.stride(0),
+                                 ptr(out.XS), ptr(out.XA), stream()), "kt_quant_q8")
+    return Act(out.XQ, out.XS, out.XA, M, C, per_row)
+
+
+class Workspace(object):
+    """zero-filled scratch for the K-split reductions, grown on demand (the kernels leave it zeroed)"""
+
+    def __init__(self, device="cuda"):
+        self.device = device
+        self.buf = None
+
+    def get(self, nbytes):
+        if nbytes == 0:
+            return None
+        if self.buf is None or self.buf.numel() < nbytes:
+            self.buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
+        return self.buf
+
+
+class Linear(object):
+    """The ternary tensors of a model and the products over them (Kindi's linear-call surface).
+
+    decode_max: up to this many tokens a product runs on the wave64 bandwidth kernel (kt_tern_gemv), above it on
+    the matrix cores (kt_tern_gemm). Each kernel's split is fixed per shape, so within one kernel a token's result
+    does not depend on how many tokens share the pass (tc_hip.cu:14-15)."""
+
+    def __init__(self, mats=None, device="cuda", decode_max=16, per_row=False):
+        self.w = dict(mats or {})
+        self.device = device
+        self.decode_max = decode_max
+        self.per_row = per_row
+        self.ws = Workspace(device)
+
+    def add(self, name, mat):
+        self.w[name] = mat
+
+    # ------------------------------------------------------------------ decode
+    def gemv_q(self, names, act, outs, dbg=None):
+        """up to three tensors with the same (quantized) input in one launch: outs[i] fp32 [M, R_i]
+        (k_tc_mv3_* / k_tc_mv*, spec.py:646-673)"""
+        lib = gpudrv.load()
+        ms = [self.w[n] for n in names]
+        if not 1 <= len(ms) <= 3:
+            raise ValueError("1 to 3 tensors per launch")
+        C = ms[0].C
+        if any(m.C != C for m in ms) or act.C != C:
+            raise ValueError("tensors of one launch share the input width")
+        for m, o in zip(ms, outs):
+            if o.dtype != torch.float32 or o.shape[-1] != m.R or o.numel() < act.M * m.R or not o.is_contiguous():
+                raise ValueError("output for %d rows x %d tokens" % (m.R, act.M))
+        if len(ms) == 1:
+            ws = self.ws.get(lib.kt_tern_gemv_workspace(ms[0].R, C, act.M))
+            rc = lib.kt_tern_gemv(ptr(ms[0].W), ms[0].R, C, ptr(act.XQ), act.XQ.stride(0), ptr(act.XS), ptr(act.XA),
+                                  act.M, ptr(outs[0]), ms[0].R, ptr(dbg), ptr(ws), stream())
+            return gpudrv.check(rc, "kt_tern_gemv") or 1
+        if dbg is not None:
+            raise ValueError("dbg takes a single tensor")
+        Rs = [m.R for m in ms] + [0] * (3 - len(ms))
+        Ws = [ptr(m.W) for m in ms] + [None] * (3 - len(ms))
+        Ys = [ptr(o) for o in outs] + [None] * (3 - len(ms))
+        ws = self.ws.get(lib.kt_tern_gemv3_workspace(Rs[0], Rs[1], Rs[2], C, act.M))
+        rc = lib.kt_tern_gemv3(Ws[0], Rs[0], Ys[0], Ws[1], Rs[1], Ys[1], Ws[2], Rs[2], Ys[2], C, ptr(act.XQ),
+                               act.XQ.stride(0), ptr(act.XS), ptr(act.XA), act.M, ptr(ws), stream())
+        return gpudrv.check(rc, "kt_tern_gemv3") or 1
+
+    def gemv(self, names, x, outs, parts_ok=False):
+        """Engine.gemv (engine.py:254-274): up to three ternary tensors with the same fp32 input x ([C] or [M, C]).
+        The input is quantized once (the int8 path); the K-split parts are added inside the launch, so the part
+        count returned is always 1 (parts_ok is accepted for the reference's signature)."""
+        act = quantize(x, self.per_row)
+        outs = [o.reshape(act.M, -1) for o in outs]
+        return self.gemv_q(names, act, outs)
+
+    # ------------------------------------------------------------------ prefill
+    def gemm(self, name, act, Y=None, Y16=None, dbg=None):
+        """chunk.gemm_tc (chunk.py:273-296): Y fp32 and/or Y16 fp16 [M, R] on the matrix cores"""
+        lib = gpudrv.load()
+        m = self.w[name]
+        if act.C != m.C:
+            raise ValueError("input width %d != %d" % (act.C, m.C))
+        if Y is None and Y16 is None:
+            Y = torch.empty((act.M, m.R), dtype=torch.float32, device=act.XQ.device)
+        ldy = (Y if Y is not None else Y16).stride(0)
+        y16 = Y16.view(torch.int16) if Y16 is not None else None
+        rc = lib.kt_tern_gemm(ptr(m.W), m.R, m.C, ptr(act.XQ), act.XQ.stride(0), ptr(act.XS), ptr(act.XA), act.M,
+                              ptr(Y), ptr(y16), ldy, ptr(dbg), stream())
+        gpudrv.check(rc, "kt_tern_gemm")
+        return Y if Y is not None else Y16
+
+    # ------------------------------------------------------------------ either
+    def forward(self, name, X, per_row=None):
+        """Y = W X for fp32 X [M, C]: decode kernel up to decode_max tokens, matrix cores above"""
+        act = quantize(X, self.per_row if per_row is None else per_row)
+        m = self.w[name]
+        if act.M <= self.decode_max:
+            Y = torch.empty((act.M, m.R), dtype=torch.float32, device=X.device)
+            self.gemv_q([name], act, [Y])
+            return Y
+        return self.gemm(name, act)
+
+
+def tern_sum(P, R, M, sp, y=None):
+    """k_tc_sum (tc_hip.cu:271-279): parts [M, sp, R] -> [M, R] in part order"""
+    if y is None:
+        y = torch.empty((M, R), dtype=torch.float32, device=P.device)
+    gpudrv.check(gpudrv.load().kt_tern_sum(ptr(P), ptr(y), R, M, sp, stream()), "kt_tern_sum")
+    return y

@@ -1,0 +1,76 @@
+"""The C ABI without a GPU: the library loads, exports exactly what include/kt.h declares, and its host-side
+validation rejects shapes the kernels do not take (those paths return before any launch)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HDR = os.path.join(ROOT, "include", "kt.h")
+INVALID = 1                                              # hipErrorInvalidValue
+
+
+def declared():
+    src = open(HDR).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(kt_\w+)\s*\(", src, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from kindi_amd import gpudrv
+    if not os.path.exists(gpudrv.LIB):
+        pytest.fail("libkt_gfx950.so not built: run __graft_entry__.build()")
+    return gpudrv.load()
+
+
+def test_exports_every_declared_symbol(lib):
+    names = declared()
+    assert len(names) >= 20
+    for n in names:
+        assert hasattr(lib, n), n
+    from kindi_amd import gpudrv
+    assert sorted(n for n, _, _ in gpudrv.SIGNATURES) == names      # the ctypes table covers the header exactly
+
+
+def test_version_and_sizes(lib):
+    assert lib.kt_version() == 1
+    # kt2: 2 bits + fp16 per 128 (2.125 b/w), rows padded to 64
+    assert lib.kt_tern_weight_bytes(6144, 2048) == 6144 * 2048 // 4 + 6144 * 16 * 2
+    assert lib.kt_tern_weight_bytes(100, 256) == 128 * 256 // 4 + 128 * 2 * 2
+    assert lib.kt_tern_weight_bytes(64, 100) == 0
+    # kq8: 34 bytes per 32
+    assert lib.kt_q8_weight_bytes(1856, 2688) == 1856 * 2688 // 32 * 34
+    assert lib.kt_q8_weight_bytes(64, 48) == 0
+
+
+def test_split_plan_is_shape_only(lib):
+    for R, C in ((6144, 2048), (1024, 5120), (5120, 17408), (17408, 5120)):
+        sp = lib.kt_tern_gemv_splits(R, C)
+        assert sp >= 1 and C // 128 // sp >= 4 * 2 or sp == 1
+        for M in (1, 4, 16):
+            ws = lib.kt_tern_gemv_workspace(R, C, M)
+            assert (ws == 0) == (sp == 1)
+
+
+def test_validation_rejects_bad_shapes(lib):
+    fake = ctypes.c_void_p(0x1000)
+    # C not a multiple of 128
+    assert lib.kt_tern_pack(fake, fake, 64, 100, fake, None) == INVALID
+    assert lib.kt_quant_q8(fake, 100, 1, 100, 0, fake, 112, fake, fake, None) == INVALID
+    # ldq not a multiple of 16
+    assert lib.kt_tern_gemv(fake, 64, 256, fake, 260, fake, fake, 1, fake, 64, None, None, None) == INVALID
+    # null output
+    assert lib.kt_tern_gemm(fake, 64, 256, fake, 256, fake, fake, 4, None, None, 64, None, None) == INVALID
+    # q8: C % 32
+    assert lib.kt_q8_gemv(fake, 64, 48, fake, 48, fake, 1, 1, fake, 64, None, None, None) == INVALID
+    # moe: k > 16, E > 1024
+    assert lib.kt_moe_topk(fake, 1, 128, 17, fake, fake, None) == INVALID
+    assert lib.kt_moe_sort(fake, 1, 6, 2048, fake, fake, fake, fake, fake, fake, None) == INVALID
+    # M = 0: a no-op
+    assert lib.kt_tern_gemv(fake, 64, 256, fake, 256, fake, fake, 0, fake, 64, None, None, None) == 0
+    # a split product without its workspace
+    R, C = 1024, 5120
+    assert lib.kt_tern_gemv_splits(R, C) > 1
+    assert lib.kt_tern_gemv(fake, R, C, fake, C, fake, fake, 1, fake, R, None, None, None) == INVALID

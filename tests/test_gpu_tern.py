@@ -1,0 +1,192 @@
+"""GPU parity of the ternary path (kt_tern_pack, kt_quant_q8, kt_tern_gemv / gemv3, kt_tern_gemm) against the CPU
+oracle. Bars: quantized activations and the int32 group values bit-exact; fp32 outputs bit-exact against the oracle
+evaluated in the kernel's documented summation tree, and within 1e-3 relative of the oracle's sequential
+(reference-order) value."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as orc
+from kt_cases import say, tern_case, dev, host, max_rel, rng
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3                                   # north_star: scaled outputs within 1e-3 relative
+
+
+@pytest.fixture(scope="module")
+def kt():
+    assert torch.cuda.is_available(), "GPU tests need the MI355X"
+    from kindi_amd import gpudrv, linear
+    lib = gpudrv.load()
+    return lib, linear
+
+
+def upload(linear, R, C, seed):
+    dig, bc, dpm = tern_case(R, C, seed)
+    return linear.TernaryMatrix(bc, dpm, R, C), dig, bc, dpm
+
+
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("M,C", [(1, 128), (3, 2048), (17, 5120), (64, 17408)])
+def test_quantizer_bit_exact(kt, M, C, per_row):
+    lib, linear = kt
+    say("quant", M, C, per_row)
+    X = rng(M * 7 + C).normal(0, 1, (M, C)).astype(np.float32)
+    X[0, :128] = 0.0                                        # a zero group
+    if C > 256:
+        X[-1, 256:384] = np.float32(127.0)                  # a group of exact maxima
+        X[-1, 300] = np.float32(-63.5)                      # a tie: 63.5 -> 64 (even)
+    act = linear.quantize(dev(X), per_row=per_row)
+    Q, XS, XA = orc.quant_q8(X, per_row)
+    assert np.array_equal(host(act.XQ), Q)
+    assert np.array_equal(host(act.XS), XS)
+    assert np.array_equal(host(act.XA), XA)
+
+
+SHAPES = [(64, 128), (100, 256), (6144, 2048), (1024, 5120), (2048, 6144), (5120, 17408)]
+
+
+@pytest.mark.parametrize("R,C", SHAPES)
+def test_gemv_m1(kt, R, C):
+    lib, linear = kt
+    say("gemv M=1", R, C)
+    W, dig, bc, dpm = upload(linear, R, C, R + C)
+    X = rng(R * 3 + C).normal(0, 1, (1, C)).astype(np.float32)
+    L = linear.Linear({"w": W})
+    act = linear.quantize(dev(X))
+    Y = torch.empty((1, R), dtype=torch.float32, device="cuda")
+    dbg = torch.empty((1, R, C // 128), dtype=torch.int32, device="cuda")
+    L.gemv_q(["w"], act, [Y], dbg=dbg)
+    Q, XS, XA = orc.quant_q8(X)
+    acc = orc.tern_acc(bc, R, C, Q)
+    assert np.array_equal(host(dbg), acc), "int32 group values"
+    dq = dpm.view(np.float16).astype(np.float32)
+    tree = orc.out_tree(acc, XS, dq, lib.kt_tern_gemv_splits(R, C), 4, 0)
+    y = host(Y)
+    assert np.array_equal(y, tree), "fp32 in the kernel's summation tree"
+    seq = orc.tern_out(acc, XS, dpm, R, C)
+    assert max_rel(y, seq) < TOL
+    # without dbg the output is the same
+    Y2 = torch.empty_like(Y)
+    L.gemv_q(["w"], act, [Y2])
+    assert np.array_equal(host(Y2), y)
+
+
+@pytest.mark.parametrize("R,C", [(640, 1024), (2048, 6144)])
+def test_gemv_token_invariance(kt, R, C):
+    """a token's output does not depend on how many tokens share the pass (tc_hip.cu:14-15), for M = 1 .. 20"""
+    lib, linear = kt
+    say("gemv T-invariance", R, C)
+    W, dig, bc, dpm = upload(linear, R, C, 5 + R)
+    L = linear.Linear({"w": W})
+    X = rng(9).normal(0, 1, (20, C)).astype(np.float32)
+    Xd = dev(X)
+    Q, XS, XA = orc.quant_q8(X)
+    acc = orc.tern_acc(bc, R, C, Q)
+    dq = dpm.view(np.float16).astype(np.float32)
+    tree = orc.out_tree(acc, XS, dq, lib.kt_tern_gemv_splits(R, C), 4, 0)
+    for M in (1, 2, 3, 4, 5, 8, 9, 13, 16, 17, 20):
+        act = linear.quantize(Xd[:M])
+        Y = torch.empty((M, R), dtype=torch.float32, device="cuda")
+        dbg = torch.empty((M, R, C // 128), dtype=torch.int32, device="cuda")
+        L.gemv_q(["w"], act, [Y], dbg=dbg)
+        assert np.array_equal(host(dbg), acc[:M]), M
+        assert np.array_equal(host(Y), tree[:M]), M
+
+
+def test_gemv3_qkv(kt):
+    """q / k / v of the 2B layer in one launch (k_tc_mv3, spec.py:659-673), M = 4"""
+    lib, linear = kt
+    say("gemv3 qkv")
+    C, M = 2048, 4
+    mats = {n: upload(linear, R, C, s) for n, R, s in (("q", 2048, 1), ("k", 512, 2), ("v", 512, 3))}
+    L = linear.Linear({n: m[0] for n, m in mats.items()})
+    X = rng(4).normal(0, 1, (M, C)).astype(np.float32)
+    outs = [torch.empty((M, mats[n][0].R), dtype=torch.float32, device="cuda") for n in "qkv"]
+    assert L.gemv(["q", "k", "v"], dev(X), outs) == 1
+    for n, o in zip("qkv", outs):
+        W, dig, bc, dpm = mats[n]
+        ref, acc, _ = orc.tern_linear(bc, dpm, W.R, C, X)
+        assert max_rel(host(o), ref) < TOL, n
+        # a separate launch of the same tensor agrees to rounding
+        Y1 = torch.empty_like(o)
+        L.gemv_q([n], linear.quantize(dev(X)), [Y1])
+        assert max_rel(host(Y1), host(o)) < 1e-5
+
+
+@pytest.mark.parametrize("R,C,M", [(128, 256, 128), (100, 256, 5), (256, 512, 300), (384, 1024, 200)])
+def test_gemm_small(kt, R, C, M):
+    lib, linear = kt
+    say("gemm", R, C, M)
+    W, dig, bc, dpm = upload(linear, R, C, R * 11 + M)
+    L = linear.Linear({"w": W})
+    X = rng(M + 1).normal(0, 1, (M, C)).astype(np.float32)
+    act = linear.quantize(dev(X))
+    Y = torch.empty((M, R), dtype=torch.float32, device="cuda")
+    Y16 = torch.empty((M, R), dtype=torch.float16, device="cuda")
+    dbg = torch.empty((M, R, C // 128), dtype=torch.int32, device="cuda")
+    L.gemm("w", act, Y=Y, Y16=Y16, dbg=dbg)
+    Q, XS, XA = orc.quant_q8(X)
+    acc = orc.tern_acc(bc, R, C, Q)
+    assert np.array_equal(host(dbg), acc), "int32 group values"
+    seq = orc.tern_out(acc, XS, dpm, R, C)
+    y = host(Y)
+    assert np.array_equal(y, seq), "fp32: groups in order, the reference expression"
+    assert np.array_equal(host(Y16), seq.astype(np.float16))
+
+
+@pytest.mark.parametrize("R,C,M", [(12288, 4096, 512), (4096, 12288, 512)])
+def test_gemm_config2_sampled(kt, R, C, M):
+    """config 2 shapes at M = 512: int32 group values and outputs of 96 sampled rows against the oracle, all rows
+    against the decode kernel's fp32 output for 16 tokens (the same int32 values, another summation tree)"""
+    lib, linear = kt
+    say("gemm config2", R, C, M)
+    import kindi_amd.synth as syn
+    bc_t, dpm_t = syn.tern_pack(R, C, 20, device="cuda")
+    W = linear.TernaryMatrix(bc_t, dpm_t, R, C)
+    L = linear.Linear({"w": W})
+    Xd = syn.activations(M, C, 22, device="cuda")
+    act = linear.quantize(Xd, per_row=True)
+    Y = L.gemm("w", act)
+    rows = np.sort(rng(1).choice(R, 96, replace=False))
+    bc = host(bc_t)[:, rows]
+    dpm = host(dpm_t).view(np.uint16)[:, rows]
+    X = host(Xd)
+    Q, XS, XA = orc.quant_q8(X, per_row=True)
+    assert np.array_equal(host(act.XQ), Q)
+    acc = orc.tern_acc(np.ascontiguousarray(bc), len(rows), C, Q)
+    seq = orc.tern_out(acc, XS, np.ascontiguousarray(dpm), len(rows), C)
+    y = host(Y)
+    assert np.array_equal(y[:, rows], seq)
+    Yd = torch.empty((16, R), dtype=torch.float32, device="cuda")
+    sub = linear.quantize(Xd[:16], per_row=True)
+    L.gemv_q(["w"], sub, [Yd])
+    assert max_rel(host(Yd), y[:16]) < 1e-5
+
+
+def test_gemv_full_size_linearity(kt):
+    """config 3 gate shape [17408 x 5120]: the exact group values are linear in the int8 input (v(q1 + q2) =
+    v(q1) + v(q2)), checked over every row; 64 sampled rows against the oracle"""
+    lib, linear = kt
+    say("gemv 27B gate linearity")
+    import kindi_amd.synth as syn
+    R, C = 17408, 5120
+    bc_t, dpm_t = syn.tern_pack(R, C, 104, device="cuda")
+    W = linear.TernaryMatrix(bc_t, dpm_t, R, C)
+    L = linear.Linear({"w": W})
+    r = rng(3)
+    q1 = r.integers(-63, 64, (2, C)).astype(np.int8)
+    q2 = r.integers(-63, 64, (2, C)).astype(np.int8)
+    outs = []
+    for q in (q1, q2, (q1.astype(np.int16) + q2).astype(np.int8)):
+        XS = np.ones((2, C // 128), np.float32)
+        XA = q.astype(np.int32).reshape(2, -1, 128).sum(2).astype(np.int32)
+        act = linear.Act(dev(q), dev(XS), dev(XA), 2, C, False)
+        dbg = torch.empty((2, R, C // 128), dtype=torch.int32, device="cuda")
+        Y = torch.empty((2, R), dtype=torch.float32, device="cuda")
+        L.gemv_q(["w"], act, [Y], dbg=dbg)
+        outs.append(host(dbg))
+    assert np.array_equal(outs[0] + outs[1], outs[2])
+    rows = np.sort(r.choice(R, 64, replace=False))
+    acc = orc.tern_acc(np.ascontiguousarray(host(bc_t)[:, rows]), 64, C, q1)
+    assert np.array_equal(outs[0][:, rows], acc)

@@ -1,0 +1,331 @@
+"""Pins of the CPU oracle (oracle/), each against something other than its own formula: the reference's compiled
+CPU code (oracle/_ref), brute-force integer arithmetic in NumPy, float64 closed forms, format round trips and
+hand-built known answers."""
+import numpy as np
+import pytest
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def rand_digits(R, C, seed):
+    u = rng(seed).random((R, C))
+    return ((u >= 0.3).astype(np.uint8) + (u >= 0.7).astype(np.uint8))
+
+
+def rand_scales(shape, seed):
+    return np.exp(rng(seed).normal(-3.0, 0.3, shape)).astype(np.float16).view(np.uint16)
+
+
+# ------------------------------------------------------------------------------------------- formats
+def test_pack_round_trip_selftest(orc):
+    """convert.selftest (convert.py:55-60): 4096 x 128 random digits, seed 7, survive bytes -> digits"""
+    tr = np.random.RandomState(7).randint(0, 3, size=(4096, 128)).astype(np.uint8)
+    b = orc.pack_from_digits(tr)
+    assert b.shape == (32, 4096) and b.max() <= 80
+    assert np.array_equal(orc.digits_from_pack(b, 4096, 128), tr)
+
+
+def test_pack_known_answers(orc):
+    # byte = d0 + 3 d1 + 9 d2 + 27 d3 (convert.py:49-52): digits (2,0,1,2) -> 2 + 0 + 9 + 54 = 65; all zero-weights
+    # (digit 1) -> 40 (the padding code layout.py:76 uses)
+    d = np.array([[2, 0, 1, 2, 1, 1, 1, 1]], dtype=np.uint8)
+    b = orc.pack_from_digits(d)
+    assert b[:, 0].tolist() == [65, 40]
+
+
+def test_ptq1_round_trip_and_known_answer(orc):
+    """PTQ1_0 decode (convert.py:33-46) inverts the TQ1 encoding ceil(v * 256 / 243)"""
+    dig = rand_digits(300, 128, 3)
+    sc = rand_scales(300, 4)
+    raw = orc.ptq1_from_digits(dig, sc)
+    assert np.array_equal(orc.trits_from_ptq1(raw), dig)
+    assert np.array_equal(raw[:, 26:28].copy().view(np.uint16).ravel(), sc)
+    # all digits 2: v = 242 -> byte ceil(242 * 256 / 243) = 255; all digits 0 -> 0
+    d2 = np.full((1, 128), 2, np.uint8)
+    r2 = orc.ptq1_from_digits(d2, [0])
+    assert (r2[0, :24] == 255).all()
+    assert np.array_equal(orc.trits_from_ptq1(r2), d2)
+
+
+def test_paircodes_decode(orc):
+    """cpu.paircodes (cpu.py:69-88): code k < 8 -> the k-th nonzero (w0, w1) pair, 8 -> both zero"""
+    R, C = 16, 256
+    dig = rand_digits(R, C, 5)
+    words = orc.paircodes(orc.pack_from_digits(dig), R, C)
+    pairs = [(-1, -1), (0, -1), (1, -1), (-1, 0), (1, 0), (-1, 1), (0, 1), (1, 1)]
+    t = dig.astype(int) - 1
+    for r in (0, 7, 9, 15):
+        for c in (0, 2, 100, 254):
+            g, p = c // 128, (c % 128) // 2
+            code = (int(words[r // 8, g, p]) >> (4 * (r % 8))) & 15
+            got = (0, 0) if code == 8 else pairs[code]
+            assert got == (t[r, c], t[r, c + 1])
+
+
+def test_fp16_conversions(orc):
+    vals = np.array([0.0, -0.0, 1.0, 65504.0, 65519.0, 6.1e-5, 5.96e-8, 1e-9, 3.14159, -2.5e-3, 2 ** -24 * 1.5],
+                    dtype=np.float32)
+    vals = np.concatenate([vals, rng(2).normal(0, 3, 2000).astype(np.float32),
+                           np.exp(rng(3).normal(-6, 3, 2000)).astype(np.float32)])
+    for v in vals:
+        assert orc.f2h(v) == int(np.float32(v).astype(np.float16).view(np.uint16))
+    for h in rng(1).integers(0, 0x7C00, 2000):
+        assert orc.h2f(h) == float(np.uint16(h).view(np.float16))
+
+
+# ------------------------------------------------------------------------------------------- activations
+def test_quant_special_cases(orc):
+    C = 256
+    X = np.zeros((3, C), np.float32)
+    X[1, :128] = np.linspace(-1.0, 1.0, 128, dtype=np.float32)
+    X[1, 128:] = 0.0                              # an all-zero group: q = 0, XS = 0, XA = 0
+    X[2, 5] = -3.0                                # lone max: q = -127 exactly
+    Q, XS, XA = orc.quant_q8(X)
+    assert (Q[0] == 0).all() and (XS[0] == 0).all() and (XA[0] == 0).all()
+    assert Q[1, 0] == -127 and Q[1, 127] == 127 and (Q[1, 128:] == 0).all() and XS[1, 1] == 0
+    assert Q[2, 5] == -127 and XS[2, 0] == np.float32(3.0) / np.float32(127.0)
+    assert np.array_equal(XA, Q.reshape(3, 2, 128).astype(np.int64).sum(2))
+    assert np.abs(Q.astype(int)).max() <= 127
+
+
+def test_quant_ties_round_to_even(orc):
+    """q = rne(x * (127 / amax)): with amax = 127 the factor is exactly 1, so x = k + 0.5 rounds to even"""
+    x = np.zeros((1, 128), np.float32)
+    x[0, 0] = 127.0
+    x[0, 1:9] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5, 126.5]
+    Q, XS, _ = orc.quant_q8(x)
+    assert Q[0, :9].tolist() == [127, 0, 2, 2, 0, -2, -2, 4, 126]
+    assert XS[0, 0] == 1.0
+
+
+def test_quant_matches_reference_quant_q8(orc):
+    """the reference's own rounding (dsv41_cpu.c quant_q8, compiled from its source): give every 32-block of a
+    128-group the group's amax, so the 32-block and 128-group quantizers see the same amax and must agree"""
+    if orc.ref_dsv41() is None:
+        pytest.skip("oracle/_ref not built (reference sources absent)")
+    r = rng(11)
+    X = r.normal(0, 1, (8, 1024)).astype(np.float32)
+    G = X.reshape(8, 8, 4, 32)
+    amax = np.abs(X.reshape(8, 8, 128)).max(2)
+    G[:, :, :, 7] = amax[:, :, None] * np.where(r.random((8, 8, 4)) < 0.5, -1, 1)
+    X = G.reshape(8, 1024)
+    Q, XS, XA = orc.quant_q8(X)
+    for n in range(8):
+        q, d = orc.ref_quant_q8(X[n])
+        assert np.array_equal(q, Q[n])
+    # per-row mode: every group's q follows the row amax
+    Qr, XSr, XAr = orc.quant_q8(X, per_row=True)
+    rmax = np.abs(X).max(1)
+    assert np.all(XSr == (rmax / np.float32(127))[:, None])
+    assert np.array_equal(XAr, Qr.reshape(8, 8, 128).astype(np.int64).sum(2))
+
+
+def test_quant_per_row_matches_reference_on_uniform_groups(orc):
+    """per-row = per-group whenever each group holds the row max"""
+    X = rng(12).normal(0, 1, (4, 512)).astype(np.float32)
+    m = np.abs(X).max(1, keepdims=True)
+    X.reshape(4, 4, 128)[:, :, 0] = m
+    assert all(np.array_equal(a, b) for a, b in zip(orc.quant_q8(X), orc.quant_q8(X, per_row=True)))
+
+
+# ------------------------------------------------------------------------------------------- ternary products
+def test_tern_acc_brute_force(orc):
+    """the exact group values equal an int64 matmul of the decoded trits (sum (d - 1) q, tc_hip.cu:12-15)"""
+    R, C, M = 40, 384, 3
+    dig = rand_digits(R, C, 21)
+    Q = rng(22).integers(-127, 128, (M, C)).astype(np.int8)
+    acc = orc.tern_acc(orc.pack_from_digits(dig), R, C, Q)
+    t = dig.astype(np.int64) - 1
+    ref = np.einsum("rgc,mgc->mrg", t.reshape(R, 3, 128), Q.astype(np.int64).reshape(M, 3, 128))
+    assert np.array_equal(acc, ref)
+    # the digit form with the activation sum: sum d q - XA
+    XA = Q.astype(np.int64).reshape(M, 3, 128).sum(2)
+    dq = np.einsum("rgc,mgc->mrg", dig.astype(np.int64).reshape(R, 3, 128), Q.astype(np.int64).reshape(M, 3, 128))
+    assert np.array_equal(acc, dq - XA[:, None, :])
+
+
+def test_tern_extremes(orc):
+    """|v| <= 128 * 127: all +1 against all 127 (and -1 against -127)"""
+    R, C = 2, 128
+    dig = np.full((R, C), 2, np.uint8)
+    dig[1] = 0
+    Q = np.full((1, C), 127, np.int8)
+    acc = orc.tern_acc(orc.pack_from_digits(dig), R, C, Q)
+    assert acc[0, :, 0].tolist() == [16256, -16256]
+
+
+def test_tern_out_float64(orc):
+    """the fp32 output agrees with the float64 value of sum_g v XS d"""
+    R, C, M = 64, 1024, 2
+    dig = rand_digits(R, C, 31)
+    dpm = rand_scales((C // 128, R), 32)
+    X = rng(33).normal(0, 1, (M, C)).astype(np.float32)
+    Y, acc, (Q, XS, XA) = orc.tern_linear(orc.pack_from_digits(dig), dpm, R, C, X)
+    d = dpm.view(np.float16).astype(np.float64)                     # [G, R]
+    ref = np.einsum("mrg,mg,gr->mr", acc.astype(np.float64), XS.astype(np.float64), d)
+    assert np.allclose(Y, ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
+    # and the dequantized-activation product it approximates
+    W = (dig.astype(np.float64) - 1) * np.repeat(d.T, 128, axis=1)
+    deq = Q.astype(np.float64) * np.repeat(XS, 128, axis=1)
+    assert np.allclose(Y, deq @ W.T, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
+
+
+def test_out_tree_cases(orc):
+    """the split tree with one split and one slice is the sequential chain; other trees differ only in rounding"""
+    R, C, M = 64, 2048, 2
+    dig = rand_digits(R, C, 41)
+    dpm = rand_scales((C // 128, R), 42)
+    X = rng(43).normal(0, 1, (M, C)).astype(np.float32)
+    Y, acc, (Q, XS, XA) = orc.tern_linear(orc.pack_from_digits(dig), dpm, R, C, X)
+    dq = dpm.view(np.float16).astype(np.float32)
+    assert np.array_equal(orc.out_tree(acc, XS, dq, 1, 1, 0), Y)
+    for sp, nw in ((2, 4), (3, 4), (1, 4), (5, 1)):
+        T = orc.out_tree(acc, XS, dq, sp, nw, 0)
+        assert np.allclose(T, Y, rtol=1e-5, atol=1e-6 * np.abs(Y).max())
+    # a hand-summed tree: 16 groups, 2 splits x 4 slices of 2 groups
+    v = acc[0, 3].astype(np.float64)
+    s = (XS[0] * dq[:, 3]).astype(np.float32).astype(np.float64)
+
+    def fma32(a, b, c):        # a * b + c rounded once: the float64 sum is exact here (|v| < 2^15, 24-bit s)
+        return np.float32(a * b + np.float64(c))
+
+    ch = [fma32(v[2 * i + 1], s[2 * i + 1], fma32(v[2 * i], s[2 * i], 0.0)) for i in range(8)]
+    q0 = np.float32(np.float32(np.float32(ch[0] + ch[1]) + ch[2]) + ch[3])
+    q1 = np.float32(np.float32(np.float32(ch[4] + ch[5]) + ch[6]) + ch[7])
+    assert orc.out_tree(acc, XS, dq, 2, 4, 0)[0, 3] == np.float32(q0 + q1)
+
+
+def test_tern_sum_order(orc):
+    P = rng(5).normal(0, 1, (2, 3, 7)).astype(np.float32)
+    y = orc.tern_sum(P, 7, 2, 3)
+    ref = np.float32(np.float32(P[:, 0] + P[:, 1]) + P[:, 2])
+    assert np.array_equal(y, ref)
+
+
+# ------------------------------------------------------------------------------------------- kcpu pair GEMV
+def test_pair_gemv_matches_reference_kcpu(orc):
+    """the restatement of kcpu.c's pair-table GEMV equals the reference's own gemv() (kcpu.c:116-135, compiled
+    from its source) bit for bit, and both match the float64 product"""
+    R, C = 256, 1024
+    dig = rand_digits(R, C, 51)
+    dpm = rand_scales((C // 128, R), 52)
+    bc = orc.pack_from_digits(dig)
+    Pc, S = orc.paircodes(bc, R, C), orc.pair_scales(dpm, R, C)
+    x = rng(53).normal(0, 1, C).astype(np.float32)
+    y = orc.pair_gemv(Pc, S, R, C, x)
+    W = (dig.astype(np.float64) - 1) * np.repeat(dpm.view(np.float16).astype(np.float64).T, 128, axis=1)
+    ref = W @ x.astype(np.float64)
+    assert np.allclose(y, ref, rtol=1e-4, atol=1e-5 * np.abs(ref).max())
+    if orc.ref_kcpu() is None:
+        pytest.skip("oracle/_ref not built")
+    assert np.array_equal(orc.ref_gemv(Pc, S, R, C, x), y)
+
+
+def test_pair_gemv_equals_int_path_on_dequantized_input(orc):
+    """fed the dequantized int8 activations, the fp32 table path and the int8 path agree to ~1e-6"""
+    R, C = 128, 2048
+    dig = rand_digits(R, C, 61)
+    dpm = rand_scales((C // 128, R), 62)
+    bc = orc.pack_from_digits(dig)
+    X = rng(63).normal(0, 1, (1, C)).astype(np.float32)
+    Y, acc, (Q, XS, XA) = orc.tern_linear(bc, dpm, R, C, X)
+    xhat = (Q[0].astype(np.float32) * np.repeat(XS[0], 128)).astype(np.float32)
+    y = orc.pair_gemv(orc.paircodes(bc, R, C), orc.pair_scales(dpm, R, C), R, C, xhat)
+    assert np.allclose(y, Y[0], rtol=1e-4, atol=2e-6 * np.abs(Y).max())
+
+
+# ------------------------------------------------------------------------------------------- q8_0
+def q8_case(R, C, seed):
+    r = rng(seed)
+    codes = r.integers(-127, 128, (R, C)).astype(np.int8)
+    sc = np.exp(r.normal(-6, 0.5, (R, C // 32))).astype(np.float16).view(np.uint16)
+    return codes, sc
+
+
+def test_q8_quant_matches_reference(orc):
+    """llama.cpp's CPU q8_0 rounding as the reference's dsv41_cpu.c quant_q8 implements it, bit for bit"""
+    x = rng(71).normal(0, 1, (6, 2688)).astype(np.float32)
+    x[2, :32] = 0.0
+    x[3, 64:96] = 0.5                                   # amax = 0.5 throughout a block
+    q, d = orc.q8_quant(x)
+    assert (q[2, :32] == 0).all() and d[2, 0] == 0
+    if orc.ref_dsv41() is None:
+        pytest.skip("oracle/_ref not built")
+    for n in range(6):
+        rq, rd = orc.ref_quant_q8(x[n])
+        assert np.array_equal(rq, q[n]) and np.array_equal(rd, d[n])
+
+
+def test_q8_acc_and_out(orc):
+    R, C, M = 48, 640, 3
+    codes, sc = q8_case(R, C, 72)
+    rows = orc.q8_0_rows(codes, sc)
+    x = rng(73).normal(0, 1, (M, C)).astype(np.float32)
+    q, d = orc.q8_quant(x)
+    acc = orc.q8_acc(rows, R, C, q)
+    ref = np.einsum("rbc,mbc->mrb", codes.astype(np.int64).reshape(R, -1, 32), q.astype(np.int64).reshape(M, -1, 32))
+    assert np.array_equal(acc, ref)
+    Y = orc.q8_out(acc, rows, R, C, d)
+    w = sc.view(np.float16).astype(np.float64)
+    yref = np.einsum("mrb,rb,mb->mr", acc.astype(np.float64), w, d.astype(np.float64))
+    assert np.allclose(Y, yref, rtol=1e-5, atol=1e-6 * np.abs(yref).max())
+    # the canonical chain is the split tree with one split and one slice (q8_0 form)
+    assert np.array_equal(orc.out_tree(acc, d, np.ascontiguousarray(w.astype(np.float32).T), 1, 1, 1), Y)
+    # the AVX2 baseline and the reference's k_q8g agree with it to rounding
+    for n in range(M):
+        ya = orc.q8_gemv_avx2(rows, R, C, q[n], d[n])
+        assert np.allclose(ya, Y[n], rtol=1e-5, atol=1e-6 * np.abs(Y).max())
+        if orc.ref_dsv41() is not None:
+            yk = orc.ref_k_q8g(orc.q8_0_group4(rows, R, C), R, C, q[n], d[n])
+            assert np.allclose(yk, Y[n], rtol=1e-5, atol=1e-6 * np.abs(Y).max())
+
+
+# ------------------------------------------------------------------------------------------- MoE
+def test_moe_sort_invariants(orc):
+    M, k, E = 37, 6, 128
+    r = rng(81)
+    ids = np.stack([r.choice(E, k, replace=False) for _ in range(M)]).astype(np.int32)
+    cnt, off, xrow, where = orc.moe_sort(ids, E)
+    assert cnt.sum() == M * k and np.array_equal(cnt, np.bincount(ids.ravel(), minlength=E))
+    assert np.array_equal(off, np.concatenate([[0], np.cumsum(cnt)[:-1]]))
+    assert sorted(where.tolist()) == list(range(M * k))            # a permutation
+    for i in range(M * k):
+        e, p = ids.ravel()[i], where[i]
+        assert off[e] <= p < off[e] + cnt[e] and xrow[p] == i // k
+    for e in range(E):                                               # stable: ascending flat index inside a range
+        seg = [i for i in range(M * k) if ids.ravel()[i] == e]
+        assert [where[i] for i in seg] == list(range(off[e], off[e] + cnt[e]))
+
+
+def test_moe_combine_brute_force(orc):
+    M, k, cols = 5, 6, 33
+    r = rng(82)
+    where = r.permutation(M * k).astype(np.int32)
+    gw = r.random((M, k)).astype(np.float32)
+    yd = r.normal(0, 1, (M * k, cols)).astype(np.float32)
+    ysh = r.normal(0, 1, (M, cols)).astype(np.float32)
+    x = r.normal(0, 1, (M, cols)).astype(np.float32)
+    out = orc.moe_combine(yd, ysh, where, gw, x)
+    ref = x.astype(np.float64) + np.einsum("mj,mjc->mc", gw.astype(np.float64),
+                                           yd[where.reshape(M, k)].astype(np.float64)) + ysh
+    assert np.allclose(out, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_router_softmax_topk(orc):
+    """against a float64 softmax over all E, top-k by probability, renormalized"""
+    M, E, k = 50, 128, 6
+    lg = rng(83).normal(0, 1, (M, E)).astype(np.float32)
+    ids, gw = orc.router_topk(lg, k)
+    p = np.exp(lg.astype(np.float64) - lg.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    top = np.argsort(-p, axis=1, kind="stable")[:, :k]
+    assert np.array_equal(ids, top)
+    sel = np.take_along_axis(p, top, 1)
+    assert np.allclose(gw, sel / sel.sum(1, keepdims=True), rtol=1e-6)
+    # ties go to the lower expert index
+    t = np.zeros((1, 8), np.float32)
+    t[0, [5, 2, 6]] = 1.0
+    ids, gw = orc.router_topk(t, 2)
+    assert ids.tolist() == [[2, 5]] and np.allclose(gw, 0.5)
