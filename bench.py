@@ -1,0 +1,348 @@
+"""Benchmark of the quantized linear-layer path on one MI355X.
+
+Headline (BASELINE.json metric, config 3): the 27B-class decode sweep at M = 1. One step = the ternary products of
+one decode token through all 64 layers, in the engine's launch order per layer: q/k/v in one launch, o, gate/up in
+one launch, down (256 launches, k_tc_mv3 / k_tc_mv as spec.py:619-673 issues them), over int8 activations that are
+resident and quantized before the timed region. The 448 weight matrices (5.62 GB packed) are resident in HBM and
+streamed once per step. value = algorithmic bytes per step / time per step (GB/s).
+
+Also reported (under "configs"): config 0 (one product), config 1 (2B layer, M = 1 / 4 / 8), config 2 (prefill
+int8 TOPS, M = 512 / 2048), config 3 at M = 16, config 4 (q8_0 MoE step, M = 1 / 256).
+
+The CPU baseline (cpu_baseline) is the reference's own kcpu.c fp32 pair-table GEMV (oracle/_ref, compiled from
+the reference source) on one 27B layer, or the repo's restatement of it when _ref is absent.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+def log(*a):
+    print("[bench %.0fs]" % (time.time() - T0), *a, file=sys.stderr, flush=True)
+
+
+T0 = time.time()
+HBM_PEAK = 8000.0            # GB/s, MI355X published
+INT8_PEAK = 5000.0           # TOPS dense, MI355X published
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--quick", action="store_true", help="headline only")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
+    return ap.parse_args()
+
+
+def tern_bytes(R, C, M, shared_input=True):
+    """algorithmic HBM bytes of one product: codes 2 b/w + fp16 scale per 128, int8 input + XS/XA per group,
+    fp32 output"""
+    return R * C // 4 + R * (C // 128) * 2 + (M * C + M * (C // 128) * 8 if shared_input else 0) + M * R * 4
+
+
+class Timer(object):
+    """HIP events on torch's current stream (the stream every kt_* launch here goes to)"""
+
+    def __init__(self, torch):
+        self.t = torch
+
+    def run(self, fn, steps, warmup):
+        t = self.t
+        for _ in range(warmup):
+            fn()
+        t.cuda.synchronize()
+        e0, e1 = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        t.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps           # ms per step
+
+
+def graphed(torch, fn, use_graph):
+    """capture fn's launches in a HIP graph (no memsets inside: every buffer is prepared before capture)"""
+    if not use_graph:
+        return fn
+    fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g.replay
+
+
+# ----------------------------------------------------------------------------------------------- config 3
+def build_27b(torch, linear, synth, M_list):
+    cfg = synth.CFG["c3"]
+    layers = []
+    for l in range(cfg["layers"]):
+        mats = {}
+        for i, (n, R, C) in enumerate(cfg["mats"]):
+            bc, dpm = synth.tern_pack(R, C, 100 + l * 8 + i, device="cuda")
+            mats[n] = linear.TernaryMatrix(bc, dpm, R, C)
+            del bc, dpm
+        layers.append(mats)
+    torch.cuda.synchronize()
+    return layers
+
+
+def sweep_step(torch, linear, layers, M, seed=7):
+    """the per-layer launches of one decode step over resident int8 activations; returns (fn, bytes, launches)"""
+    Lin = linear.Linear({})
+    acts, outs = [], []
+    nbytes, launches = 0, []
+    for l, mats in enumerate(layers):
+        for n, m in mats.items():
+            Lin.add("%d.%s" % (l, n), m)
+        x = [torch.randn((M, C), device="cuda", generator=torch.Generator(device="cuda").manual_seed(seed + 4 * l + i))
+             for i, C in enumerate((5120, 5120, 5120, 17408))]
+        a = [linear.quantize(xi) for xi in x]
+        o = {n: torch.empty((M, m.R), dtype=torch.float32, device="cuda") for n, m in mats.items()}
+        acts.append(a)
+        outs.append(o)
+        nbytes += sum(tern_bytes(mats[n].R, mats[n].C, M, i == 0) for grp in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",))
+                      for i, n in enumerate(grp))
+        launches += [("%d.q/k/v" % l, tern_bytes(mats["q"].R + mats["k"].R + mats["v"].R, 5120, M)),
+                     ("%d.o" % l, tern_bytes(5120, 5120, M)),
+                     ("%d.gate/up" % l, tern_bytes(2 * 17408, 5120, M)),
+                     ("%d.down" % l, tern_bytes(5120, 17408, M))]
+    # size the shared workspace for the largest launch before any capture (it is zero-filled once)
+    lib = __import__("kindi_amd.gpudrv", fromlist=["x"]).load()
+    need = max(lib.kt_tern_gemv3_workspace(5120, 1024, 1024, 5120, M), lib.kt_tern_gemv_workspace(5120, 5120, M),
+               lib.kt_tern_gemv3_workspace(17408, 17408, 0, 5120, M), lib.kt_tern_gemv_workspace(5120, 17408, M))
+    Lin.ws.get(need)
+
+    calls = []
+    for l in range(len(layers)):
+        a, o = acts[l], outs[l]
+        p = "%d." % l
+        calls.append((Lin.gemv_q, [p + "q", p + "k", p + "v"], a[0], [o["q"], o["k"], o["v"]]))
+        calls.append((Lin.gemv_q, [p + "o"], a[1], [o["o"]]))
+        calls.append((Lin.gemv_q, [p + "gate", p + "up"], a[2], [o["gate"], o["up"]]))
+        calls.append((Lin.gemv_q, [p + "down"], a[3], [o["down"]]))
+
+    def step():
+        for f, names, act, o in calls:
+            f(names, act, o)
+
+    return step, nbytes, calls, launches
+
+
+def per_launch_ms(torch, calls):
+    """one instrumented pass: HIP events around every launch (the dominant kernel's duration per launch)"""
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(len(calls) + 1)]
+    torch.cuda.synchronize()
+    evs[0].record()
+    for i, (f, names, act, o) in enumerate(calls):
+        f(names, act, o)
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    return [evs[i].elapsed_time(evs[i + 1]) for i in range(len(calls))]
+
+
+# ----------------------------------------------------------------------------------------------- other configs
+def config0(torch, linear, synth, timer, steps, use_graph):
+    R, C = synth.CFG["c0"]["R"], synth.CFG["c0"]["C"]
+    bc, dpm = synth.tern_pack(R, C, 0, device="cuda")
+    L = linear.Linear({"w": linear.TernaryMatrix(bc, dpm, R, C)})
+    act = linear.quantize(synth.activations(1, C, 1, device="cuda"), per_row=True)
+    Y = torch.empty((1, R), dtype=torch.float32, device="cuda")
+    L.ws.get(__import__("kindi_amd.gpudrv", fromlist=["x"]).load().kt_tern_gemv_workspace(R, C, 1))
+    reps = 50
+
+    def fn():
+        for _ in range(reps):
+            L.gemv_q(["w"], act, [Y])
+
+    ms = timer.run(graphed(torch, fn, use_graph), steps, 2) / reps
+    b = tern_bytes(R, C, 1)
+    return {"shape": [R, C], "M": 1, "us": round(ms * 1e3, 3), "GB/s": round(b / ms / 1e6, 1),
+            "bytes": b, "note": "%d back-to-back launches per timed step" % reps}
+
+
+def config1(torch, linear, synth, timer, steps, use_graph):
+    cfg = synth.CFG["c1"]
+    mats = {}
+    for i, (n, R, C) in enumerate(cfg["mats"]):
+        bc, dpm = synth.tern_pack(R, C, 10 + i, device="cuda")
+        mats[n] = linear.TernaryMatrix(bc, dpm, R, C)
+    L = linear.Linear(mats)
+    lib = __import__("kindi_amd.gpudrv", fromlist=["x"]).load()
+    res = {}
+    for M in (1, 4, 8):
+        x = [synth.activations(M, C, 30 + i, device="cuda") for i, C in enumerate((2048, 2048, 2048, 6144))]
+        a = [linear.quantize(xi, per_row=True) for xi in x]
+        o = {n: torch.empty((M, m.R), dtype=torch.float32, device="cuda") for n, m in mats.items()}
+        L.ws.get(max(lib.kt_tern_gemv3_workspace(2048, 512, 512, 2048, M), lib.kt_tern_gemv_workspace(2048, 2048, M),
+                     lib.kt_tern_gemv3_workspace(6144, 6144, 0, 2048, M), lib.kt_tern_gemv_workspace(2048, 6144, M)))
+        reps = 20
+
+        def fn():
+            for _ in range(reps):
+                L.gemv_q(["q", "k", "v"], a[0], [o["q"], o["k"], o["v"]])
+                L.gemv_q(["o"], a[1], [o["o"]])
+                L.gemv_q(["gate", "up"], a[2], [o["gate"], o["up"]])
+                L.gemv_q(["down"], a[3], [o["down"]])
+
+        ms = timer.run(graphed(torch, fn, use_graph), steps, 2) / reps
+        b = (tern_bytes(3072, 2048, M) + tern_bytes(2048, 2048, M) + tern_bytes(12288, 2048, M)
+             + tern_bytes(2048, 6144, M))
+        res["M=%d" % M] = {"us_per_layer": round(ms * 1e3, 2), "GB/s": round(b / ms / 1e6, 1), "bytes": b}
+    return res
+
+
+def config2(torch, linear, synth, timer, steps):
+    res = {}
+    for i, (n, R, C) in enumerate(synth.CFG["c2"]["mats"]):
+        bc, dpm = synth.tern_pack(R, C, 20 + i, device="cuda")
+        L = linear.Linear({"w": linear.TernaryMatrix(bc, dpm, R, C)})
+        for M in (512, 2048):
+            act = linear.quantize(synth.activations(M, C, 22 + i, device="cuda"), per_row=True)
+            Y16 = torch.empty((M, R), dtype=torch.float16, device="cuda")
+            ms = timer.run(lambda: L.gemm("w", act, Y16=Y16), max(steps // 2, 3), 2)
+            tops = 2.0 * M * R * C / ms / 1e9
+            res["%s M=%d" % (n, M)] = {"shape": [R, C], "us": round(ms * 1e3, 1), "TOPS": round(tops, 1),
+                                       "frac_int8_peak": round(tops / INT8_PEAK, 4)}
+    return res
+
+
+def config4(torch, moe, synth, timer, steps, use_graph):
+    c = synth.CFG["c4"]
+    E, k, H, F = c["E"], c["k"], c["H"], c["F"]
+    up = moe.Q8Experts([synth.q8_rows(F, H, 40_000 + e, device="cuda") for e in range(E)], F, H)
+    down = moe.Q8Experts([synth.q8_rows(H, F, 50_000 + e, device="cuda") for e in range(E)], H, F)
+    layer = moe.MoE(up, down, k)
+    res = {}
+    for M in (1, 256):
+        x0 = synth.activations(M, H, 42, device="cuda")
+        lg = synth.logits(M, E, 41, device="cuda")
+        x = x0.clone()
+        bufs = layer.buffers(M)
+        out, st = layer.forward(x, lg, bufs)
+        torch.cuda.synchronize()
+        touched = int((st["lists"][0] > 0).sum().item())
+        per_expert = 2 * up.bytes_per_expert
+        b = touched * per_expert + M * H * (4 + 1 + 4 / 32) + M * k * (F * (4 + 1 + 4 / 32) + H * 4) + M * H * 4
+        ms = timer.run(graphed(torch, lambda: layer.forward(x, lg, bufs), use_graph), steps, 2)
+        res["M=%d" % M] = {"experts_touched": touched, "us": round(ms * 1e3, 1), "GB/s": round(b / ms / 1e6, 1),
+                           "bytes": int(b), "frac_hbm": round(b / ms / 1e6 / HBM_PEAK, 4)}
+    return res
+
+
+# ----------------------------------------------------------------------------------------------- CPU baseline
+def cpu_baseline(synth, budget_s=20.0):
+    """kcpu.c's pair-table GEMV over one 27B layer (7 matrices), on the host's cores"""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    ref = orc.ref_kcpu() is not None
+    mats = []
+    nbytes = 0
+    for i, (n, R, C) in enumerate(synth.CFG["c3"]["mats"]):
+        bc, dpm = synth.tern_pack(R, C, 100 + i, device="cpu")
+        bc = bc.numpy()
+        dpm = dpm.numpy().view(np.uint16)
+        mats.append((orc.paircodes_fast(bc, R, C), orc.pair_scales(dpm, R, C), R, C))
+        nbytes += tern_bytes(R, C, 1)
+    xs = {C: np.random.default_rng(C).normal(0, 1, C).astype(np.float32) for C in (5120, 17408)}
+    gemv = orc.ref_gemv if ref else orc.pair_gemv
+
+    def layer():
+        for Pc, S, R, C in mats:
+            gemv(Pc, S, R, C, xs[C])
+
+    layer()
+    times = []
+    t_end = time.time() + budget_s
+    while len(times) < 5 or (time.time() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        layer()
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count()))
+    return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": threads,
+            "kind": "reference" if ref else "port",
+            "sample": "one 27B-class layer (q,k,v,o,gate,up,down; %.1f MB of ternary weights) per rep, fp32 "
+                      "pair-table GEMV (kcpu.c gemv), median of %d reps, %d OpenMP threads" % (nbytes / 1e6, len(times), threads)}
+
+
+# ----------------------------------------------------------------------------------------------- main
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print("bench.py: this build measures one GPU; the product shards per GPU (see DESIGN.md) but multi-GPU "
+              "runs are not part of it. Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from kindi_amd import linear, moe, synth
+    torch.cuda.set_device(0)
+    timer = Timer(torch)
+    use_graph = not a.no_graph
+
+    t0 = time.time()
+    log("building the 27B-class weights")
+    layers = build_27b(torch, linear, synth, (1, 16))
+    log("config 3, M=1")
+    step, nbytes, calls, launches = sweep_step(torch, linear, layers, 1)
+    run = graphed(torch, step, use_graph)
+    ms = timer.run(run, a.steps, a.warmup)
+    gbs = nbytes / ms / 1e6
+    # the dominant kernel (k_gemv<ternary, 1 token>): its per-launch durations, events around each launch
+    dur = per_launch_ms(torch, calls)
+    dur = per_launch_ms(torch, calls)
+    kern_ms = sum(dur)
+    achieved = nbytes / kern_ms / 1e6
+    out = {
+        "metric": "decode GEMV HBM GB/s (% of 8 TB/s) + prefill int8 TOPS, ternary 27B shapes",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 x ternary (int32 accumulate, fp32 scale)", "data": "synthetic (seeded; BASELINE config 3)",
+        "config": {"workload": "config 3: 27B-class decode sweep, 64 layers x {q,k,v,o,gate,up,down}, M=1",
+                   "tokens": 1, "bytes_per_step": nbytes, "launches_per_step": len(calls),
+                   "graph": use_graph, "frac_hbm": round(gbs / HBM_PEAK, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK, 4), "traffic": None,
+                     "kernel": "k_gemv<ternary,MT=1>", "launches": len(calls),
+                     "avg_launch_us": round(kern_ms / len(calls) * 1e3, 3)},
+    }
+    if not a.quick:
+        cfgs = {}
+        log("config 3, M=16")
+        step16, nb16, calls16, _ = sweep_step(torch, linear, layers, 16)
+        ms16 = timer.run(graphed(torch, step16, use_graph), max(a.steps // 2, 3), 2)
+        cfgs["c3 M=16"] = {"ms_per_step": round(ms16, 4), "GB/s": round(nb16 / ms16 / 1e6, 1),
+                           "frac_hbm": round(nb16 / ms16 / 1e6 / HBM_PEAK, 4)}
+        del layers, step16, calls16, step, calls, run
+        torch.cuda.empty_cache()
+        log("configs 0, 1, 2, 4")
+        cfgs["c0"] = config0(torch, linear, synth, timer, a.steps, use_graph)
+        cfgs["c1"] = config1(torch, linear, synth, timer, a.steps, use_graph)
+        cfgs["c2"] = config2(torch, linear, synth, timer, a.steps)
+        cfgs["c4"] = config4(torch, moe, synth, timer, a.steps, use_graph)
+        out["configs"] = cfgs
+    if not a.no_cpu:
+        log("cpu baseline")
+        out["cpu_baseline"] = cpu_baseline(synth)
+    out["wall_s"] = round(time.time() - t0, 1)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -223,6 +223,27 @@ static void or_rows8(const uint32_t* P, const float* S, int C, float* y, const f
   }
 }
 
+/* cpu.paircodes (cpu.py:69-88) from the pack: P [R/8][C/128][64] u32, word p = the 8 rows' 4-bit codes of columns
+   2p, 2p+1 (code of the digit pair (d0, d1): d0 + 3 d1 mapped 0 1 2 3 8 4 5 6 7, i.e. 4 = both zero -> 8) */
+void or_paircodes(const uint8_t* bcodes, int R, int C, uint32_t* P){
+  static const uint32_t code[9] = {0, 1, 2, 3, 8, 4, 5, 6, 7};
+  const int G = C / 128;
+  #pragma omp parallel for schedule(static)
+  for(int rb = 0; rb < R / 8; ++rb)
+    for(int g = 0; g < G; ++g)
+      for(int p = 0; p < 64; ++p){
+        const int s = (g * 128 + 2 * p) >> 2, sh = (2 * p) & 3;      /* both columns sit in one pack byte */
+        uint32_t w = 0;
+        for(int l = 0; l < 8; ++l){
+          unsigned int b = bcodes[(size_t)s * R + rb * 8 + l];
+          if(sh) b /= 9u;
+          const uint32_t d0 = b % 3u, d1 = (b / 3u) % 3u;
+          w |= code[d0 + 3 * d1] << (4 * l);
+        }
+        P[((size_t)rb * G + g) * 64 + p] = w;
+      }
+}
+
 /* y = W x over all threads: tables for the whole input, then 8-row blocks split evenly (kcpu.c:116-135).
    T: scratch of C * 4 floats (C/2 pairs x 8), 32-byte aligned. */
 void or_pair_gemv(const uint32_t* P, const float* S, int R, int C, const float* x, float* y, float* T){

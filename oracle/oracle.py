@@ -51,6 +51,7 @@ def lib():
         h.or_tern_sum.argtypes = [P, P, I, I, I]
         h.or_out_tree.argtypes = [P, P, I, P, I, I, I, I, I, I, P, I]
         h.or_pair_gemv.argtypes = [P, P, I, I, P, P, P]
+        h.or_paircodes.argtypes = [P, I, I, P]
         h.or_q8_quant.argtypes = [P, I, P, P]
         h.or_q8_acc.argtypes = [P, I, I, P, I, I, P]
         h.or_q8_out.argtypes = [P, P, I, I, P, I, I, P, I]
@@ -143,6 +144,13 @@ def paircodes(bcodes, R, C):
     for l in range(8):
         word |= pc[:, l] << np.uint32(4 * l)
     return word
+
+
+def paircodes_fast(bcodes, R, C):
+    """paircodes() in C (OpenMP), for full-size matrices"""
+    out = np.empty((R // 8, C // 128, 64), np.uint32)
+    lib().or_paircodes(_p(_c(bcodes, np.uint8)), R, C, _p(out))
+    return out
 
 
 def pair_scales(dpm, R, C):

@@ -49,6 +49,12 @@ def test_ptq1_round_trip_and_known_answer(orc):
     assert np.array_equal(orc.trits_from_ptq1(r2), d2)
 
 
+def test_paircodes_fast_matches_numpy(orc):
+    R, C = 64, 512
+    bc = orc.pack_from_digits(rand_digits(R, C, 6))
+    assert np.array_equal(orc.paircodes_fast(bc, R, C), orc.paircodes(bc, R, C))
+
+
 def test_paircodes_decode(orc):
     """cpu.paircodes (cpu.py:69-88): code k < 8 -> the k-th nonzero (w0, w1) pair, 8 -> both zero"""
     R, C = 16, 256
