@@ -28,7 +28,7 @@ static inline bool kt_al(const void* p, size_t a){ return ((uintptr_t)p % a) == 
 /* the K split of a launch over ntiles 64-row tiles and NU units: a function of the shape only (never of M), so a
    token's result does not depend on how many tokens share the pass, and is fixed across runs */
 static int kt_nsplit(int ntiles, int NU, int min_units){
-  const int target_blocks = 2048 / KT_WAVES;                 /* 8 waves per CU on 256 CUs */
+  const int target_blocks = KT_TARGET_WAVES / KT_WAVES;
   int sp = (target_blocks + ntiles - 1) / ntiles;
   const int cap = NU / (KT_WAVES * min_units);
   if(sp > cap) sp = cap;
@@ -110,12 +110,12 @@ int kt_quant_q8(const float* X, int ldx, int M, int C, int per_row, int8_t* XQ, 
 /* ------------------------------------------------------------------ decode products */
 int kt_tern_gemv_splits(int R, int C){
   if(R <= 0 || C <= 0 || C % 128) return 0;
-  return kt_nsplit(kt_rp(R) / KT_TR, C / 128, 2);
+  return kt_nsplit(kt_rp(R) / KT_TR, C / 128, KT_MIN_UNITS);
 }
 
 size_t kt_tern_gemv_workspace(int R, int C, int M){
   if(R <= 0 || C <= 0 || C % 128 || M <= 0) return 0;
-  const int ntiles = kt_rp(R) / KT_TR, sp = kt_nsplit(ntiles, C / 128, 2), mt = kt_mt(M);
+  const int ntiles = kt_rp(R) / KT_TR, sp = kt_nsplit(ntiles, C / 128, KT_MIN_UNITS), mt = kt_mt(M);
   (void)mt;
   return kt_ws_bytes(sp, M, ntiles);
 }
@@ -145,7 +145,7 @@ static int kt_tern_gemv_n(int nmat, const void* const* W, const int* Rs, float* 
   a.xq = XQ; a.ldq = ldq; a.xs = XS; a.xa = (const int*)XA; a.ldxs = NG;
   a.M = M;
   a.dbg = dbg;
-  a.nsplit = kt_nsplit(tiles, NG, 2);
+  a.nsplit = kt_nsplit(tiles, NG, KT_MIN_UNITS);
   a.Rtot = tiles * KT_TR;
   a.ntiles = tiles;
   if(kt_ws_set(a, ws)) return KT_INVALID;
@@ -163,7 +163,7 @@ int kt_tern_gemv(const void* W, int R, int C, const int8_t* XQ, int ldq, const f
 size_t kt_tern_gemv3_workspace(int R0, int R1, int R2, int C, int M){
   if(C <= 0 || C % 128 || M <= 0 || R0 <= 0) return 0;
   const int tiles = kt_rp(R0) / KT_TR + (R1 > 0 ? kt_rp(R1) / KT_TR : 0) + (R2 > 0 ? kt_rp(R2) / KT_TR : 0);
-  return kt_ws_bytes(kt_nsplit(tiles, C / 128, 2), M, tiles);
+  return kt_ws_bytes(kt_nsplit(tiles, C / 128, KT_MIN_UNITS), M, tiles);
 }
 
 int kt_tern_gemv3(const void* W0, int R0, float* Y0, const void* W1, int R1, float* Y1, const void* W2, int R2,

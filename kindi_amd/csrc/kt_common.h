@@ -24,6 +24,18 @@
 
 #define KT_TR 64                      /* rows per tile = lanes per wave */
 #define KT_WAVES 4                    /* waves per decode block: K slices reduced in LDS */
+#ifndef KT_UB_TERN
+#define KT_UB_TERN 4                  /* ternary units (128 columns) whose loads a wave keeps in flight */
+#endif
+#ifndef KT_UB_Q8
+#define KT_UB_Q8 8                    /* q8_0 units (32 columns) likewise */
+#endif
+#ifndef KT_TARGET_WAVES
+#define KT_TARGET_WAVES 2048          /* waves a decode launch aims for (K split chosen from it) */
+#endif
+#ifndef KT_MIN_UNITS
+#define KT_MIN_UNITS 2                /* least ternary units per wave when splitting K */
+#endif
 #define KT_MAXMAT 3                   /* matrices sharing one input in a launch (q/k/v, gate/up) */
 
 enum { KT_FMT_TERN = 0, KT_FMT_Q8 = 1 };

@@ -202,7 +202,7 @@ __global__ void __launch_bounds__(256) k_gemv(const KtGemvArgs a, const int8_t* 
   const uint4* __restrict__ wp = (const uint4*)mat.codes + (long long)tile * NU * 128 + lane;
   const uint16_t* __restrict__ sc = mat.scales + (long long)tile * NU * 64 + lane;
   constexpr int XW = FMT == KT_FMT_TERN ? 32 : 8;             /* activation words per unit */
-  constexpr int UB = FMT == KT_FMT_TERN ? 4 : 8;              /* units whose loads are in flight together */
+  constexpr int UB = FMT == KT_FMT_TERN ? KT_UB_TERN : KT_UB_Q8; /* units whose loads are in flight together */
 
   float acc[MT];
 #pragma unroll
@@ -258,29 +258,35 @@ __global__ void __launch_bounds__(256) k_gemv(const KtGemvArgs a, const int8_t* 
     }
     return;
   }
-  /* split K across blocks: park this part, the last block of the tile adds the parts in split order */
+  /* split K across blocks: park this part, the last block of the tile adds the parts in split order. The parts
+     and the counter are accessed with agent-scope atomics (coherent across the XCDs' L2s, which an ordinary store
+     is not); the fences are workgroup-scope (they only order this wave's own accesses), because an agent-scope
+     fence would write back and invalidate the whole L2 of the XCD on every block. */
   const long long grow = (long long)gt * KT_TR + lane;
 #pragma unroll
   for(int t = 0; t < MT; ++t)
-    if(t < nt) a.parts[((long long)sp * a.M + t0 + t) * a.Rtot + grow] = q[t];
-  __threadfence();
+    if(t < nt) __hip_atomic_store(a.parts + ((long long)sp * a.M + t0 + t) * a.Rtot + grow, q[t], __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);                             /* the parts' stores have completed (sc1: write-through) */
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   int* cnt = a.counters + (long long)blockIdx.z * a.ntiles + gt;
   int last = 0;
-  if(lane == 0) last = atomicAdd(cnt, 1) == a.nsplit - 1;
+  if(lane == 0) last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.nsplit - 1;
   if(!__shfl(last, 0)) return;
-  __threadfence();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   if(row < mat.R){
 #pragma unroll
     for(int t = 0; t < MT; ++t){
       if(t < nt){
-        const float* p = a.parts + (long long)(t0 + t) * a.Rtot + grow;
-        float s = __builtin_nontemporal_load(p);
-        for(int k = 1; k < a.nsplit; ++k) s += __builtin_nontemporal_load(p + (long long)k * a.M * a.Rtot);
+        float* p = a.parts + (long long)(t0 + t) * a.Rtot + grow;
+        float s = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for(int k = 1; k < a.nsplit; ++k)
+          s += __hip_atomic_load(p + (long long)k * a.M * a.Rtot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         mat.y[(long long)(t0 + t) * mat.ldy + row] = s;
       }
     }
   }
-  if(lane == 0) *cnt = 0;                                    /* ready for the next launch */
+  if(lane == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   /* ready for the next launch */
 }
 
 #define KT_INST(FMT, MT) template __global__ void k_gemv<FMT, MT>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*);

@@ -190,3 +190,29 @@ def test_gemv_full_size_linearity(kt):
     rows = np.sort(r.choice(R, 64, replace=False))
     acc = orc.tern_acc(np.ascontiguousarray(host(bc_t)[:, rows]), 64, C, q1)
     assert np.array_equal(outs[0][:, rows], acc)
+
+
+def test_split_reduction_repeated(kt):
+    """the K-split's last-block reduction over many back-to-back launches on one shared workspace, alternating
+    shapes: every launch reproduces the same bits"""
+    lib, linear = kt
+    say("split reduction x400")
+    shapes = [(1024, 5120), (5120, 5120), (640, 2048)]
+    mats, acts, refs, outs = {}, {}, {}, {}
+    L = linear.Linear({})
+    for i, (R, C) in enumerate(shapes):
+        assert lib.kt_tern_gemv_splits(R, C) > 1
+        W = upload(linear, R, C, 50 + i)[0]
+        L.add(str(i), W)
+        acts[i] = linear.quantize(dev(rng(i).normal(0, 1, (1, C)).astype(np.float32)))
+        outs[i] = torch.empty((1, R), dtype=torch.float32, device="cuda")
+        L.gemv_q([str(i)], acts[i], [outs[i]])
+        refs[i] = host(outs[i]).copy()
+    bad = 0
+    for k in range(400):
+        i = k % 3
+        outs[i].fill_(float("nan"))
+        L.gemv_q([str(i)], acts[i], [outs[i]])
+        if k % 10 == 9 or k > 390:
+            bad += int(not np.array_equal(host(outs[i]), refs[i]))
+    assert bad == 0
