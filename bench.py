@@ -123,11 +123,6 @@ def sweep_step(torch, linear, layers, M, seed=7):
                      ("%d.o" % l, tern_bytes(5120, 5120, M)),
                      ("%d.gate/up" % l, tern_bytes(2 * 17408, 5120, M)),
                      ("%d.down" % l, tern_bytes(5120, 17408, M))]
-    # size the shared workspace for the largest launch before any capture (it is zero-filled once)
-    lib = __import__("kindi_amd.gpudrv", fromlist=["x"]).load()
-    need = max(lib.kt_tern_gemv3_workspace(5120, 1024, 1024, 5120, M), lib.kt_tern_gemv_workspace(5120, 5120, M),
-               lib.kt_tern_gemv3_workspace(17408, 17408, 0, 5120, M), lib.kt_tern_gemv_workspace(5120, 17408, M))
-    Lin.ws.get(need)
 
     calls = []
     for l in range(len(layers)):
@@ -164,7 +159,6 @@ def config0(torch, linear, synth, timer, steps, use_graph):
     L = linear.Linear({"w": linear.TernaryMatrix(bc, dpm, R, C)})
     act = linear.quantize(synth.activations(1, C, 1, device="cuda"), per_row=True)
     Y = torch.empty((1, R), dtype=torch.float32, device="cuda")
-    L.ws.get(__import__("kindi_amd.gpudrv", fromlist=["x"]).load().kt_tern_gemv_workspace(R, C, 1))
     reps = 50
 
     def fn():
@@ -184,14 +178,11 @@ def config1(torch, linear, synth, timer, steps, use_graph):
         bc, dpm = synth.tern_pack(R, C, 10 + i, device="cuda")
         mats[n] = linear.TernaryMatrix(bc, dpm, R, C)
     L = linear.Linear(mats)
-    lib = __import__("kindi_amd.gpudrv", fromlist=["x"]).load()
     res = {}
     for M in (1, 4, 8):
         x = [synth.activations(M, C, 30 + i, device="cuda") for i, C in enumerate((2048, 2048, 2048, 6144))]
         a = [linear.quantize(xi, per_row=True) for xi in x]
         o = {n: torch.empty((M, m.R), dtype=torch.float32, device="cuda") for n, m in mats.items()}
-        L.ws.get(max(lib.kt_tern_gemv3_workspace(2048, 512, 512, 2048, M), lib.kt_tern_gemv_workspace(2048, 2048, M),
-                     lib.kt_tern_gemv3_workspace(6144, 6144, 0, 2048, M), lib.kt_tern_gemv_workspace(2048, 6144, M)))
         reps = 20
 
         def fn():

@@ -15,9 +15,9 @@
 
    Numbers (the reference's, tc.cu:1-18, tc_hip.cu:8-15): activations are int8 per 128-column group (XS = amax/127,
    q = round-to-nearest-even(x * 127 / amax), XA = sum q); a group's value v = sum t q over its 128 columns is an
-   exact int32 (t in {-1, 0, +1}); the fp32 output adds fmaf((float)v, XS * d, acc) group after group. A K split of a
-   product (fixed per shape, never per M) adds its parts in a fixed order, so a token's result does not depend on
-   how many tokens share the pass and is the same on every run. */
+   exact int32 (t in {-1, 0, +1}); the fp32 output adds fmaf((float)v, XS * d, acc) group after group (the prefill
+   product in exactly that order; the decode products in the fixed tree documented at kt_tern_gemv), so a token's
+   result is the same on every run. */
 #ifndef KT_H
 #define KT_H
 
@@ -53,21 +53,22 @@ int kt_quant_q8(const float* X, int ldx, int M, int C, int per_row, int8_t* XQ, 
 
 /* ---------------------------------------------------------------- decode products (1 .. 16 tokens a pass)
    Y[n][ldy] = W x_n for tokens n < M. dbg (nullable): the exact group values v, int32 [M][R][C/128].
-   ws: workspace of kt_tern_gemv_workspace(R, C, M) bytes (NULL when that is 0). Its first 64 KB hold the arrival
-   counters of the K split's last-block reduction: zero-fill them once when the workspace is allocated; every
-   launch leaves them zero, so one workspace serves every shape and M (sized for the largest). Launches that share
-   a workspace must not run concurrently (same stream, or ordered).
+   Every output row's sum is formed inside one block in a fixed order that depends only on C (never on M or R), so
+   a token's result does not depend on how many tokens share the pass. The order: the row's K units are split into
+   KS = kt_decode_kslices(C, 0) contiguous slices of whole steps (a step = 8 consecutive units; slice k = steps
+   [k S / KS, (k + 1) S / KS)); in a slice, lane c (0..7) chains fmaf over its units 8 s + c in increasing order,
+   the 8 lane sums are added by the xor butterfly ((l0 + l1) + (l2 + l3)) + ((l4 + l5) + (l6 + l7)), and the slice
+   sums are added left to right. No workspace, no second pass.
    Replaces k_tc_mv{2,4,8} + k_tc_sum (tc_hip.cu:180-199, 236-240, 271-279; spec.py:619-657). */
-int kt_tern_gemv_splits(int R, int C);
-size_t kt_tern_gemv_workspace(int R, int C, int M);
+int kt_decode_kslices(int C, int q8);
 int kt_tern_gemv(const void* W, int R, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M,
-                 float* Y, int ldy, int32_t* dbg, void* ws, void* stream);
+                 float* Y, int ldy, int32_t* dbg, void* stream);
 
 /* up to three matrices sharing one input (q/k/v, gate/up) in one launch; Y_i is [M][R_i]; R_i <= 0 ends the list.
-   Replaces k_tc_mv3_{2,4,8} (tc_hip.cu:201-234; spec.py:659-673). */
-size_t kt_tern_gemv3_workspace(int R0, int R1, int R2, int C, int M);
+   Each matrix's outputs are bit-identical to its own kt_tern_gemv. Replaces k_tc_mv3_{2,4,8} (tc_hip.cu:201-234;
+   spec.py:659-673). */
 int kt_tern_gemv3(const void* W0, int R0, float* Y0, const void* W1, int R1, float* Y1, const void* W2, int R2,
-                  float* Y2, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M, void* ws,
+                  float* Y2, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M,
                   void* stream);
 
 /* y[n R + r] = sum over parts p < sp of P[(n sp + p) R + r], in part order. k_tc_sum (tc_hip.cu:271-279). */
@@ -88,14 +89,13 @@ int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const f
    (d = fp16(amax/127), q = rne(x * 127 / amax); quant_q8 dsv41_cpu.c:251-280, moe_cpu.c:84-112); act = 1 applies
    relu^2 first (lt_quant2, lightning.cu:470).
    kt_q8_gemv: Y = W x for M tokens: per block v = sum w q exact, acc = fmaf((float)v, dw * dx, acc) (lt_mv_q8
-   lightning.cu:258-284, k_q8 dsv41_gpu.cu:131-296); dbg int32 [M][R][C/32]; ws as kt_tern_gemv. */
+   lightning.cu:258-284, k_q8 dsv41_gpu.cu:131-296), summed in kt_tern_gemv's order over 32-column units
+   (KS = kt_decode_kslices(C, 1)); dbg int32 [M][R][C/32]. */
 size_t kt_q8_weight_bytes(int R, int C);
 int kt_q8_pack(const uint8_t* rows, int R, int C, void* W, void* stream);
 int kt_q8_quant(const float* X, int ldx, int M, int C, int act, int8_t* Q, int ldq, float* D, int ldd, void* stream);
-int kt_q8_gemv_splits(int R, int C);
-size_t kt_q8_gemv_workspace(int R, int C, int M);
 int kt_q8_gemv(const void* W, int R, int C, const int8_t* Q, int ldq, const float* D, int ldd, int M, float* Y,
-               int ldy, int32_t* dbg, void* ws, void* stream);
+               int ldy, int32_t* dbg, void* stream);
 
 /* ---------------------------------------------------------------- MoE
    kt_moe_topk: logits [M][E] -> ids / gw [M][k]: softmax, the k largest (ties to the lower index), weights

@@ -1,19 +1,22 @@
-/* kt_api.hip - the C ABI of libkt_gfx950.so: host-side validation, launch plans and launches. Every entry point
-   takes caller-owned device pointers and a stream (NULL = the null stream), never allocates, never synchronizes,
-   and returns a hipError_t as int (0 = success; hipErrorInvalidValue for shapes or strides the kernels do not
-   take). The declarations and the reference interfaces they replace are in include/kt.h. */
+/* kt_api.hip - the C ABI of libkt_gfx950.so: host-side validation and launches. Every entry point takes
+   caller-owned device pointers and a stream (NULL = the null stream), never allocates, never synchronizes, and
+   returns a hipError_t as int (0 = success; hipErrorInvalidValue for shapes or strides the kernels do not take).
+   The declarations and the reference interfaces they replace are in include/kt.h. */
 #include "kt_common.h"
 #include "../../include/kt.h"
 
-template <int FMT, int MT> __global__ void k_gemv(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*);
-template <int MT> __global__ void k_q8_grouped(const KtGroupedArgs);
-extern "C" __global__ void k_tern_pack(const uint8_t*, const uint16_t*, int, int, int, uint32_t*, uint16_t*);
-extern "C" __global__ void k_q8_pack(const uint8_t*, int, int, int, uint32_t*, uint16_t*);
+template <int FMT, int MT, int KS, int RGB, bool XL>
+__global__ void k_gemv(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*);
+template <int FMT, int MT, int KS, int RPL, bool DBG>
+__global__ void k_gemv_pipe(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*);
+template <int MT> __global__ void k_q8_grouped(const KtGroupedArgs, const int8_t*, const float*, float*, int32_t*);
+extern "C" __global__ void k_tern_pack(const uint8_t*, const uint16_t*, int, int, uint32_t*, uint16_t*);
+extern "C" __global__ void k_q8_pack(const uint8_t*, int, int, uint32_t*, uint16_t*);
 extern "C" __global__ void k_quant_tern(const float*, int, int, int, int8_t*, int, float*, int*);
 extern "C" __global__ void k_quant_q8(const float*, int, int, int, int8_t*, int, float*, int);
 extern "C" __global__ void k_tern_sum(const float*, float*, int, int, int);
-extern "C" __global__ void k_tern_gemm(const uint32_t*, const uint16_t*, int, int, int, const int8_t*, int,
-                                       const float*, int, float*, uint16_t*, int, int32_t*);
+extern "C" __global__ void k_tern_gemm(const uint32_t*, const uint16_t*, int, int, const int8_t*, int, const float*,
+                                       int, float*, uint16_t*, int, int32_t*);
 extern "C" __global__ void k_moe_topk(const float*, int, int, int*, float*);
 extern "C" __global__ void k_moe_sort(const int*, int, int, int*, int*, int*, int*, int*, int*, int);
 extern "C" __global__ void k_moe_combine(const float*, const float*, const int*, const float*, int, int, float*);
@@ -22,51 +25,112 @@ extern "C" __global__ void k_moe_combine(const float*, const float*, const int*,
 #define KT_LAUNCH_CHECK() do { const hipError_t _e = hipGetLastError(); if(_e != hipSuccess) return (int)_e; } while(0)
 
 static inline hipStream_t kt_stream(void* s){ return (hipStream_t)s; }
-static inline int kt_rp(int R){ return (R + KT_TR - 1) / KT_TR * KT_TR; }
 static inline bool kt_al(const void* p, size_t a){ return ((uintptr_t)p % a) == 0; }
-
-/* the K split of a launch over ntiles 64-row tiles and NU units: a function of the shape only (never of M), so a
-   token's result does not depend on how many tokens share the pass, and is fixed across runs */
-static int kt_nsplit(int ntiles, int NU, int min_units){
-  const int target_blocks = KT_TARGET_WAVES / KT_WAVES;
-  int sp = (target_blocks + ntiles - 1) / ntiles;
-  const int cap = NU / (KT_WAVES * min_units);
-  if(sp > cap) sp = cap;
-  if(sp < 1) sp = 1;
-  return sp;
-}
-
-/* workspace: the arrival counters of every launch live in a fixed prefix (zero between launches, whatever shape
-   used the workspace before), the partial sums after it */
-#define KT_WS_COUNTERS 16384
-#define KT_WS_PARTS ((size_t)KT_WS_COUNTERS * 4)
-static size_t kt_ws_bytes(int nsplit, int M, int ntiles){
-  return nsplit <= 1 ? 0 : KT_WS_PARTS + (size_t)nsplit * M * ntiles * KT_TR * 4;
-}
-static int kt_ws_set(KtGemvArgs& a, void* ws){
-  if(a.nsplit <= 1) return 0;
-  const int mt = a.M <= 1 ? 1 : a.M <= 2 ? 2 : a.M <= 4 ? 4 : a.M <= 8 ? 8 : 16;
-  if(!ws || !kt_al(ws, 16) || (long long)((a.M + mt - 1) / mt) * a.ntiles > KT_WS_COUNTERS) return KT_INVALID;
-  a.counters = (int*)ws;
-  a.parts = (float*)((uint8_t*)ws + KT_WS_PARTS);
-  return 0;
-}
-
+/* bytes of a matrix's codes and scales (both layouts: 32 bytes and one fp16 per row and unit, rows padded to 8) */
+static inline size_t kt_code_bytes(int R, int NU){ return (size_t)kt_r8(R) * NU * 256; }
+static inline size_t kt_scale_bytes(int R, int NU){ return (size_t)kt_r8(R) * NU * 16; }
 static int kt_mt(int M){ return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16; }
 
+/* K slices of a decode product: a function of the step count S = ceil(units / 8) only (never of M or R), so a
+   token's result does not depend on how many tokens share the pass, and a matrix gives the same bits alone or in a
+   multi-matrix launch */
+static int kt_kslices(int NU){ const int S = kt_steps(NU); return S >= 12 ? 4 : S >= 4 ? 2 : 1; }
+
+#ifndef KT_XL_BYTES
+#define KT_XL_BYTES 98304             /* LDS budget of the staged activations */
+#endif
+#ifndef KT_MIN_BLOCKS
+#define KT_MIN_BLOCKS 1024
+#endif
+#ifndef KT_WAVES_TARGET
+#define KT_WAVES_TARGET 2048          /* waves a decode launch aims for (8 per CU) */
+#endif
+/* row groups per block: the most (with KS RGB <= KT_MAXW waves) that keeps >= KT_MIN_BLOCKS blocks; it changes no
+   number */
+static int kt_rgb(int ngroups, int ks){
+  for(int rgb = KT_MAXW / ks; rgb > 1; rgb >>= 1) if(ngroups / rgb >= KT_MIN_BLOCKS) return rgb;
+  return 1;
+}
+
+/* row groups per lane of the pipelined product: enough blocks for ~KT_WAVES_TARGET waves; it changes no number */
+static int kt_rpl(int ngroups, int ks){
+  for(int rpl = 4; rpl > 1; rpl >>= 1) if((long long)(ngroups / rpl) * ks >= KT_WAVES_TARGET) return rpl;
+  return 1;
+}
+
+template <int FMT, int MT>
+static void kt_launch_pipe(const KtGemvArgs& a, int ngroups, int npass, const int8_t* xq, const float* xs,
+                           const int* xa, int32_t* dbg, hipStream_t s){
+  const int ks = kt_kslices(a.NU), rpl = kt_rpl(ngroups, ks), uw = FMT == KT_FMT_TERN ? 128 : 32;
+  const size_t lds = (size_t)MT * a.NU * (uw + 16 + 4 + (FMT == KT_FMT_TERN ? 4 : 0)) + (size_t)ks * rpl * MT * 8 * 4;
+  const dim3 grid((ngroups + rpl - 1) / rpl, npass), block(64 * ks);
+#define KT_L2(KS, RPL) do { if(dbg) hipLaunchKernelGGL((k_gemv_pipe<FMT, MT, KS, RPL, true>), grid, block, lds, s, a, xq, xs, xa, dbg); \
+                            else hipLaunchKernelGGL((k_gemv_pipe<FMT, MT, KS, RPL, false>), grid, block, lds, s, a, xq, xs, xa, dbg); } while(0)
+#define KT_L(KS) do { if(rpl == 4) KT_L2(KS, 4); else if(rpl == 2) KT_L2(KS, 2); else KT_L2(KS, 1); } while(0)
+  if(ks == 4) KT_L(4); else if(ks == 2) KT_L(2); else KT_L(1);
+#undef KT_L
+#undef KT_L2
+}
+
+template <int FMT, int MT, bool XL>
+static void kt_launch_kr(const KtGemvArgs& a, int ngroups, int npass, const int8_t* xq, const float* xs,
+                         const int* xa, int32_t* dbg, hipStream_t s){
+  const int ks = kt_kslices(a.NU), rgb = kt_rgb(ngroups, ks), w = ks * rgb, uw = FMT == KT_FMT_TERN ? 128 : 32;
+  const size_t lds = (XL ? (size_t)MT * a.NU * (uw + 16 + 4 + (FMT == KT_FMT_TERN ? 4 : 0)) : 0)
+                     + (ks > 1 ? (size_t)w * MT * 8 * 4 : 0);
+  const dim3 grid((ngroups + rgb - 1) / rgb, npass), block(64 * w);
+#define KT_L(KS, RGB) hipLaunchKernelGGL((k_gemv<FMT, MT, KS, RGB, XL>), grid, block, lds, s, a, xq, xs, xa, dbg)
+  if(ks == 4){ if(KT_MAXW >= 8 && rgb == 2) KT_L(4, 2); else KT_L(4, 1); }
+  else if(ks == 2){ if(KT_MAXW >= 8 && rgb == 4) KT_L(2, 4); else if(rgb == 2) KT_L(2, 2); else KT_L(2, 1); }
+  else { if(KT_MAXW >= 8 && rgb == 8) KT_L(1, 8); else if(rgb == 4) KT_L(1, 4); else if(rgb == 2) KT_L(1, 2); else KT_L(1, 1); }
+#undef KT_L
+}
+
+/* up to 4 tokens a pass: activations staged in LDS (while they fit in 64 KB); more tokens: read through L1 */
 template <int FMT>
-static int kt_launch_gemv(KtGemvArgs& a, int ntiles, hipStream_t s){
-  const int mt = kt_mt(a.M), npass = (a.M + mt - 1) / mt;
-  const dim3 grid(ntiles, a.nsplit, npass), block(256);
+static int kt_launch_gemv(const KtGemvArgs& a, int ngroups, const int8_t* xq, const float* xs, const int* xa,
+                          int32_t* dbg, hipStream_t s){
+  const int mt = kt_mt(a.M), npass = (a.M + mt - 1) / mt, uw = FMT == KT_FMT_TERN ? 128 : 32;
+  const bool xl = mt <= 4 && (size_t)mt * a.NU * (uw + 24) <= KT_XL_BYTES;
   switch(mt){
-    case 1: hipLaunchKernelGGL((k_gemv<FMT, 1>), grid, block, 0, s, a, a.xq, a.xs, a.xa, a.dbg); break;
-    case 2: hipLaunchKernelGGL((k_gemv<FMT, 2>), grid, block, 0, s, a, a.xq, a.xs, a.xa, a.dbg); break;
-    case 4: hipLaunchKernelGGL((k_gemv<FMT, 4>), grid, block, 0, s, a, a.xq, a.xs, a.xa, a.dbg); break;
-    case 8: hipLaunchKernelGGL((k_gemv<FMT, 8>), grid, block, 0, s, a, a.xq, a.xs, a.xa, a.dbg); break;
-    default: hipLaunchKernelGGL((k_gemv<FMT, 16>), grid, block, 0, s, a, a.xq, a.xs, a.xa, a.dbg); break;
+    case 1: if(xl) kt_launch_pipe<FMT, 1>(a, ngroups, npass, xq, xs, xa, dbg, s);
+            else kt_launch_kr<FMT, 1, false>(a, ngroups, npass, xq, xs, xa, dbg, s); break;
+    case 2: if(xl) kt_launch_pipe<FMT, 2>(a, ngroups, npass, xq, xs, xa, dbg, s);
+            else kt_launch_kr<FMT, 2, false>(a, ngroups, npass, xq, xs, xa, dbg, s); break;
+    case 4: if(xl) kt_launch_pipe<FMT, 4>(a, ngroups, npass, xq, xs, xa, dbg, s);
+            else kt_launch_kr<FMT, 4, false>(a, ngroups, npass, xq, xs, xa, dbg, s); break;
+    case 8: kt_launch_kr<FMT, 8, false>(a, ngroups, npass, xq, xs, xa, dbg, s); break;
+    default: kt_launch_kr<FMT, 16, false>(a, ngroups, npass, xq, xs, xa, dbg, s); break;
   }
   KT_LAUNCH_CHECK();
   return 0;
+}
+
+static int kt_tern_gemv_n(int nmat, const void* const* W, const int* Rs, float* const* Ys, const int* ldys, int C,
+                          const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M, int32_t* dbg,
+                          void* stream){
+  if(M == 0) return 0;
+  if(M < 0 || C <= 0 || C % 128 || !XQ || !XS || !XA || ldq < C || ldq % 16 || !kt_al(XQ, 16)) return KT_INVALID;
+  KtGemvArgs a = {};
+  const int NG = C / 128;
+  int groups = 0;
+  for(int i = 0; i < nmat; ++i){
+    if(!W[i] || !Ys[i] || Rs[i] <= 0 || ldys[i] < Rs[i] || !kt_al(W[i], 16)) return KT_INVALID;
+    a.mat[i].codes = (const uint32_t*)W[i];
+    a.mat[i].scales = (const uint16_t*)((const uint8_t*)W[i] + kt_code_bytes(Rs[i], NG));
+    a.mat[i].y = Ys[i];
+    a.mat[i].R = Rs[i];
+    a.mat[i].ldy = ldys[i];
+    a.mat[i].rg0 = groups;
+    groups += kt_r8(Rs[i]);
+  }
+  if(dbg && nmat != 1) return KT_INVALID;
+  a.nmat = nmat;
+  a.NU = NG;
+  a.ldq = ldq;
+  a.ldxs = NG;
+  a.M = M;
+  return kt_launch_gemv<KT_FMT_TERN>(a, groups, XQ, XS, (const int*)XA, dbg, kt_stream(stream));
 }
 
 extern "C" {
@@ -80,18 +144,17 @@ const char* kt_error_string(int rc){ return hipGetErrorString((hipError_t)rc); }
 /* ------------------------------------------------------------------ ternary weights */
 size_t kt_tern_weight_bytes(int R, int C){
   if(R <= 0 || C <= 0 || C % 128) return 0;
-  const size_t Rp = (size_t)kt_rp(R), NG = (size_t)(C / 128);
-  return Rp * NG * 32 + Rp * NG * 2;
+  return kt_code_bytes(R, C / 128) + kt_scale_bytes(R, C / 128);
 }
 
 int kt_tern_pack(const uint8_t* bcodes, const uint16_t* dpm, int R, int C, void* W, void* stream){
   if(!bcodes || !dpm || !W || R <= 0 || C <= 0 || C % 128 || !kt_al(W, 16)) return KT_INVALID;
-  const int Rp = kt_rp(R), NG = C / 128;
+  const int NG = C / 128;
   uint32_t* codes = (uint32_t*)W;
-  uint16_t* scales = (uint16_t*)((uint8_t*)W + (size_t)Rp * NG * 32);
-  const long long nw = (long long)Rp * NG * 8;
+  uint16_t* scales = (uint16_t*)((uint8_t*)W + kt_code_bytes(R, NG));
+  const long long nw = (long long)kt_code_bytes(R, NG) / 4;
   hipLaunchKernelGGL(k_tern_pack, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, kt_stream(stream),
-                     bcodes, dpm, R, C, Rp, codes, scales);
+                     bcodes, dpm, R, C, codes, scales);
   KT_LAUNCH_CHECK();
   return 0;
 }
@@ -108,72 +171,27 @@ int kt_quant_q8(const float* X, int ldx, int M, int C, int per_row, int8_t* XQ, 
 }
 
 /* ------------------------------------------------------------------ decode products */
-int kt_tern_gemv_splits(int R, int C){
-  if(R <= 0 || C <= 0 || C % 128) return 0;
-  return kt_nsplit(kt_rp(R) / KT_TR, C / 128, KT_MIN_UNITS);
-}
-
-size_t kt_tern_gemv_workspace(int R, int C, int M){
-  if(R <= 0 || C <= 0 || C % 128 || M <= 0) return 0;
-  const int ntiles = kt_rp(R) / KT_TR, sp = kt_nsplit(ntiles, C / 128, KT_MIN_UNITS), mt = kt_mt(M);
-  (void)mt;
-  return kt_ws_bytes(sp, M, ntiles);
-}
-
-static int kt_tern_gemv_n(int nmat, const void* const* W, const int* Rs, float* const* Ys, const int* ldys, int C,
-                          const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M, int32_t* dbg,
-                          void* ws, void* stream){
-  if(M == 0) return 0;
-  if(M < 0 || C <= 0 || C % 128 || !XQ || !XS || !XA || ldq < C || ldq % 16 || !kt_al(XQ, 16)) return KT_INVALID;
-  KtGemvArgs a = {};
-  const int NG = C / 128;
-  int tiles = 0;
-  for(int i = 0; i < nmat; ++i){
-    if(!W[i] || !Ys[i] || Rs[i] <= 0 || ldys[i] < Rs[i] || !kt_al(W[i], 16)) return KT_INVALID;
-    const int Rp = kt_rp(Rs[i]);
-    a.mat[i].codes = (const uint32_t*)W[i];
-    a.mat[i].scales = (const uint16_t*)((const uint8_t*)W[i] + (size_t)Rp * NG * 32);
-    a.mat[i].y = Ys[i];
-    a.mat[i].R = Rs[i];
-    a.mat[i].ldy = ldys[i];
-    a.mat[i].tile0 = tiles;
-    tiles += Rp / KT_TR;
-  }
-  if(dbg && nmat != 1) return KT_INVALID;
-  a.nmat = nmat;
-  a.NU = NG;
-  a.xq = XQ; a.ldq = ldq; a.xs = XS; a.xa = (const int*)XA; a.ldxs = NG;
-  a.M = M;
-  a.dbg = dbg;
-  a.nsplit = kt_nsplit(tiles, NG, KT_MIN_UNITS);
-  a.Rtot = tiles * KT_TR;
-  a.ntiles = tiles;
-  if(kt_ws_set(a, ws)) return KT_INVALID;
-  return kt_launch_gemv<KT_FMT_TERN>(a, tiles, kt_stream(stream));
+int kt_decode_kslices(int C, int q8){
+  if(C <= 0 || C % (q8 ? 32 : 128)) return 0;
+  return kt_kslices(q8 ? C / 32 : C / 128);
 }
 
 int kt_tern_gemv(const void* W, int R, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M,
-                 float* Y, int ldy, int32_t* dbg, void* ws, void* stream){
+                 float* Y, int ldy, int32_t* dbg, void* stream){
   const void* w[1] = {W};
   const int r[1] = {R}, l[1] = {ldy};
   float* y[1] = {Y};
-  return kt_tern_gemv_n(1, w, r, y, l, C, XQ, ldq, XS, XA, M, dbg, ws, stream);
-}
-
-size_t kt_tern_gemv3_workspace(int R0, int R1, int R2, int C, int M){
-  if(C <= 0 || C % 128 || M <= 0 || R0 <= 0) return 0;
-  const int tiles = kt_rp(R0) / KT_TR + (R1 > 0 ? kt_rp(R1) / KT_TR : 0) + (R2 > 0 ? kt_rp(R2) / KT_TR : 0);
-  return kt_ws_bytes(kt_nsplit(tiles, C / 128, KT_MIN_UNITS), M, tiles);
+  return kt_tern_gemv_n(1, w, r, y, l, C, XQ, ldq, XS, XA, M, dbg, stream);
 }
 
 int kt_tern_gemv3(const void* W0, int R0, float* Y0, const void* W1, int R1, float* Y1, const void* W2, int R2,
-                  float* Y2, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M, void* ws,
+                  float* Y2, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M,
                   void* stream){
   const void* w[3] = {W0, W1, W2};
   const int r[3] = {R0, R1, R2};
   float* y[3] = {Y0, Y1, Y2};
   const int n = R1 <= 0 ? 1 : R2 <= 0 ? 2 : 3;
-  return kt_tern_gemv_n(n, w, r, y, r, C, XQ, ldq, XS, XA, M, NULL, ws, stream);
+  return kt_tern_gemv_n(n, w, r, y, r, C, XQ, ldq, XS, XA, M, NULL, stream);
 }
 
 int kt_tern_sum(const float* P, float* y, int R, int M, int sp, void* stream){
@@ -192,11 +210,11 @@ int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const f
   if(M == 0) return 0;
   if(!W || !XQ || !XS || (!Y && !Y16) || R <= 0 || M < 0 || C <= 0 || C % 128 || ldq < C || ldq % 16 || ldy < R
      || !kt_al(W, 16) || !kt_al(XQ, 16)) return KT_INVALID;
-  const int Rp = kt_rp(R), NG = C / 128, ntiles = Rp / KT_TR;
+  const int NG = C / 128;
   const uint32_t* codes = (const uint32_t*)W;
-  const uint16_t* scales = (const uint16_t*)((const uint8_t*)W + (size_t)Rp * NG * 32);
+  const uint16_t* scales = (const uint16_t*)((const uint8_t*)W + kt_code_bytes(R, NG));
   const dim3 grid((R + 127) / 128, (M + 127) / 128);
-  hipLaunchKernelGGL(k_tern_gemm, grid, dim3(256), 0, kt_stream(stream), codes, scales, R, NG, ntiles, XQ, ldq, XS, M,
+  hipLaunchKernelGGL(k_tern_gemm, grid, dim3(256), 0, kt_stream(stream), codes, scales, R, NG, XQ, ldq, XS, M,
                      Y, Y16, ldy, dbg);
   KT_LAUNCH_CHECK();
   return 0;
@@ -205,17 +223,16 @@ int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const f
 /* ------------------------------------------------------------------ q8_0 */
 size_t kt_q8_weight_bytes(int R, int C){
   if(R <= 0 || C <= 0 || C % 32) return 0;
-  const size_t Rp = (size_t)kt_rp(R), NB = (size_t)(C / 32);
-  return Rp * NB * 32 + Rp * NB * 2;
+  return kt_code_bytes(R, C / 32) + kt_scale_bytes(R, C / 32);
 }
 
 int kt_q8_pack(const uint8_t* rows, int R, int C, void* W, void* stream){
   if(!rows || !W || R <= 0 || C <= 0 || C % 32 || !kt_al(W, 16)) return KT_INVALID;
-  const int Rp = kt_rp(R), NB = C / 32;
+  const int NB = C / 32;
   uint32_t* codes = (uint32_t*)W;
-  uint16_t* scales = (uint16_t*)((uint8_t*)W + (size_t)Rp * NB * 32);
-  const long long nw = (long long)Rp * NB * 8;
-  hipLaunchKernelGGL(k_q8_pack, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, kt_stream(stream), rows, R, C, Rp,
+  uint16_t* scales = (uint16_t*)((uint8_t*)W + kt_code_bytes(R, NB));
+  const long long nw = (long long)kt_code_bytes(R, NB) / 4;
+  hipLaunchKernelGGL(k_q8_pack, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, kt_stream(stream), rows, R, C,
                      codes, scales);
   KT_LAUNCH_CHECK();
   return 0;
@@ -231,34 +248,20 @@ int kt_q8_quant(const float* X, int ldx, int M, int C, int act, int8_t* Q, int l
   return 0;
 }
 
-int kt_q8_gemv_splits(int R, int C){
-  if(R <= 0 || C <= 0 || C % 32) return 0;
-  return kt_nsplit(kt_rp(R) / KT_TR, C / 32, 4);
-}
-
-size_t kt_q8_gemv_workspace(int R, int C, int M){
-  if(R <= 0 || C <= 0 || C % 32 || M <= 0) return 0;
-  const int ntiles = kt_rp(R) / KT_TR;
-  return kt_ws_bytes(kt_nsplit(ntiles, C / 32, 4), M, ntiles);
-}
-
 int kt_q8_gemv(const void* W, int R, int C, const int8_t* Q, int ldq, const float* D, int ldd, int M, float* Y,
-               int ldy, int32_t* dbg, void* ws, void* stream){
+               int ldy, int32_t* dbg, void* stream){
   if(M == 0) return 0;
   if(!W || !Q || !D || !Y || R <= 0 || M < 0 || C <= 0 || C % 32 || ldq < C || ldq % 16 || ldd < C / 32 || ldy < R
      || !kt_al(W, 16) || !kt_al(Q, 16)) return KT_INVALID;
-  const int Rp = kt_rp(R), NB = C / 32, tiles = Rp / KT_TR;
+  const int NB = C / 32;
   KtGemvArgs a = {};
   a.mat[0].codes = (const uint32_t*)W;
-  a.mat[0].scales = (const uint16_t*)((const uint8_t*)W + (size_t)Rp * NB * 32);
-  a.mat[0].y = Y; a.mat[0].R = R; a.mat[0].ldy = ldy; a.mat[0].tile0 = 0;
+  a.mat[0].scales = (const uint16_t*)((const uint8_t*)W + kt_code_bytes(R, NB));
+  a.mat[0].y = Y; a.mat[0].R = R; a.mat[0].ldy = ldy; a.mat[0].rg0 = 0;
   a.nmat = 1; a.NU = NB;
-  a.xq = Q; a.ldq = ldq; a.xs = D; a.xa = NULL; a.ldxs = ldd;
-  a.M = M; a.dbg = dbg;
-  a.nsplit = kt_nsplit(tiles, NB, 4);
-  a.Rtot = tiles * KT_TR; a.ntiles = tiles;
-  if(kt_ws_set(a, ws)) return KT_INVALID;
-  return kt_launch_gemv<KT_FMT_Q8>(a, tiles, kt_stream(stream));
+  a.ldq = ldq; a.ldxs = ldd;
+  a.M = M;
+  return kt_launch_gemv<KT_FMT_Q8>(a, kt_r8(R), Q, D, NULL, dbg, kt_stream(stream));
 }
 
 /* ------------------------------------------------------------------ MoE */
@@ -280,8 +283,8 @@ int kt_moe_sort(const int* ids, int M, int k, int E, int* cnt, int* off, int* xr
 }
 
 int kt_q8_grouped(const void* const* Wexp, int R, int C, int E, const int* cnt, const int* off, const int* act,
-                  const int* nact, const int* xrow, int nentries, int M, const int8_t* Q, int ldq,
-                  const float* D, int ldd, float* Y, int ldy, int32_t* dbg, void* stream){
+                  const int* nact, const int* xrow, int nentries, int M, const int8_t* Q, int ldq, const float* D,
+                  int ldd, float* Y, int ldy, int32_t* dbg, void* stream){
   if(nentries == 0) return 0;
   if(!Wexp || !cnt || !off || !act || !nact || !Q || !D || !Y || R <= 0 || C <= 0 || C % 32 || E <= 0
      || nentries < 0 || M <= 0 || ldq < C || ldq % 16 || ldd < C / 32 || ldy < R || !kt_al(Q, 16))
@@ -290,16 +293,16 @@ int kt_q8_grouped(const void* const* Wexp, int R, int C, int E, const int* cnt, 
   a.wexp = (const uint8_t* const*)Wexp;
   a.R = R; a.C = C; a.NU = C / 32;
   a.cnt = cnt; a.off = off; a.act = act; a.nact = nact; a.xrow = xrow;
-  a.xq = Q; a.ldq = ldq; a.xd = D; a.ldd = ldd; a.y = Y; a.ldy = ldy; a.dbg = dbg;
+  a.ldq = ldq; a.ldd = ldd; a.ldy = ldy;
   const int mt = M <= 1 ? 1 : M <= 4 ? 4 : M <= 8 ? 8 : 16;    /* an expert's list holds at most M tokens */
   const int ny = E < nentries ? E : nentries;
-  const dim3 grid(kt_rp(R) / KT_TR, ny), block(256);
+  const dim3 grid(kt_r8(R), ny), block(64);
   hipStream_t s = kt_stream(stream);
   switch(mt){
-    case 1: hipLaunchKernelGGL(k_q8_grouped<1>, grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL(k_q8_grouped<4>, grid, block, 0, s, a); break;
-    case 8: hipLaunchKernelGGL(k_q8_grouped<8>, grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL(k_q8_grouped<16>, grid, block, 0, s, a); break;
+    case 1: hipLaunchKernelGGL(k_q8_grouped<1>, grid, block, 0, s, a, Q, D, Y, dbg); break;
+    case 4: hipLaunchKernelGGL(k_q8_grouped<4>, grid, block, 0, s, a, Q, D, Y, dbg); break;
+    case 8: hipLaunchKernelGGL(k_q8_grouped<8>, grid, block, 0, s, a, Q, D, Y, dbg); break;
+    default: hipLaunchKernelGGL(k_q8_grouped<16>, grid, block, 0, s, a, Q, D, Y, dbg); break;
   }
   KT_LAUNCH_CHECK();
   return 0;

@@ -8,7 +8,7 @@
                     active experts in ascending order. Entries of one expert are in ascending flat index t k + j
                     (stable), so the lists are deterministic.
      k_q8_grouped   per active expert, its list's tokens against its q8_0 rows (kq8 layout), MT tokens per pass;
-                    output row = list entry. Same unit arithmetic as the dense q8_0 decode product.
+                    output row = list entry. The dense q8_0 decode product's lanes, arithmetic and summation tree.
      k_moe_combine  x[t] += sum_j fmaf(gw[t k + j], yd[where[t k + j]], .) (+ ysh[t]).
 */
 #include "kt_common.h"
@@ -86,20 +86,21 @@ extern "C" __global__ void __launch_bounds__(1024) k_moe_sort(const int* __restr
   }
 }
 
-/* grid (ntiles, min(E, entries)), block 256: block y = active expert y; its list's tokens in passes of MT (the
-   expert's rows are re-read from L2 per pass). 4 waves take K slices of the rows, added in wave order. */
+/* grid (row groups, min(E, entries)), block 64: wave (rg, y) takes active expert y's 8 rows rg for its whole list,
+   MT tokens a pass (the rows are re-read from L2 for each further pass). Lanes as the dense decode product
+   (k_gemv): lane 8 c + r takes units c, c + 8, ... of row r; the 8 k-lanes of a row are added by the same xor
+   butterfly. Output row = list entry. */
 template <int MT>
-__global__ void __launch_bounds__(256) k_q8_grouped(const KtGroupedArgs a){
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, tile = blockIdx.x;
+__global__ void __launch_bounds__(64) k_q8_grouped(const KtGroupedArgs a, const int8_t* __restrict__ xq,
+                                                   const float* __restrict__ xd, float* __restrict__ y,
+                                                   int32_t* __restrict__ dbg){
+  const int lane = threadIdx.x, r = lane & 7, c = lane >> 3, rg = blockIdx.x;
   if((int)blockIdx.y >= *a.nact) return;
   const int e = a.act[blockIdx.y], ce = a.cnt[e], oe = a.off[e];
-  const int row = tile * KT_TR + lane, NU = a.NU;
-  const int Rp = (a.R + KT_TR - 1) / KT_TR * KT_TR;
+  const int row = rg * KT_RG + r, NU = a.NU, S = kt_steps(NU), R8 = kt_r8(a.R);
   const uint8_t* base = a.wexp[e];
-  const uint4* __restrict__ wp = (const uint4*)base + (long long)tile * NU * 128 + lane;
-  const uint16_t* __restrict__ sc = (const uint16_t*)(base + (long long)Rp * a.C) + (long long)tile * NU * 64 + lane;
-  const int w0 = (int)((long long)wv * NU / KT_WAVES), w1 = (int)((long long)(wv + 1) * NU / KT_WAVES);
-  __shared__ float red[KT_WAVES][MT][KT_TR];
+  const uint4* __restrict__ wb = (const uint4*)base;
+  const uint16_t* __restrict__ sb = (const uint16_t*)(base + (long long)R8 * NU * 256);
 
   for(int t0 = 0; t0 < ce; t0 += MT){
     const int nt = min(MT, ce - t0);
@@ -112,39 +113,53 @@ __global__ void __launch_bounds__(256) k_q8_grouped(const KtGroupedArgs a){
     float acc[MT];
 #pragma unroll
     for(int t = 0; t < MT; ++t) acc[t] = 0.0f;
-    for(int u = w0; u < w1; ++u){
-      const uint4 c0 = wp[(long long)u * 128];
-      const uint4 c1 = wp[(long long)u * 128 + 64];
-      const float d = kt_h2f(sc[(long long)u * 64]);
-      const int w[8] = {(int)c0.x, (int)c0.y, (int)c0.z, (int)c0.w, (int)c1.x, (int)c1.y, (int)c1.z, (int)c1.w};
+    for(int s0 = 0; s0 < S; s0 += KT_UB){
+      uint4 c0[KT_UB], c1[KT_UB];
+      uint16_t hs[KT_UB];
 #pragma unroll
-      for(int t = 0; t < MT; ++t){
-        if(t < nt){
-          const int* __restrict__ x = (const int*)(a.xq + (long long)xr[t] * a.ldq) + u * 8;
-          int v = 0;
+      for(int k = 0; k < KT_UB; ++k){
+        const int u = (s0 + k) * KT_KL + c;
+        if(s0 + k < S && u < NU){
+          c0[k] = wb[kt_widx(NU, rg, s0 + k, 0, c, r)];
+          c1[k] = wb[kt_widx(NU, rg, s0 + k, 1, c, r)];
+          hs[k] = sb[kt_sidx(NU, rg, u, r)];
+        }
+      }
 #pragma unroll
-          for(int j = 0; j < 8; ++j) v = kt_dot4(w[j], x[j], v);
-          acc[t] = fmaf((float)v, d * a.xd[(long long)xr[t] * a.ldd + u], acc[t]);
-          if(a.dbg && row < a.R) a.dbg[((long long)(oe + t0 + t) * a.R + row) * NU + u] = v;
+      for(int k = 0; k < KT_UB; ++k){
+        const int u = (s0 + k) * KT_KL + c;
+        if(s0 + k < S && u < NU){
+          const float d = kt_h2f(hs[k]);
+          const int w[8] = {(int)c0[k].x, (int)c0[k].y, (int)c0[k].z, (int)c0[k].w,
+                            (int)c1[k].x, (int)c1[k].y, (int)c1[k].z, (int)c1[k].w};
+#pragma unroll
+          for(int t = 0; t < MT; ++t){
+            if(t < nt){
+              const uint4* q = (const uint4*)(xq + (long long)xr[t] * a.ldq + (long long)u * 32);
+              const uint4 q0 = q[0], q1 = q[1];
+              int v = kt_dot4(w[0], (int)q0.x, 0);
+              v = kt_dot4(w[1], (int)q0.y, v); v = kt_dot4(w[2], (int)q0.z, v); v = kt_dot4(w[3], (int)q0.w, v);
+              v = kt_dot4(w[4], (int)q1.x, v); v = kt_dot4(w[5], (int)q1.y, v); v = kt_dot4(w[6], (int)q1.z, v);
+              v = kt_dot4(w[7], (int)q1.w, v);
+              acc[t] = fmaf((float)v, d * xd[(long long)xr[t] * a.ldd + u], acc[t]);
+              if(dbg && row < a.R) dbg[((long long)(oe + t0 + t) * a.R + row) * NU + u] = v;
+            }
+          }
         }
       }
     }
-    __syncthreads();                                         /* the previous pass's sums are read */
 #pragma unroll
-    for(int t = 0; t < MT; ++t) red[wv][t][lane] = acc[t];
-    __syncthreads();
-    if(wv == 0 && row < a.R){
-#pragma unroll
-      for(int t = 0; t < MT; ++t)
-        if(t < nt)
-          a.y[(long long)(oe + t0 + t) * a.ldy + row] = ((red[0][t][lane] + red[1][t][lane]) + red[2][t][lane]) + red[3][t][lane];
+    for(int t = 0; t < MT; ++t){
+      float v = acc[t];
+      v += __shfl_xor(v, 8);
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      if(c == 0 && t < nt && row < a.R) y[(long long)(oe + t0 + t) * a.ldy + row] = v;
     }
   }
 }
-template __global__ void k_q8_grouped<1>(const KtGroupedArgs);
-template __global__ void k_q8_grouped<4>(const KtGroupedArgs);
-template __global__ void k_q8_grouped<8>(const KtGroupedArgs);
-template __global__ void k_q8_grouped<16>(const KtGroupedArgs);
+#define KT_GINST(MT) template __global__ void k_q8_grouped<MT>(const KtGroupedArgs, const int8_t*, const float*, float*, int32_t*);
+KT_GINST(1) KT_GINST(4) KT_GINST(8) KT_GINST(16)
 
 extern "C" __global__ void __launch_bounds__(256) k_moe_combine(const float* __restrict__ yd, const float* __restrict__ ysh,
     const int* __restrict__ where, const float* __restrict__ gw, int k, int cols, float* __restrict__ x){

@@ -5,7 +5,7 @@
 
    Block: 256 threads (4 waves) own 128 tokens x 128 weight rows; wave (wt, wr) owns tokens 64 wt .., rows 64 wr ..
    as 2 x 2 MFMA tiles of 32 x 32. Per group: the block loads the 128 rows' packed trits (4 KB: one 16-byte load
-   per thread, straight from the kt2 layout), unpacks them to signed int8 once (shift, mask, v_perm byte lookup)
+   per thread, 32 lines of 128 bytes of the kt2 layout), unpacks them to signed int8 once (shift, mask, v_perm byte lookup)
    into LDS, stages the 128 tokens' int8 activations in LDS, and each wave runs 4 k-steps of 2 x 2 MFMAs. The
    MFMA A operand is the activations (rows = tokens), B the weights (columns = weight rows), so a lane's 16
    accumulators share one weight row: its group scale is one register. After the group the int32 accumulators are
@@ -27,7 +27,7 @@ typedef int kt_v16i __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ uint32_t kt_trits(uint32_t dig){ return __builtin_amdgcn_perm(0x000100FFu, 0x000100FFu, dig); }
 
 extern "C" __global__ void __launch_bounds__(256) k_tern_gemm(const uint32_t* __restrict__ codes,
-    const uint16_t* __restrict__ scales, int R, int NG, int ntiles, const int8_t* __restrict__ XQ, int ldq,
+    const uint16_t* __restrict__ scales, int R, int NG, const int8_t* __restrict__ XQ, int ldq,
     const float* __restrict__ XS, int M, float* __restrict__ Y, uint16_t* __restrict__ Y16, int ldy,
     int32_t* __restrict__ dbg){
   __shared__ __attribute__((aligned(16))) uint8_t Xl[PF_BT * PF_LD];
@@ -37,12 +37,14 @@ extern "C" __global__ void __launch_bounds__(256) k_tern_gemm(const uint32_t* __
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wt = wv >> 1, wr = wv & 1;
   const int r0 = blockIdx.x * PF_BR, n0 = blockIdx.y * PF_BT;
 
-  /* this thread's weight chunk: tile (r0/64 + tid/128), half (tid/64)&1, lane tid&63 */
-  const int ltile = tid >> 7, lh = (tid >> 6) & 1, ll = tid & 63;
-  const int gtile = (r0 >> 6) + ltile;
-  const bool wvalid = gtile < ntiles;
-  const uint4* __restrict__ wsrc = (const uint4*)codes + (long long)gtile * NG * 128 + lh * 64 + ll;
-  uint8_t* wdst = Wl + (ltile * 64 + ll) * PF_LD + lh * 64;
+  const int R8 = kt_r8(R);
+  /* this thread's weight chunk: row group r0/8 + (tid >> 4), half (tid >> 3) & 1, row tid & 7 (16 bytes = 64
+     columns of one row); a unit's 128 rows are 32 chunks of 128 contiguous bytes */
+  const int lrg = tid >> 4, lh = (tid >> 3) & 1, lr = tid & 7;
+  const int grg = (r0 >> 3) + lrg;
+  const bool wvalid = grg < R8;
+  const uint4* __restrict__ wsrc = (const uint4*)codes;
+  uint8_t* wdst = Wl + (lrg * 8 + lr) * PF_LD + lh * 64;
 
   /* this thread's activation chunk: token tid/2, 64 bytes at (tid&1)*64 */
   const int xt = tid >> 1, xh = tid & 1;
@@ -52,9 +54,8 @@ extern "C" __global__ void __launch_bounds__(256) k_tern_gemm(const uint32_t* __
 
   /* scales of this lane's two weight rows (columns of the 2 B tiles) */
   const int cr0 = r0 + wr * 64 + (lane & 31), cr1 = cr0 + 32;
-  const uint16_t* __restrict__ s0p = scales + (long long)(cr0 >> 6) * NG * 64 + (cr0 & 63);
-  const uint16_t* __restrict__ s1p = scales + (long long)(cr1 >> 6) * NG * 64 + (cr1 & 63);
-  const bool c0v = (cr0 >> 6) < ntiles, c1v = (cr1 >> 6) < ntiles;
+  const int crg0 = cr0 >> 3, crg1 = cr1 >> 3;
+  const bool c0v = (cr0 >> 3) < R8, c1v = (cr1 >> 3) < R8;
 
   float acc[2][2][16];
 #pragma unroll
@@ -67,12 +68,12 @@ extern "C" __global__ void __launch_bounds__(256) k_tern_gemm(const uint32_t* __
   for(int g = 0; g < NG; ++g){
     /* global -> registers */
     uint4 wc = make_uint4(0x55555555u, 0x55555555u, 0x55555555u, 0x55555555u);
-    if(wvalid) wc = kt_ldnt(wsrc + (long long)g * 128);
+    if(wvalid) wc = kt_ldnt(wsrc + kt_widx(NG, grg, g >> 3, lh, g & 7, lr));   /* step g / 8, k-lane g % 8 */
     uint4 xv[4];
 #pragma unroll
     for(int k = 0; k < 4; ++k) xv[k] = xvalid ? ((const uint4*)(xsrc + g * 128))[k] : make_uint4(0u, 0u, 0u, 0u);
-    const float d0 = c0v ? kt_h2f(s0p[(long long)g * 64]) : 0.0f;
-    const float d1 = c1v ? kt_h2f(s1p[(long long)g * 64]) : 0.0f;
+    const float d0 = c0v ? kt_h2f(scales[kt_sidx(NG, crg0, g, cr0 & 7)]) : 0.0f;
+    const float d1 = c1v ? kt_h2f(scales[kt_sidx(NG, crg1, g, cr1 & 7)]) : 0.0f;
 
     __syncthreads();                                          /* the previous group's operands are consumed */
     /* unpack: word j of the chunk = columns 16j .. +15 of the half; slot s = columns 16j + 4s .. +3 */

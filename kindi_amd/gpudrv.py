@@ -23,19 +23,15 @@ SIGNATURES = [
     ("kt_tern_weight_bytes", S, [I, I]),
     ("kt_tern_pack", I, [P, P, I, I, P, P]),
     ("kt_quant_q8", I, [P, I, I, I, I, P, I, P, P, P]),
-    ("kt_tern_gemv_splits", I, [I, I]),
-    ("kt_tern_gemv_workspace", S, [I, I, I]),
-    ("kt_tern_gemv", I, [P, I, I, P, I, P, P, I, P, I, P, P, P]),
-    ("kt_tern_gemv3_workspace", S, [I, I, I, I, I]),
-    ("kt_tern_gemv3", I, [P, I, P, P, I, P, P, I, P, I, P, I, P, P, I, P, P]),
+    ("kt_decode_kslices", I, [I, I]),
+    ("kt_tern_gemv", I, [P, I, I, P, I, P, P, I, P, I, P, P]),
+    ("kt_tern_gemv3", I, [P, I, P, P, I, P, P, I, P, I, P, I, P, P, I, P]),
     ("kt_tern_sum", I, [P, P, I, I, I, P]),
     ("kt_tern_gemm", I, [P, I, I, P, I, P, P, I, P, P, I, P, P]),
     ("kt_q8_weight_bytes", S, [I, I]),
     ("kt_q8_pack", I, [P, I, I, P, P]),
     ("kt_q8_quant", I, [P, I, I, I, I, P, I, P, I, P]),
-    ("kt_q8_gemv_splits", I, [I, I]),
-    ("kt_q8_gemv_workspace", S, [I, I, I]),
-    ("kt_q8_gemv", I, [P, I, I, P, I, P, I, I, P, I, P, P, P]),
+    ("kt_q8_gemv", I, [P, I, I, P, I, P, I, I, P, I, P, P]),
     ("kt_moe_topk", I, [P, I, I, I, P, P, P]),
     ("kt_moe_sort", I, [P, I, I, I, P, P, P, P, P, P, P]),
     ("kt_q8_grouped", I, [P, I, I, I, P, P, P, P, P, I, I, P, I, P, I, P, I, P, P]),

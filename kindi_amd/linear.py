@@ -85,34 +85,18 @@ def quantize(X, per_row=False, out=None):
     return Act(out.XQ, out.XS, out.XA, M, C, per_row)
 
 
-class Workspace(object):
-    """zero-filled scratch for the K-split reductions, grown on demand (the kernels leave it zeroed)"""
-
-    def __init__(self, device="cuda"):
-        self.device = device
-        self.buf = None
-
-    def get(self, nbytes):
-        if nbytes == 0:
-            return None
-        if self.buf is None or self.buf.numel() < nbytes:
-            self.buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
-        return self.buf
-
-
 class Linear(object):
     """The ternary tensors of a model and the products over them (Kindi's linear-call surface).
 
     decode_max: up to this many tokens a product runs on the wave64 bandwidth kernel (kt_tern_gemv), above it on
-    the matrix cores (kt_tern_gemm). Each kernel's split is fixed per shape, so within one kernel a token's result
-    does not depend on how many tokens share the pass (tc_hip.cu:14-15)."""
+    the matrix cores (kt_tern_gemm). Within one kernel a token's result does not depend on how many tokens share
+    the pass (tc_hip.cu:14-15)."""
 
     def __init__(self, mats=None, device="cuda", decode_max=16, per_row=False):
         self.w = dict(mats or {})
         self.device = device
         self.decode_max = decode_max
         self.per_row = per_row
-        self.ws = Workspace(device)
 
     def add(self, name, mat):
         self.w[name] = mat
@@ -132,23 +116,21 @@ class Linear(object):
             if o.dtype != torch.float32 or o.shape[-1] != m.R or o.numel() < act.M * m.R or not o.is_contiguous():
                 raise ValueError("output for %d rows x %d tokens" % (m.R, act.M))
         if len(ms) == 1:
-            ws = self.ws.get(lib.kt_tern_gemv_workspace(ms[0].R, C, act.M))
             rc = lib.kt_tern_gemv(ptr(ms[0].W), ms[0].R, C, ptr(act.XQ), act.XQ.stride(0), ptr(act.XS), ptr(act.XA),
-                                  act.M, ptr(outs[0]), ms[0].R, ptr(dbg), ptr(ws), stream())
+                                  act.M, ptr(outs[0]), ms[0].R, ptr(dbg), stream())
             return gpudrv.check(rc, "kt_tern_gemv") or 1
         if dbg is not None:
             raise ValueError("dbg takes a single tensor")
         Rs = [m.R for m in ms] + [0] * (3 - len(ms))
         Ws = [ptr(m.W) for m in ms] + [None] * (3 - len(ms))
         Ys = [ptr(o) for o in outs] + [None] * (3 - len(ms))
-        ws = self.ws.get(lib.kt_tern_gemv3_workspace(Rs[0], Rs[1], Rs[2], C, act.M))
         rc = lib.kt_tern_gemv3(Ws[0], Rs[0], Ys[0], Ws[1], Rs[1], Ys[1], Ws[2], Rs[2], Ys[2], C, ptr(act.XQ),
-                               act.XQ.stride(0), ptr(act.XS), ptr(act.XA), act.M, ptr(ws), stream())
+                               act.XQ.stride(0), ptr(act.XS), ptr(act.XA), act.M, stream())
         return gpudrv.check(rc, "kt_tern_gemv3") or 1
 
     def gemv(self, names, x, outs, parts_ok=False):
         """Engine.gemv (engine.py:254-274): up to three ternary tensors with the same fp32 input x ([C] or [M, C]).
-        The input is quantized once (the int8 path); the K-split parts are added inside the launch, so the part
+        The input is quantized once (the int8 path); every row's sum is completed inside the launch, so the part
         count returned is always 1 (parts_ok is accepted for the reference's signature)."""
         act = quantize(x, self.per_row)
         outs = [o.reshape(act.M, -1) for o in outs]

@@ -12,7 +12,7 @@ import numpy as np
 import torch
 
 from . import gpudrv
-from .linear import ptr, stream, _dev_u8, Workspace
+from .linear import ptr, stream, _dev_u8
 
 
 def q8_quantize(X, act=0, Q=None, D=None):
@@ -41,7 +41,6 @@ class Q8Matrix(object):
             raise ValueError("q8_0 rows do not match %d x %d" % (R, C))
         self.W = torch.empty(nbytes, dtype=torch.uint8, device=device) if W is None else W
         gpudrv.check(lib.kt_q8_pack(ptr(src), self.R, self.C, ptr(self.W), stream()), "kt_q8_pack")
-        self.ws = Workspace(device)
 
     def gemv(self, Q, D, Y=None, dbg=None):
         """Y [M, R] = W x for the quantized rows (Q, D)"""
@@ -49,9 +48,8 @@ class Q8Matrix(object):
         M = Q.shape[0]
         if Y is None:
             Y = torch.empty((M, self.R), dtype=torch.float32, device=Q.device)
-        ws = self.ws.get(lib.kt_q8_gemv_workspace(self.R, self.C, M))
         rc = lib.kt_q8_gemv(ptr(self.W), self.R, self.C, ptr(Q), Q.stride(0), ptr(D), D.stride(0), M, ptr(Y),
-                            Y.stride(0), ptr(dbg), ptr(ws), stream())
+                            Y.stride(0), ptr(dbg), stream())
         gpudrv.check(rc, "kt_q8_gemv")
         return Y
 

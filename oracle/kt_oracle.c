@@ -171,6 +171,43 @@ void or_out_tree(const int32_t* acc, const float* XS, int ldxs, const float* dq,
   free(d);
 }
 
+/* The decode products' order: the K units of a row are taken KL at a time (steps), the steps split into KS
+   contiguous slices (slice k = steps [k S / KS, (k + 1) S / KS)); in a slice, lane c chains fmaf over its units
+   st KL + c in increasing step order, the KL lane sums are added by an xor butterfly (level k adds the lanes c and
+   c ^ 2^k; KL = 8: ((l0 + l1) + (l2 + l3)) + ((l4 + l5) + (l6 + l7))), and the slice sums are added left to right.
+   fmt and dq as or_out_tree. */
+void or_out_lanes(const int32_t* acc, const float* XS, int ldxs, const float* dq, int R, int NU, int M, int KL, int KS,
+                  int fmt, float* Y, int ldy){
+  float* d = (float*)malloc((size_t)NU * sizeof(float));
+  float lane[64], nxt[64];
+  for(int n = 0; n < M; ++n)
+    for(int r = 0; r < R; ++r){
+      for(int u = 0; u < NU; ++u) d[u] = dq[(size_t)u * R + r];
+      const int32_t* v = acc + ((size_t)n * R + r) * NU;
+      const float* xs = XS + (size_t)n * ldxs;
+      const int S = (NU + KL - 1) / KL;
+      float y = 0.0f;
+      for(int k = 0; k < KS; ++k){
+        const int s0 = k * S / KS, s1 = (k + 1) * S / KS;
+        for(int c = 0; c < KL; ++c){
+          float s = 0.0f;
+          for(int st = s0; st < s1; ++st){
+            const int u = st * KL + c;
+            if(u < NU) s = fmaf((float)v[u], fmt == 0 ? xs[u] * d[u] : d[u] * xs[u], s);
+          }
+          lane[c] = s;
+        }
+        for(int st = 1; st < KL; st *= 2){
+          for(int c = 0; c < KL; ++c) nxt[c] = lane[c] + lane[c ^ st];
+          for(int c = 0; c < KL; ++c) lane[c] = nxt[c];
+        }
+        y = k == 0 ? lane[0] : y + lane[0];
+      }
+      Y[(size_t)n * ldy + r] = y;
+    }
+  free(d);
+}
+
 /* k_tc_sum (tc_hip.cu:271-279): y[n][r] = sum over parts p = 0 .. sp-1 of P[(n sp + p) R + r], in part order */
 void or_tern_sum(const float* P, float* y, int R, int M, int sp){
   for(int n = 0; n < M; ++n)

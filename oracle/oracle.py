@@ -50,6 +50,7 @@ def lib():
         h.or_tern_out.argtypes = [P, P, P, I, I, I, P, I]
         h.or_tern_sum.argtypes = [P, P, I, I, I]
         h.or_out_tree.argtypes = [P, P, I, P, I, I, I, I, I, I, P, I]
+        h.or_out_lanes.argtypes = [P, P, I, P, I, I, I, I, I, I, P, I]
         h.or_pair_gemv.argtypes = [P, P, I, I, P, P, P]
         h.or_paircodes.argtypes = [P, I, I, P]
         h.or_q8_quant.argtypes = [P, I, P, P]
@@ -225,6 +226,18 @@ def out_tree(acc, XS, dq, nsplit, nwave, fmt):
     XS = _c(XS, np.float32)
     Y = np.empty((M, R), np.float32)
     lib().or_out_tree(_p(acc), _p(XS), XS.shape[1], _p(_c(dq, np.float32)), R, NU, M, nsplit, nwave, fmt, _p(Y), R)
+    return Y
+
+
+def out_lanes(acc, XS, dq, KL, fmt, KS=1):
+    """Y [M, R] from exact unit values in the decode products' order: KS slices of steps of KL units; in a slice
+    units dealt to KL lanes (strided fma chains), the lanes added by an xor butterfly, slices left to right.
+    fmt 0 ternary, 1 q8_0; XS [M, NU]; dq [NU, R] fp32 weight scales"""
+    acc = _c(acc, np.int32)
+    M, R, NU = acc.shape
+    XS = _c(XS, np.float32)
+    Y = np.empty((M, R), np.float32)
+    lib().or_out_lanes(_p(acc), _p(XS), XS.shape[1], _p(_c(dq, np.float32)), R, NU, M, KL, KS, fmt, _p(Y), R)
     return Y
 
 

@@ -27,7 +27,7 @@ def lib():
 
 def test_exports_every_declared_symbol(lib):
     names = declared()
-    assert len(names) >= 20
+    assert len(names) == 19
     for n in names:
         assert hasattr(lib, n), n
     from kindi_amd import gpudrv
@@ -36,22 +36,21 @@ def test_exports_every_declared_symbol(lib):
 
 def test_version_and_sizes(lib):
     assert lib.kt_version() == 1
-    # kt2: 2 bits + fp16 per 128 (2.125 b/w), rows padded to 64
+    # kt2: 32 bytes of codes + one fp16 per row and 128-column group (2.125 b/w), rows padded to 8
     assert lib.kt_tern_weight_bytes(6144, 2048) == 6144 * 2048 // 4 + 6144 * 16 * 2
-    assert lib.kt_tern_weight_bytes(100, 256) == 128 * 256 // 4 + 128 * 2 * 2
+    assert lib.kt_tern_weight_bytes(100, 256) == 104 * 2 * 34
     assert lib.kt_tern_weight_bytes(64, 100) == 0
-    # kq8: 34 bytes per 32
+    # kq8: 34 bytes per 32 columns, no padding along K (1856 rows = 232 row groups)
     assert lib.kt_q8_weight_bytes(1856, 2688) == 1856 * 2688 // 32 * 34
+    assert lib.kt_q8_weight_bytes(2688, 1856) == 2688 * 1856 // 32 * 34
     assert lib.kt_q8_weight_bytes(64, 48) == 0
 
 
-def test_split_plan_is_shape_only(lib):
-    for R, C in ((6144, 2048), (1024, 5120), (5120, 17408), (17408, 5120)):
-        sp = lib.kt_tern_gemv_splits(R, C)
-        assert sp >= 1 and C // 128 // sp >= 4 * 2 or sp == 1
-        for M in (1, 4, 16):
-            ws = lib.kt_tern_gemv_workspace(R, C, M)
-            assert (ws == 0) == (sp == 1)
+def test_decode_kslices(lib):
+    """the K-slice count of the decode order depends on the width only"""
+    assert [lib.kt_decode_kslices(C, 0) for C in (128, 2048, 4096, 5120, 12288, 17408)] == [1, 1, 2, 2, 4, 4]
+    assert [lib.kt_decode_kslices(C, 1) for C in (1856, 2688)] == [2, 2]
+    assert lib.kt_decode_kslices(100, 0) == 0
 
 
 def test_validation_rejects_bad_shapes(lib):
@@ -60,17 +59,16 @@ def test_validation_rejects_bad_shapes(lib):
     assert lib.kt_tern_pack(fake, fake, 64, 100, fake, None) == INVALID
     assert lib.kt_quant_q8(fake, 100, 1, 100, 0, fake, 112, fake, fake, None) == INVALID
     # ldq not a multiple of 16
-    assert lib.kt_tern_gemv(fake, 64, 256, fake, 260, fake, fake, 1, fake, 64, None, None, None) == INVALID
+    assert lib.kt_tern_gemv(fake, 64, 256, fake, 260, fake, fake, 1, fake, 64, None, None) == INVALID
+    # ldy < R
+    assert lib.kt_tern_gemv(fake, 64, 256, fake, 256, fake, fake, 1, fake, 63, None, None) == INVALID
     # null output
     assert lib.kt_tern_gemm(fake, 64, 256, fake, 256, fake, fake, 4, None, None, 64, None, None) == INVALID
     # q8: C % 32
-    assert lib.kt_q8_gemv(fake, 64, 48, fake, 48, fake, 1, 1, fake, 64, None, None, None) == INVALID
+    assert lib.kt_q8_gemv(fake, 64, 48, fake, 48, fake, 1, 1, fake, 64, None, None) == INVALID
     # moe: k > 16, E > 1024
     assert lib.kt_moe_topk(fake, 1, 128, 17, fake, fake, None) == INVALID
     assert lib.kt_moe_sort(fake, 1, 6, 2048, fake, fake, fake, fake, fake, fake, None) == INVALID
     # M = 0: a no-op
-    assert lib.kt_tern_gemv(fake, 64, 256, fake, 256, fake, fake, 0, fake, 64, None, None, None) == 0
-    # a split product without its workspace
-    R, C = 1024, 5120
-    assert lib.kt_tern_gemv_splits(R, C) > 1
-    assert lib.kt_tern_gemv(fake, R, C, fake, C, fake, fake, 1, fake, R, None, None, None) == INVALID
+    assert lib.kt_tern_gemv(fake, 64, 256, fake, 256, fake, fake, 0, fake, 64, None, None) == 0
+    # dbg with several matrices in one launch

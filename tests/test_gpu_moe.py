@@ -46,7 +46,7 @@ def test_q8_gemv(kt, R, C, M):
     acc = orc.q8_acc(rows, R, C, q)
     assert np.array_equal(host(dbg), acc)
     dq = np.ascontiguousarray(sc.view(np.float16).astype(np.float32).T)
-    tree = orc.out_tree(acc, d, dq, lib.kt_q8_gemv_splits(R, C), 4, 1)
+    tree = orc.out_lanes(acc, d, dq, 8, 1, lib.kt_decode_kslices(C, 1))
     y = host(Y)
     assert np.array_equal(y, tree)
     assert max_rel(y, orc.q8_out(acc, rows, R, C, d)) < TOL
@@ -151,7 +151,7 @@ def test_moe_forward_config4(kt, M):
     assert np.array_equal(host(dbg)[p], acc)
     dq = np.ascontiguousarray(up_rows[e].reshape(F, H // 32, 34)[:, :, :2].copy().view(np.float16)[..., 0]
                               .astype(np.float32).T)
-    assert np.array_equal(host(Y)[p], orc.out_tree(acc, d[xrow[p]], dq, 1, 4, 1))
+    assert np.array_equal(host(Y)[p], orc.out_lanes(acc, d[xrow[p]], dq, 8, 1, 1))   # one K slice per wave
 
 
 def test_combine_bit_exact(kt):

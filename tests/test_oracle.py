@@ -190,7 +190,7 @@ def test_out_tree_cases(orc):
     for sp, nw in ((2, 4), (3, 4), (1, 4), (5, 1)):
         T = orc.out_tree(acc, XS, dq, sp, nw, 0)
         assert np.allclose(T, Y, rtol=1e-5, atol=1e-6 * np.abs(Y).max())
-    # a hand-summed tree: 16 groups, 2 splits x 4 slices of 2 groups
+    # a hand-summed tree: 16 groups, 2 ranges x 4 slices of 2 groups
     v = acc[0, 3].astype(np.float64)
     s = (XS[0] * dq[:, 3]).astype(np.float32).astype(np.float64)
 
@@ -201,6 +201,28 @@ def test_out_tree_cases(orc):
     q0 = np.float32(np.float32(np.float32(ch[0] + ch[1]) + ch[2]) + ch[3])
     q1 = np.float32(np.float32(np.float32(ch[4] + ch[5]) + ch[6]) + ch[7])
     assert orc.out_tree(acc, XS, dq, 2, 4, 0)[0, 3] == np.float32(q0 + q1)
+
+
+def test_out_lanes_tree(orc):
+    """the decode order: with one lane it is the sequential chain; with 8 lanes a hand-built butterfly"""
+    R, C, M = 16, 2048, 2
+    dig = rand_digits(R, C, 44)
+    dpm = rand_scales((C // 128, R), 45)
+    X = rng(46).normal(0, 1, (M, C)).astype(np.float32)
+    Y, acc, (Q, XS, XA) = orc.tern_linear(orc.pack_from_digits(dig), dpm, R, C, X)
+    dq = dpm.view(np.float16).astype(np.float32)
+    assert np.array_equal(orc.out_lanes(acc, XS, dq, 1, 0), Y)
+    T = orc.out_lanes(acc, XS, dq, 8, 0)
+    assert np.allclose(T, Y, rtol=1e-5, atol=1e-6 * np.abs(Y).max())
+    v = acc[1, 5].astype(np.float64)
+    s = (XS[1] * dq[:, 5]).astype(np.float32).astype(np.float64)
+    lane = []
+    for c in range(8):                     # 16 groups: lane c takes c and c + 8
+        a = np.float32(v[c] * s[c])
+        lane.append(np.float32(v[c + 8] * s[c + 8] + np.float64(a)))
+    f = np.float32
+    ref = f(f(f(lane[0] + lane[1]) + f(lane[2] + lane[3])) + f(f(lane[4] + lane[5]) + f(lane[6] + lane[7])))
+    assert T[1, 5] == ref
 
 
 def test_tern_sum_order(orc):
