@@ -37,7 +37,7 @@ const char* kt_error_string(int rc);
 
 /* ---------------------------------------------------------------- ternary weights
    Device layout "kt2": 2-bit digits + fp16 scale per 128 columns, the same 2.125 bits per weight as the pack.
-   kt_tern_weight_bytes: the size of one matrix (rows padded to a multiple of 64), 0 if C % 128 != 0.
+   kt_tern_weight_bytes: the size of one matrix (rows padded to a multiple of 8), 0 if C % 128 != 0.
    kt_tern_pack: the reference pack of one tensor, unchanged (bcodes [C/4][R]: byte = d0 + 3 d1 + 9 d2 + 27 d3 of
    4 columns, convert.py:49-52, 144-159; dpm [C/128][R] fp16 bits, convert.py:155) -> W (16-byte aligned).
    Replaces layout.repack (layout.py:32-48) and spec.repack / k_tc_pack (spec.py:327-383, tc_hip.cu:31-40). */
