@@ -319,7 +319,7 @@ def main():
     run = graphed(torch, step, use_graph)
     ms = timer.run(run, a.steps, a.warmup)
     gbs = nbytes / ms / 1e6
-    # the dominant kernel (k_gemv_pipe<ternary, 1 token>) is every launch of the step; inside the graph they run
+    # the dominant kernel (k_gemv_flat<ternary, 1 token>) is every launch of the step; inside the graph they run
     # back to back, so the average launch duration is the timed region over the launch count (an upper bound:
     # it includes the gaps between launches)
     launch_ms = ms / len(calls)
@@ -338,7 +338,7 @@ def main():
                      "traffic": traffic["bytes_per_launch"] if traffic else None,
                      "traffic_source": traffic["source"] if traffic else None,
                      "algorithmic_bytes_per_launch": nbytes // len(calls),
-                     "kernel": "k_gemv_pipe<ternary,MT=1>", "launches": len(calls),
+                     "kernel": "k_gemv_flat<ternary,MT=1>", "launches": len(calls),
                      "avg_launch_us": round(launch_ms * 1e3, 3)},
     }
     if not a.quick:

@@ -55,10 +55,10 @@ int kt_quant_q8(const float* X, int ldx, int M, int C, int per_row, int8_t* XQ, 
    Y[n][ldy] = W x_n for tokens n < M. dbg (nullable): the exact group values v, int32 [M][R][C/128].
    Every output row's sum is formed inside one block in a fixed order that depends only on C (never on M or R), so
    a token's result does not depend on how many tokens share the pass. The order: the row's K units are split into
-   KS = kt_decode_kslices(C, 0) contiguous slices of whole steps (a step = 8 consecutive units; slice k = steps
-   [k S / KS, (k + 1) S / KS)); in a slice, lane c (0..7) chains fmaf over its units 8 s + c in increasing order,
-   the 8 lane sums are added by the xor butterfly ((l0 + l1) + (l2 + l3)) + ((l4 + l5) + (l6 + l7)), and the slice
-   sums are added left to right. No workspace, no second pass.
+   KS = kt_decode_kslices(C, 0) contiguous slices of whole steps (a step = 8 consecutive units, S steps; KS =
+   min(ceil(S / 2), 16); slice k = steps [k S / KS, (k + 1) S / KS)); in a slice, lane c (0..7) chains fmaf over its
+   units 8 s + c in increasing order, the 8 lane sums are added by the xor butterfly ((l0 + l1) + (l2 + l3)) +
+   ((l4 + l5) + (l6 + l7)), and the slice sums are added left to right. No workspace, no second pass.
    Replaces k_tc_mv{2,4,8} + k_tc_sum (tc_hip.cu:180-199, 236-240, 271-279; spec.py:619-657). */
 int kt_decode_kslices(int C, int q8);
 int kt_tern_gemv(const void* W, int R, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M,

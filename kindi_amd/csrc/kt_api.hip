@@ -5,10 +5,8 @@
 #include "kt_common.h"
 #include "../../include/kt.h"
 
-template <int FMT, int MT, int KS, int RGB, bool XL>
-__global__ void k_gemv(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*);
-template <int FMT, int MT, int KS, int RPL, bool DBG>
-__global__ void k_gemv_pipe(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*);
+template <int FMT, int MT, bool DBG>
+__global__ void k_gemv_flat(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
 template <int MT> __global__ void k_q8_grouped(const KtGroupedArgs, const int8_t*, const float*, float*, int32_t*);
 extern "C" __global__ void k_tern_pack(const uint8_t*, const uint16_t*, int, int, uint32_t*, uint16_t*);
 extern "C" __global__ void k_q8_pack(const uint8_t*, int, int, uint32_t*, uint16_t*);
@@ -29,79 +27,27 @@ static inline bool kt_al(const void* p, size_t a){ return ((uintptr_t)p % a) == 
 /* bytes of a matrix's codes and scales (both layouts: 32 bytes and one fp16 per row and unit, rows padded to 8) */
 static inline size_t kt_code_bytes(int R, int NU){ return (size_t)kt_r8(R) * NU * 256; }
 static inline size_t kt_scale_bytes(int R, int NU){ return (size_t)kt_r8(R) * NU * 16; }
-static int kt_mt(int M){ return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16; }
-
 /* K slices of a decode product: a function of the step count S = ceil(units / 8) only (never of M or R), so a
    token's result does not depend on how many tokens share the pass, and a matrix gives the same bits alone or in a
-   multi-matrix launch */
-static int kt_kslices(int NU){ const int S = kt_steps(NU); return S >= 12 ? 4 : S >= 4 ? 2 : 1; }
-
-#ifndef KT_XL_BYTES
-#define KT_XL_BYTES 98304             /* LDS budget of the staged activations */
-#endif
-#ifndef KT_MIN_BLOCKS
-#define KT_MIN_BLOCKS 1024
-#endif
-#ifndef KT_WAVES_TARGET
-#define KT_WAVES_TARGET 2048          /* waves a decode launch aims for (8 per CU) */
-#endif
-/* row groups per block: the most (with KS RGB <= KT_MAXW waves) that keeps >= KT_MIN_BLOCKS blocks; it changes no
-   number */
-static int kt_rgb(int ngroups, int ks){
-  for(int rgb = KT_MAXW / ks; rgb > 1; rgb >>= 1) if(ngroups / rgb >= KT_MIN_BLOCKS) return rgb;
-  return 1;
+   multi-matrix launch: slices of at most KT_SL steps, at most KT_KSMAX of them */
+static int kt_kslices(int NU){
+  const int S = kt_steps(NU), ks = (S + KT_SL - 1) / KT_SL;
+  return ks < KT_KSMAX ? ks : KT_KSMAX;
 }
 
-/* row groups per lane of the pipelined product: enough blocks for ~KT_WAVES_TARGET waves; it changes no number */
-static int kt_rpl(int ngroups, int ks){
-  for(int rpl = 4; rpl > 1; rpl >>= 1) if((long long)(ngroups / rpl) * ks >= KT_WAVES_TARGET) return rpl;
-  return 1;
-}
-
-template <int FMT, int MT>
-static void kt_launch_pipe(const KtGemvArgs& a, int ngroups, int npass, const int8_t* xq, const float* xs,
-                           const int* xa, int32_t* dbg, hipStream_t s){
-  const int ks = kt_kslices(a.NU), rpl = kt_rpl(ngroups, ks), uw = FMT == KT_FMT_TERN ? 128 : 32;
-  const size_t lds = (size_t)MT * a.NU * (uw + 16 + 4 + (FMT == KT_FMT_TERN ? 4 : 0)) + (size_t)ks * rpl * MT * 8 * 4;
-  const dim3 grid((ngroups + rpl - 1) / rpl, npass), block(64 * ks);
-#define KT_L2(KS, RPL) do { if(dbg) hipLaunchKernelGGL((k_gemv_pipe<FMT, MT, KS, RPL, true>), grid, block, lds, s, a, xq, xs, xa, dbg); \
-                            else hipLaunchKernelGGL((k_gemv_pipe<FMT, MT, KS, RPL, false>), grid, block, lds, s, a, xq, xs, xa, dbg); } while(0)
-#define KT_L(KS) do { if(rpl == 4) KT_L2(KS, 4); else if(rpl == 2) KT_L2(KS, 2); else KT_L2(KS, 1); } while(0)
-  if(ks == 4) KT_L(4); else if(ks == 2) KT_L(2); else KT_L(1);
-#undef KT_L
-#undef KT_L2
-}
-
-template <int FMT, int MT, bool XL>
-static void kt_launch_kr(const KtGemvArgs& a, int ngroups, int npass, const int8_t* xq, const float* xs,
-                         const int* xa, int32_t* dbg, hipStream_t s){
-  const int ks = kt_kslices(a.NU), rgb = kt_rgb(ngroups, ks), w = ks * rgb, uw = FMT == KT_FMT_TERN ? 128 : 32;
-  const size_t lds = (XL ? (size_t)MT * a.NU * (uw + 16 + 4 + (FMT == KT_FMT_TERN ? 4 : 0)) : 0)
-                     + (ks > 1 ? (size_t)w * MT * 8 * 4 : 0);
-  const dim3 grid((ngroups + rgb - 1) / rgb, npass), block(64 * w);
-#define KT_L(KS, RGB) hipLaunchKernelGGL((k_gemv<FMT, MT, KS, RGB, XL>), grid, block, lds, s, a, xq, xs, xa, dbg)
-  if(ks == 4){ if(KT_MAXW >= 8 && rgb == 2) KT_L(4, 2); else KT_L(4, 1); }
-  else if(ks == 2){ if(KT_MAXW >= 8 && rgb == 4) KT_L(2, 4); else if(rgb == 2) KT_L(2, 2); else KT_L(2, 1); }
-  else { if(KT_MAXW >= 8 && rgb == 8) KT_L(1, 8); else if(rgb == 4) KT_L(1, 4); else if(rgb == 2) KT_L(1, 2); else KT_L(1, 1); }
-#undef KT_L
-}
-
-/* up to 4 tokens a pass: activations staged in LDS (while they fit in 64 KB); more tokens: read through L1 */
+/* one block per row group, every token in the launch (chunks of MT tokens whose staging fits in 64 KB of LDS) */
 template <int FMT>
 static int kt_launch_gemv(const KtGemvArgs& a, int ngroups, const int8_t* xq, const float* xs, const int* xa,
                           int32_t* dbg, hipStream_t s){
-  const int mt = kt_mt(a.M), npass = (a.M + mt - 1) / mt, uw = FMT == KT_FMT_TERN ? 128 : 32;
-  const bool xl = mt <= 4 && (size_t)mt * a.NU * (uw + 24) <= KT_XL_BYTES;
-  switch(mt){
-    case 1: if(xl) kt_launch_pipe<FMT, 1>(a, ngroups, npass, xq, xs, xa, dbg, s);
-            else kt_launch_kr<FMT, 1, false>(a, ngroups, npass, xq, xs, xa, dbg, s); break;
-    case 2: if(xl) kt_launch_pipe<FMT, 2>(a, ngroups, npass, xq, xs, xa, dbg, s);
-            else kt_launch_kr<FMT, 2, false>(a, ngroups, npass, xq, xs, xa, dbg, s); break;
-    case 4: if(xl) kt_launch_pipe<FMT, 4>(a, ngroups, npass, xq, xs, xa, dbg, s);
-            else kt_launch_kr<FMT, 4, false>(a, ngroups, npass, xq, xs, xa, dbg, s); break;
-    case 8: kt_launch_kr<FMT, 8, false>(a, ngroups, npass, xq, xs, xa, dbg, s); break;
-    default: kt_launch_kr<FMT, 16, false>(a, ngroups, npass, xq, xs, xa, dbg, s); break;
-  }
+  const int ks = kt_kslices(a.NU);
+  int mt = a.M <= 1 ? 1 : a.M <= 2 ? 2 : 4;
+  while(mt > 1 && (mt == 4 ? KtFlat<FMT, 4>::lds(ks) : KtFlat<FMT, 2>::lds(ks)) > 65536) mt >>= 1;
+  const dim3 grid(ngroups), block(64 * ks);
+#define KT_F(MT) do { const size_t lds = KtFlat<FMT, MT>::lds(ks); \
+    if(dbg) hipLaunchKernelGGL((k_gemv_flat<FMT, MT, true>), grid, block, lds, s, a, xq, xs, xa, dbg, ks); \
+    else hipLaunchKernelGGL((k_gemv_flat<FMT, MT, false>), grid, block, lds, s, a, xq, xs, xa, dbg, ks); } while(0)
+  if(mt == 4) KT_F(4); else if(mt == 2) KT_F(2); else KT_F(1);
+#undef KT_F
   KT_LAUNCH_CHECK();
   return 0;
 }

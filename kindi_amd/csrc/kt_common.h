@@ -28,15 +28,24 @@
 
 #define KT_RG 8                       /* rows per row group (one decode wave) */
 #define KT_KL 8                       /* lanes along K per row = units per step */
-#ifndef KT_UB
-#define KT_UB 4                       /* steps whose weight loads a wave keeps in flight */
-#endif
-#ifndef KT_MAXW
-#define KT_MAXW 4                     /* waves per decode block */
-#endif
 #define KT_MAXMAT 3                   /* matrices sharing one input in a launch (q/k/v, gate/up) */
 
 enum { KT_FMT_TERN = 0, KT_FMT_Q8 = 1 };
+
+/* the one-round-trip decode product (kt_flat.h): slice length and LDS sizes */
+#ifndef KT_SL
+#define KT_SL 2                       /* steps of a K slice (one register set per step) */
+#endif
+#define KT_KSMAX 16                   /* waves per block */
+
+template <int FMT, int MT>
+struct KtFlat {
+  static constexpr int UW = FMT == KT_FMT_TERN ? 128 : 32;   /* bytes of a unit's activations */
+  static constexpr int UP = UW + 16;                         /* staged stride (the 8 units of a read on other banks) */
+  static constexpr int XW = MT * KT_SL * KT_KL * UP + 16;    /* one wave's staging (+ a dump slot) */
+  static size_t lds(int ks){ return (size_t)ks * XW + (size_t)ks * MT * 8 * 4; }
+};
+
 
 __host__ __device__ __forceinline__ int kt_r8(int R){ return (R + KT_RG - 1) / KT_RG; }
 __host__ __device__ __forceinline__ int kt_steps(int NU){ return (NU + KT_KL - 1) / KT_KL; }

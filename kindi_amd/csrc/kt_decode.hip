@@ -3,16 +3,7 @@
      k_q8_pack     GGUF Q8_0 rows (34-byte blocks) -> kq8 device layout
      k_quant_tern  fp32 rows -> int8 per 128-column group (or per row), XS, XA   (k_tc_q8, tc_hip.cu:43-74)
      k_quant_q8    fp32 rows -> int8 per 32-column block, fp16-rounded scale   (quant_q8, dsv41_cpu.c:251-280)
-   (the decode product itself, k_gemv, is in kt_gemv.h)
-
-   The product kernel: one wave per 8-row group, each row's K units spread over 8 lanes (lane = 8 c + r takes units
-   c, c + 8, ... of row r), so every launch has R/8 independent waves and needs no reduction outside the wave. A
-   wave streams its rows with 128-bit loads (1 KB contiguous per instruction), keeping the loads of KT_UB steps in
-   flight. The activations of a unit are read by the 8 lanes that share it (one 128-byte line per unit, served by
-   L1). Ternary digits are isolated with one AND per 4 columns (slots 0..2 keep their 4^k factor and are shifted
-   back exactly after the unit; slot 3 takes one shift), so a unit costs 8 x (4 dot4 + 5 logic ops) per lane,
-   independent of the trit values. A lane adds its units' scaled values in order (one fma each); the 8 lanes of a
-   row are then added by a fixed xor butterfly ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)). */
+   (the decode product itself, k_gemv_flat, is in kt_gemv.h) */
 #include "kt_common.h"
 
 /* ------------------------------------------------------------------ weights: layouts */

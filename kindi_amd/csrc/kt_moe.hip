@@ -13,6 +13,8 @@
 */
 #include "kt_common.h"
 
+#define KT_MOE_UB 4                   /* steps whose weight loads a grouped-product wave keeps in flight */
+
 extern "C" __global__ void __launch_bounds__(64) k_moe_topk(const float* __restrict__ logits, int E, int k,
                                                             int* __restrict__ ids, float* __restrict__ gw){
   /* one wave per token; E <= 1024, k <= 16 */
@@ -113,11 +115,11 @@ __global__ void __launch_bounds__(64) k_q8_grouped(const KtGroupedArgs a, const 
     float acc[MT];
 #pragma unroll
     for(int t = 0; t < MT; ++t) acc[t] = 0.0f;
-    for(int s0 = 0; s0 < S; s0 += KT_UB){
-      uint4 c0[KT_UB], c1[KT_UB];
-      uint16_t hs[KT_UB];
+    for(int s0 = 0; s0 < S; s0 += KT_MOE_UB){
+      uint4 c0[KT_MOE_UB], c1[KT_MOE_UB];
+      uint16_t hs[KT_MOE_UB];
 #pragma unroll
-      for(int k = 0; k < KT_UB; ++k){
+      for(int k = 0; k < KT_MOE_UB; ++k){
         const int u = (s0 + k) * KT_KL + c;
         if(s0 + k < S && u < NU){
           c0[k] = wb[kt_widx(NU, rg, s0 + k, 0, c, r)];
@@ -126,7 +128,7 @@ __global__ void __launch_bounds__(64) k_q8_grouped(const KtGroupedArgs a, const 
         }
       }
 #pragma unroll
-      for(int k = 0; k < KT_UB; ++k){
+      for(int k = 0; k < KT_MOE_UB; ++k){
         const int u = (s0 + k) * KT_KL + c;
         if(s0 + k < S && u < NU){
           const float d = kt_h2f(hs[k]);

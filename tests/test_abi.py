@@ -48,8 +48,8 @@ def test_version_and_sizes(lib):
 
 def test_decode_kslices(lib):
     """the K-slice count of the decode order depends on the width only"""
-    assert [lib.kt_decode_kslices(C, 0) for C in (128, 2048, 4096, 5120, 12288, 17408)] == [1, 1, 2, 2, 4, 4]
-    assert [lib.kt_decode_kslices(C, 1) for C in (1856, 2688)] == [2, 2]
+    assert [lib.kt_decode_kslices(C, 0) for C in (128, 2048, 4096, 5120, 12288, 17408)] == [1, 1, 2, 3, 6, 9]
+    assert [lib.kt_decode_kslices(C, 1) for C in (1856, 2688)] == [4, 6]
     assert lib.kt_decode_kslices(100, 0) == 0
 
 
