@@ -40,6 +40,9 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="headline only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
+    ap.add_argument("--plan", action="store_true",
+                    help="headline over the decode plan (kt_plan_run: one persistent launch per step) instead of one "
+                         "launch per product")
     ap.add_argument("--calib", action="store_true",
                     help="only a plain 1 GiB device copy (the known-size kernel that scales FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
@@ -139,7 +142,8 @@ def sweep_step(torch, linear, layers, M, seed=7):
         for f, names, act, o in calls:
             f(names, act, o)
 
-    return step, nbytes, calls, launches
+    stages = [([Lin.w[n] for n in names], act, o) for _, names, act, o in calls]
+    return step, nbytes, calls, launches, stages
 
 
 # ----------------------------------------------------------------------------------------------- other configs
@@ -315,40 +319,53 @@ def main():
     log("building the 27B-class weights")
     layers = build_27b(torch, linear, synth, (1, 16))
     log("config 3, M=1")
-    step, nbytes, calls, launches = sweep_step(torch, linear, layers, 1)
-    run = graphed(torch, step, use_graph)
-    ms = timer.run(run, a.steps, a.warmup)
+    step, nbytes, calls, launches, stages = sweep_step(torch, linear, layers, 1)
+    ms_l = timer.run(graphed(torch, step, use_graph), a.steps, a.warmup)
+    plan = linear.Plan(stages) if a.plan else None
+    if plan is not None:
+        # the decode plan: one persistent launch (k_plan<1>, after a one-block counter reset) per step
+        run = graphed(torch, plan.run, use_graph)
+        ms = timer.run(run, a.steps, a.warmup)
+        torch.cuda.synchronize()
+        if plan.status() != 0:
+            raise RuntimeError("decode plan: a stage barrier timed out")
+        nlaunch, kernel = 1, "k_plan<1> (decode plan, %d stages, grid %d x %d waves)" % (
+            len(stages), plan.info.grid, plan.info.waves + 1)
+    else:
+        ms, nlaunch, kernel = ms_l, len(calls), "k_gemv_flat<ternary,MT=1>"
     gbs = nbytes / ms / 1e6
-    # the dominant kernel (k_gemv_flat<ternary, 1 token>) is every launch of the step; inside the graph they run
-    # back to back, so the average launch duration is the timed region over the launch count (an upper bound:
-    # it includes the gaps between launches)
-    launch_ms = ms / len(calls)
-    achieved = nbytes / len(calls) / launch_ms / 1e6
-    traffic = pmc_traffic()
+    # the dominant kernel is the whole step (plan) or every launch of it (launches, back to back in the graph): its
+    # average duration is the timed region over the launch count (an upper bound: it includes the gaps)
+    launch_ms = ms / nlaunch
+    achieved = nbytes / nlaunch / launch_ms / 1e6
+    traffic = pmc_traffic() if plan is None else None
     out = {
         "metric": "decode GEMV HBM GB/s (% of 8 TB/s) + prefill int8 TOPS, ternary 27B shapes",
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8 x ternary (int32 accumulate, fp32 scale)", "data": "synthetic (seeded; BASELINE config 3)",
         "config": {"workload": "config 3: 27B-class decode sweep, 64 layers x {q,k,v,o,gate,up,down}, M=1",
-                   "tokens": 1, "bytes_per_step": nbytes, "launches_per_step": len(calls),
+                   "tokens": 1, "bytes_per_step": nbytes, "launches_per_step": nlaunch,
+                   "products_per_step": len(calls), "executor": "plan" if plan is not None else "launches",
                    "graph": use_graph, "frac_hbm": round(gbs / HBM_PEAK, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK, 4),
                      "traffic": traffic["bytes_per_launch"] if traffic else None,
                      "traffic_source": traffic["source"] if traffic else None,
-                     "algorithmic_bytes_per_launch": nbytes // len(calls),
-                     "kernel": "k_gemv_flat<ternary,MT=1>", "launches": len(calls),
+                     "algorithmic_bytes_per_launch": nbytes // nlaunch,
+                     "kernel": kernel, "launches": nlaunch,
                      "avg_launch_us": round(launch_ms * 1e3, 3)},
     }
     if not a.quick:
-        cfgs = {}
+        cfgs = {"c3 M=1 launches": {"ms_per_step": round(ms_l, 4), "GB/s": round(nbytes / ms_l / 1e6, 1),
+                                    "frac_hbm": round(nbytes / ms_l / 1e6 / HBM_PEAK, 4),
+                                    "note": "%d graph-captured launches (kt_tern_gemv / gemv3) per step" % len(calls)}}
         log("config 3, M=16")
-        step16, nb16, calls16, _ = sweep_step(torch, linear, layers, 16)
+        step16, nb16, calls16, _, _ = sweep_step(torch, linear, layers, 16)
         ms16 = timer.run(graphed(torch, step16, use_graph), max(a.steps // 2, 3), 2)
         cfgs["c3 M=16"] = {"ms_per_step": round(ms16, 4), "GB/s": round(nb16 / ms16 / 1e6, 1),
                            "frac_hbm": round(nb16 / ms16 / 1e6 / HBM_PEAK, 4)}
-        del layers, step16, calls16, step, calls, run
+        del layers, step16, calls16, step, calls, stages, plan
         torch.cuda.empty_cache()
         log("configs 0, 1, 2, 4")
         cfgs["c0"] = config0(torch, linear, synth, timer, a.steps, use_graph)

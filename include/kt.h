@@ -74,6 +74,39 @@ int kt_tern_gemv3(const void* W0, int R0, float* Y0, const void* W1, int R1, flo
 /* y[n R + r] = sum over parts p < sp of P[(n sp + p) R + r], in part order. k_tc_sum (tc_hip.cu:271-279). */
 int kt_tern_sum(const float* P, float* y, int R, int M, int sp, void* stream);
 
+/* ---------------------------------------------------------------- decode plan (one launch per decode step)
+   A sequence of ternary products run in order by one persistent launch: stage s starts after every earlier stage
+   has finished and its stores are visible (the ordering of separate stream-ordered launches, so a stage may read
+   what an earlier stage wrote), while the weight loads of later stages are already in flight. Each stage is what
+   kt_tern_gemv3 takes (1 .. 3 matrices with one quantized input, Y_i [M][R_i]) and gives the same bits.
+   Replaces the plan replay of a decode step (Plan.add / replay, tp.py:282-302; spec.py:250-325, 619-673).
+   kt_plan_bytes: the device bytes of a plan of n stages (caller-allocated, 256-byte aligned).
+   kt_plan_build: checks the stages, sizes the launch for the current device (every block resident at once) and
+   writes the plan (synchronous on `stream`; not for graph capture). `info` receives what kt_plan_run needs.
+   Stages take C % 128 == 0 and C <= 30720, M 1 .. 4 tokens (the same for every stage).
+   kt_plan_run: one plan execution (a small reset kernel, then the plan kernel; graph-capturable). Nothing else
+   may run on the GPU at the same time (the plan's blocks wait for each other).
+   kt_plan_status: after the run (synchronizes `stream`): 0, or 1 if a stage barrier timed out (results invalid). */
+typedef struct kt_stage {
+  const void* W[3];                   /* up to three kt2 matrices; R[i] <= 0 ends the list */
+  int R[3];
+  float* Y[3];                        /* [M][R_i] */
+  int C;
+  const int8_t* XQ;                   /* kt_quant_q8 output [M][ldq], XS / XA [M][C/128] */
+  int ldq;
+  const float* XS;
+  const int32_t* XA;
+  int M;
+} kt_stage;
+typedef struct kt_plan_info {
+  int nstages, grid, waves, mt;
+  size_t lds;
+} kt_plan_info;
+size_t kt_plan_bytes(int nstages);
+int kt_plan_build(const kt_stage* stages, int nstages, void* plan, kt_plan_info* info, void* stream);
+int kt_plan_run(const void* plan, const kt_plan_info* info, void* stream);
+int kt_plan_status(const void* plan, const kt_plan_info* info, int* status, void* stream);
+
 /* ---------------------------------------------------------------- prefill product (any M, matrix cores)
    Y and/or Y16 [M][ldy] (fp32 / fp16 bits); dbg as kt_tern_gemv. XA is accepted for the reference's argument list
    and not read (the matrix cores take signed trits). Replaces k_tc_mm2 / k_tc_mm{4,8,16} (tc_hip.cu:243-269,

@@ -3,10 +3,13 @@
    returns a hipError_t as int (0 = success; hipErrorInvalidValue for shapes or strides the kernels do not take).
    The declarations and the reference interfaces they replace are in include/kt.h. */
 #include "kt_common.h"
+#include <vector>
 #include "../../include/kt.h"
 
 template <int FMT, int MT, bool DBG>
 __global__ void k_gemv_flat(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
+template <int MT> __global__ void k_plan(const uint8_t*, unsigned*);
+extern "C" __global__ void k_plan_reset(unsigned*, int);
 template <int MT> __global__ void k_q8_grouped(const KtGroupedArgs, const int8_t*, const float*, float*, int32_t*);
 extern "C" __global__ void k_tern_pack(const uint8_t*, const uint16_t*, int, int, uint32_t*, uint16_t*);
 extern "C" __global__ void k_q8_pack(const uint8_t*, int, int, uint32_t*, uint16_t*);
@@ -147,6 +150,90 @@ int kt_tern_sum(const float* P, float* y, int R, int M, int sp, void* stream){
   hipLaunchKernelGGL(k_tern_sum, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, kt_stream(stream), P, y, R, M, sp);
   KT_LAUNCH_CHECK();
   return 0;
+}
+
+/* ------------------------------------------------------------------ decode plan */
+size_t kt_plan_bytes(int nstages){ return nstages > 0 ? kt_plan_size(nstages) : 0; }
+
+int kt_plan_build(const kt_stage* st, int n, void* plan, kt_plan_info* info, void* stream){
+  if(!st || n <= 0 || !plan || !info || !kt_al(plan, 256)) return KT_INVALID;
+  std::vector<uint8_t> buf(kt_plan_ctr_off(n), 0);
+  KtPlanHdr* H = (KtPlanHdr*)buf.data();
+  KtPStage* S = (KtPStage*)(buf.data() + KT_PLAN_HDR);
+  const int M = st[0].M;
+  int W = 1;
+  for(int s = 0; s < n; ++s){
+    const kt_stage& x = st[s];
+    if(x.M != M || M < 1 || M > 4 || x.C <= 0 || x.C % 128 || !x.XQ || !x.XS || !x.XA || x.ldq < x.C ||
+       x.ldq % 16 || !kt_al(x.XQ, 16)) return KT_INVALID;
+    const int NU = x.C / 128, ks = kt_kslices(NU);
+    if(ks > KT_KSMAX - 1) return KT_INVALID;                     /* C <= 30720: KS + 1 waves a block */
+    KtPStage& d = S[s];
+    int groups = 0, nmat = 0;
+    for(int i = 0; i < 3 && x.R[i] > 0; ++i){
+      if(!x.W[i] || !x.Y[i] || !kt_al(x.W[i], 16)) return KT_INVALID;
+      d.mat[i].codes = (const uint32_t*)x.W[i];
+      d.mat[i].scales = (const uint16_t*)((const uint8_t*)x.W[i] + kt_code_bytes(x.R[i], NU));
+      d.mat[i].y = x.Y[i];
+      d.mat[i].R = x.R[i];
+      d.mat[i].ldy = x.R[i];
+      d.mat[i].rg0 = groups;
+      groups += kt_r8(x.R[i]);
+      ++nmat;
+    }
+    if(!nmat) return KT_INVALID;
+    d.nmat = nmat; d.NU = NU; d.KS = ks; d.ngroups = groups;
+    d.xq = x.XQ; d.xs = x.XS; d.xa = (const int*)x.XA; d.ldq = x.ldq; d.ldxs = NU; d.M = M;
+    if(ks > W) W = ks;
+  }
+  for(int s = 0; s < n; ++s){
+    S[s].rgpi = W / S[s].KS;
+    S[s].nitems = (S[s].ngroups + S[s].rgpi - 1) / S[s].rgpi;
+  }
+  const int mt = M <= 1 ? 1 : M <= 2 ? 2 : 4;
+  const size_t lds = (size_t)W * (mt == 1 ? KtFlat<KT_FMT_TERN, 1>::XW : mt == 2 ? KtFlat<KT_FMT_TERN, 2>::XW
+                                                                               : KtFlat<KT_FMT_TERN, 4>::XW)
+                     + (size_t)2 * W * mt * 8 * 4;
+  const int block = 64 * (W + 1);
+  int dev = 0, cus = 0, nb = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if(e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if(e == hipSuccess){
+    const void* k = mt == 1 ? (const void*)k_plan<1> : mt == 2 ? (const void*)k_plan<2> : (const void*)k_plan<4>;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, block, lds);
+  }
+  if(e != hipSuccess) return (int)e;
+  if(nb <= 0 || cus <= 0 || nb * cus > KT_BAR_MAXG) return KT_INVALID;
+  H->nstages = n; H->G = nb * cus; H->W = W; H->MT = mt;
+  e = hipMemcpyAsync(plan, buf.data(), buf.size(), hipMemcpyHostToDevice, kt_stream(stream));
+  if(e == hipSuccess) e = hipStreamSynchronize(kt_stream(stream));
+  if(e != hipSuccess) return (int)e;
+  info->nstages = n; info->grid = H->G; info->waves = W; info->mt = mt; info->lds = lds;
+  return 0;
+}
+
+int kt_plan_run(const void* plan, const kt_plan_info* info, void* stream){
+  if(!plan || !info || info->nstages <= 0 || info->grid <= 0 || info->waves <= 0) return KT_INVALID;
+  hipStream_t s = kt_stream(stream);
+  unsigned* ctr = (unsigned*)((uint8_t*)plan + kt_plan_ctr_off(info->nstages));
+  hipLaunchKernelGGL(k_plan_reset, dim3(1), dim3(256), 0, s, ctr, (int)(KT_BAR_SUB + (info->grid + KT_BAR_GROUP - 1) / KT_BAR_GROUP) * 32);
+  const dim3 grid(info->grid), block(64 * (info->waves + 1));
+  const uint8_t* p = (const uint8_t*)plan;
+  if(info->mt == 1) hipLaunchKernelGGL(k_plan<1>, grid, block, info->lds, s, p, ctr);
+  else if(info->mt == 2) hipLaunchKernelGGL(k_plan<2>, grid, block, info->lds, s, p, ctr);
+  else hipLaunchKernelGGL(k_plan<4>, grid, block, info->lds, s, p, ctr);
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
+int kt_plan_status(const void* plan, const kt_plan_info* info, int* status, void* stream){
+  if(!plan || !info || !status || info->nstages <= 0) return KT_INVALID;
+  unsigned v = 0;
+  const uint8_t* p = (const uint8_t*)plan + kt_plan_ctr_off(info->nstages) + (size_t)KT_BAR_STATUS * 32 * 4;
+  hipError_t e = hipMemcpyAsync(&v, p, 4, hipMemcpyDeviceToHost, kt_stream(stream));
+  if(e == hipSuccess) e = hipStreamSynchronize(kt_stream(stream));
+  *status = (int)v;
+  return (int)e;
 }
 
 /* ------------------------------------------------------------------ prefill product */

@@ -66,6 +66,22 @@ __device__ __forceinline__ uint4 kt_ldnt(const uint4* p){
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+/* global-memory (address space 1) views: pointers read from memory (a plan's tables) are generic to the compiler,
+   and generic loads are FLAT instructions, which also count against the LDS wait counter */
+#define KT_G __attribute__((address_space(1)))
+__device__ __forceinline__ uint4 kt_ldnt_g(const void* p){
+  const kt_u32x4 v = __builtin_nontemporal_load((const KT_G kt_u32x4*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+template <typename T>
+__device__ __forceinline__ T kt_ldg(const void* p){ return *(const KT_G T*)p; }
+__device__ __forceinline__ uint4 kt_ldg4(const void* p){
+  const kt_u32x4 v = *(const KT_G kt_u32x4*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+template <typename T>
+__device__ __forceinline__ void kt_stg(void* p, T v){ *(KT_G T*)p = v; }
+
 __device__ __forceinline__ int kt_dot4(int a, int b, int c){ return __builtin_amdgcn_sdot4(a, b, c, false); }
 
 /* one matrix of a decode launch: its weights, output and the first global row group it owns */
@@ -82,6 +98,36 @@ struct KtGemvArgs {
   int ldq, ldxs;                      /* activation row stride (bytes); xs / xa row stride (units) */
   int M, pad;                         /* tokens */
 };
+
+/* a decode plan in device memory: header, stages, then the stage counters and the status word */
+struct KtPStage {
+  KtMat mat[KT_MAXMAT];
+  const int8_t* xq;
+  const float* xs;
+  const int* xa;
+  int nmat, NU, KS, ngroups;          /* matrices, units along C, K slices, row groups of all matrices */
+  int rgpi, nitems;                   /* row groups an item, items */
+  int ldq, ldxs, M, pad;
+};
+struct KtPlanHdr {
+  int nstages, G, W, MT;              /* stages, blocks, data waves a block, tokens a pass */
+  int pad[12];
+};
+#define KT_PLAN_HDR 64
+__host__ __device__ __forceinline__ size_t kt_plan_ctr_off(int nstages){
+  return ((size_t)KT_PLAN_HDR + (size_t)nstages * sizeof(KtPStage) + 255) / 256 * 256;
+}
+/* barrier words (128-byte lines of 32 words): flag, root, status, then one sub-counter per group of blocks */
+#define KT_BAR_FLAG 0
+#define KT_BAR_ROOT 1
+#define KT_BAR_STATUS 2
+#define KT_BAR_SUB 3
+#define KT_BAR_GROUP 32
+#define KT_BAR_MAXG 8192                  /* blocks a plan grid may have */
+#define KT_BAR_WORDS ((KT_BAR_SUB + KT_BAR_MAXG / KT_BAR_GROUP) * 32)
+__host__ __device__ __forceinline__ size_t kt_plan_size(int nstages){
+  return kt_plan_ctr_off(nstages) + ((size_t)KT_BAR_WORDS * 4 + 255) / 256 * 256;
+}
 
 /* grouped (MoE) launch over the token-sorted lists */
 struct KtGroupedArgs {

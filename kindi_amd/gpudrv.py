@@ -15,6 +15,17 @@ P = ctypes.c_void_p
 I = ctypes.c_int
 S = ctypes.c_size_t
 
+class KtStage(ctypes.Structure):
+    """kt_stage (include/kt.h): one product of a decode plan"""
+    _fields_ = [("W", P * 3), ("R", I * 3), ("Y", P * 3), ("C", I), ("XQ", P), ("ldq", I), ("XS", P), ("XA", P),
+                ("M", I)]
+
+
+class KtPlanInfo(ctypes.Structure):
+    """kt_plan_info (include/kt.h): the launch shape kt_plan_build chose"""
+    _fields_ = [("nstages", I), ("grid", I), ("waves", I), ("mt", I), ("lds", S)]
+
+
 # (name, restype, argtypes): the declarations of include/kt.h
 SIGNATURES = [
     ("kt_version", I, []),
@@ -27,6 +38,10 @@ SIGNATURES = [
     ("kt_tern_gemv", I, [P, I, I, P, I, P, P, I, P, I, P, P]),
     ("kt_tern_gemv3", I, [P, I, P, P, I, P, P, I, P, I, P, I, P, P, I, P]),
     ("kt_tern_sum", I, [P, P, I, I, I, P]),
+    ("kt_plan_bytes", S, [I]),
+    ("kt_plan_build", I, [ctypes.POINTER(KtStage), I, P, ctypes.POINTER(KtPlanInfo), P]),
+    ("kt_plan_run", I, [P, ctypes.POINTER(KtPlanInfo), P]),
+    ("kt_plan_status", I, [P, ctypes.POINTER(KtPlanInfo), ctypes.POINTER(I), P]),
     ("kt_tern_gemm", I, [P, I, I, P, I, P, P, I, P, P, I, P, P]),
     ("kt_q8_weight_bytes", S, [I, I]),
     ("kt_q8_pack", I, [P, I, I, P, P]),

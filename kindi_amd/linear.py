@@ -164,6 +164,52 @@ class Linear(object):
         return self.gemm(name, act)
 
 
+class Plan(object):
+    """A decode step as one persistent launch (kt_plan_*): the products run in the given order, each after every
+    earlier one has finished (the ordering of separate launches), with the weight loads of later products already
+    in flight. stages: [(mats, act, outs)]: up to three TernaryMatrix with one quantized input (Act) and their fp32
+    outputs [M, R_i], as Linear.gemv_q takes them. The buffers are referenced, not copied: they must live as long
+    as the plan. Replaces Plan.add / replay of a decode step (tp.py:282-302, spec.py:250-325)."""
+
+    def __init__(self, stages, device="cuda"):
+        lib = gpudrv.load()
+        n = len(stages)
+        arr = (gpudrv.KtStage * n)()
+        self.refs = []
+        for k, (mats, act, outs) in enumerate(stages):
+            if not 1 <= len(mats) <= 3 or len(outs) != len(mats):
+                raise ValueError("stage %d: 1 to 3 matrices with one output each" % k)
+            st = arr[k]
+            for i, (m, o) in enumerate(zip(mats, outs)):
+                if m.C != act.C or o.dtype != torch.float32 or not o.is_contiguous() or o.numel() < act.M * m.R:
+                    raise ValueError("stage %d: matrix %d does not match its input or output" % (k, i))
+                st.W[i] = m.W.data_ptr()
+                st.R[i] = m.R
+                st.Y[i] = o.data_ptr()
+            st.C = act.C
+            st.XQ = act.XQ.data_ptr()
+            st.ldq = act.XQ.stride(0)
+            st.XS = act.XS.data_ptr()
+            st.XA = act.XA.data_ptr()
+            st.M = act.M
+            self.refs.append((mats, act, outs))
+        self.buf = torch.empty(lib.kt_plan_bytes(n) + 256, dtype=torch.uint8, device=device)
+        off = (-self.buf.data_ptr()) % 256
+        self.ptr = VP(self.buf.data_ptr() + off)
+        self.info = gpudrv.KtPlanInfo()
+        gpudrv.check(lib.kt_plan_build(arr, n, self.ptr, ctypes.byref(self.info), stream()), "kt_plan_build")
+
+    def run(self):
+        gpudrv.check(gpudrv.load().kt_plan_run(self.ptr, ctypes.byref(self.info), stream()), "kt_plan_run")
+
+    def status(self):
+        """0, or 1 if a stage barrier timed out in a run since the last build (results invalid)"""
+        v = ctypes.c_int(0)
+        gpudrv.check(gpudrv.load().kt_plan_status(self.ptr, ctypes.byref(self.info), ctypes.byref(v), stream()),
+                     "kt_plan_status")
+        return v.value
+
+
 def tern_sum(P, R, M, sp, y=None):
     """k_tc_sum (tc_hip.cu:271-279): parts [M, sp, R] -> [M, R] in part order"""
     if y is None:

@@ -27,7 +27,7 @@ def lib():
 
 def test_exports_every_declared_symbol(lib):
     names = declared()
-    assert len(names) == 19
+    assert len(names) == 23
     for n in names:
         assert hasattr(lib, n), n
     from kindi_amd import gpudrv
@@ -72,3 +72,30 @@ def test_validation_rejects_bad_shapes(lib):
     # M = 0: a no-op
     assert lib.kt_tern_gemv(fake, 64, 256, fake, 256, fake, fake, 0, fake, 64, None, None) == 0
     # dbg with several matrices in one launch
+
+
+def test_plan_validation(lib):
+    """kt_plan_build rejects stages the plan kernel does not take before any GPU call"""
+    from kindi_amd import gpudrv
+    assert lib.kt_plan_bytes(0) == 0 and lib.kt_plan_bytes(256) % 256 == 0
+    fake = ctypes.c_void_p(1 << 20)                       # 256-aligned, never dereferenced on these paths
+    info = gpudrv.KtPlanInfo()
+
+    def stage(C=5120, M=1, R=64, ldq=None):
+        s = gpudrv.KtStage()
+        s.W[0], s.R[0], s.Y[0] = 1 << 21, R, 1 << 22
+        s.C, s.XQ, s.ldq, s.XS, s.XA, s.M = C, 1 << 23, ldq or C, 1 << 24, 1 << 25, M
+        return s
+
+    def build(*stages):
+        arr = (gpudrv.KtStage * len(stages))(*stages)
+        return lib.kt_plan_build(arr, len(stages), fake, ctypes.byref(info), None)
+
+    assert lib.kt_plan_build(None, 1, fake, ctypes.byref(info), None) == INVALID
+    assert build(stage(C=100)) == INVALID                  # C % 128
+    assert build(stage(M=5)) == INVALID                    # one pass of at most 4 tokens
+    assert build(stage(), stage(M=2)) == INVALID           # every stage the same M
+    assert build(stage(C=32768)) == INVALID                # 16 K slices + the control wave > 16 waves
+    assert build(stage(R=0)) == INVALID                    # no matrix
+    assert build(stage(ldq=5128)) == INVALID               # ldq % 16
+    assert lib.kt_plan_run(None, ctypes.byref(info), None) == INVALID
