@@ -40,6 +40,7 @@ def parse():
     ap.add_argument("--quick", action="store_true", help="headline only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
+    ap.add_argument("--unpooled", action="store_true", help="one allocation per weight matrix instead of one pool")
     ap.add_argument("--plan", action="store_true",
                     help="headline over the decode plan (kt_plan_run: one persistent launch per step) instead of one "
                          "launch per product")
@@ -94,14 +95,21 @@ def graphed(torch, fn, use_graph):
 
 
 # ----------------------------------------------------------------------------------------------- config 3
-def build_27b(torch, linear, synth, M_list):
+def build_27b(torch, linear, synth, M_list, pooled=True):
+    """the 64 layers' 448 matrices, packed into one device pool (or one allocation each)"""
     cfg = synth.CFG["c3"]
+    lib = linear.gpudrv.load()
+    sizes = [(lib.kt_tern_weight_bytes(R, C) + 255) // 256 * 256 for n, R, C in cfg["mats"]]
+    pool = torch.empty(sum(sizes) * cfg["layers"], dtype=torch.uint8, device="cuda") if pooled else None
+    off = 0
     layers = []
     for l in range(cfg["layers"]):
         mats = {}
         for i, (n, R, C) in enumerate(cfg["mats"]):
             bc, dpm = synth.tern_pack(R, C, 100 + l * 8 + i, device="cuda")
-            mats[n] = linear.TernaryMatrix(bc, dpm, R, C)
+            W = pool[off:off + sizes[i]] if pooled else None
+            off += sizes[i]
+            mats[n] = linear.TernaryMatrix(bc, dpm, R, C, W=W)
             del bc, dpm
         layers.append(mats)
     torch.cuda.synchronize()
@@ -317,7 +325,7 @@ def main():
 
     t0 = time.time()
     log("building the 27B-class weights")
-    layers = build_27b(torch, linear, synth, (1, 16))
+    layers = build_27b(torch, linear, synth, (1, 16), pooled=not a.unpooled)
     log("config 3, M=1")
     step, nbytes, calls, launches, stages = sweep_step(torch, linear, layers, 1)
     ms_l = timer.run(graphed(torch, step, use_graph), a.steps, a.warmup)

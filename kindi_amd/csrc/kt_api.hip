@@ -184,6 +184,16 @@ int kt_plan_build(const kt_stage* st, int n, void* plan, kt_plan_info* info, voi
     if(!nmat) return KT_INVALID;
     d.nmat = nmat; d.NU = NU; d.KS = ks; d.ngroups = groups;
     d.xq = x.XQ; d.xs = x.XS; d.xa = (const int*)x.XA; d.ldq = x.ldq; d.ldxs = NU; d.M = M;
+    /* inputs that overlap an output of an earlier stage are read with coherent loads */
+    const uintptr_t in[3][2] = {{(uintptr_t)x.XQ, (uintptr_t)x.XQ + (size_t)(M - 1) * x.ldq + x.C},
+                                {(uintptr_t)x.XS, (uintptr_t)x.XS + (size_t)M * NU * 4},
+                                {(uintptr_t)x.XA, (uintptr_t)x.XA + (size_t)M * NU * 4}};
+    d.coh = 0;
+    for(int p = 0; p < s && !d.coh; ++p)
+      for(int i = 0; i < 3 && st[p].R[i] > 0; ++i){
+        const uintptr_t y0 = (uintptr_t)st[p].Y[i], y1 = y0 + (size_t)M * st[p].R[i] * 4;
+        for(int q = 0; q < 3; ++q) if(in[q][0] < y1 && y0 < in[q][1]) d.coh = 1;
+      }
     if(ks > W) W = ks;
   }
   for(int s = 0; s < n; ++s){
@@ -203,7 +213,7 @@ int kt_plan_build(const kt_stage* st, int n, void* plan, kt_plan_info* info, voi
     e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, block, lds);
   }
   if(e != hipSuccess) return (int)e;
-  if(nb <= 0 || cus <= 0 || nb * cus > KT_BAR_MAXG) return KT_INVALID;
+  if(nb <= 0 || cus <= 0) return KT_INVALID;
   H->nstages = n; H->G = nb * cus; H->W = W; H->MT = mt;
   e = hipMemcpyAsync(plan, buf.data(), buf.size(), hipMemcpyHostToDevice, kt_stream(stream));
   if(e == hipSuccess) e = hipStreamSynchronize(kt_stream(stream));
@@ -216,7 +226,7 @@ int kt_plan_run(const void* plan, const kt_plan_info* info, void* stream){
   if(!plan || !info || info->nstages <= 0 || info->grid <= 0 || info->waves <= 0) return KT_INVALID;
   hipStream_t s = kt_stream(stream);
   unsigned* ctr = (unsigned*)((uint8_t*)plan + kt_plan_ctr_off(info->nstages));
-  hipLaunchKernelGGL(k_plan_reset, dim3(1), dim3(256), 0, s, ctr, (int)(KT_BAR_SUB + (info->grid + KT_BAR_GROUP - 1) / KT_BAR_GROUP) * 32);
+  hipLaunchKernelGGL(k_plan_reset, dim3(1), dim3(256), 0, s, ctr, (int)KT_BAR_WORDS);
   const dim3 grid(info->grid), block(64 * (info->waves + 1));
   const uint8_t* p = (const uint8_t*)plan;
   if(info->mt == 1) hipLaunchKernelGGL(k_plan<1>, grid, block, info->lds, s, p, ctr);

@@ -107,7 +107,7 @@ struct KtPStage {
   const int* xa;
   int nmat, NU, KS, ngroups;          /* matrices, units along C, K slices, row groups of all matrices */
   int rgpi, nitems;                   /* row groups an item, items */
-  int ldq, ldxs, M, pad;
+  int ldq, ldxs, M, coh;              /* coh: the inputs overlap an earlier stage's outputs */
 };
 struct KtPlanHdr {
   int nstages, G, W, MT;              /* stages, blocks, data waves a block, tokens a pass */
@@ -117,14 +117,12 @@ struct KtPlanHdr {
 __host__ __device__ __forceinline__ size_t kt_plan_ctr_off(int nstages){
   return ((size_t)KT_PLAN_HDR + (size_t)nstages * sizeof(KtPStage) + 255) / 256 * 256;
 }
-/* barrier words (128-byte lines of 32 words): flag, root, status, then one sub-counter per group of blocks */
-#define KT_BAR_FLAG 0
-#define KT_BAR_ROOT 1
-#define KT_BAR_STATUS 2
-#define KT_BAR_SUB 3
-#define KT_BAR_GROUP 32
-#define KT_BAR_MAXG 8192                  /* blocks a plan grid may have */
-#define KT_BAR_WORDS ((KT_BAR_SUB + KT_BAR_MAXG / KT_BAR_GROUP) * 32)
+/* barrier words (128-byte lines of 32 words): status, then KT_BAR_SHARDS arrival counters (block b arrives on
+   shard b % KT_BAR_SHARDS) */
+#define KT_BAR_STATUS 0
+#define KT_BAR_SUB 1
+#define KT_BAR_SHARDS 32
+#define KT_BAR_WORDS ((KT_BAR_SUB + KT_BAR_SHARDS) * 32)
 __host__ __device__ __forceinline__ size_t kt_plan_size(int nstages){
   return kt_plan_ctr_off(nstages) + ((size_t)KT_BAR_WORDS * 4 + 255) / 256 * 256;
 }

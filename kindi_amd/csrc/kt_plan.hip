@@ -14,8 +14,7 @@
      scope), arrives (a two-level count) and spins (bounded) on a flag until all G blocks have arrived, then
      acquires, and the block's data waves go on (block barrier). That is the ordering and visibility of separate stream-ordered
      launches: a stage may read anything an earlier stage wrote.
-   The control wave issues no weight loads, so its fences and its spin wait for nothing but its own stores and
-   atomics. The plan (header, stages) is read-only in the launch and the barrier counters and status word come as a
+   The control wave issues no weight loads, so its waits are for nothing but its own stores and atomics. The plan (header, stages) is read-only in the launch and the barrier counters and status word come as a
    separate argument, so the stage fields are scalar loads. A spin that runs out of iterations sets the plan's status word and every later barrier then passes at
    once, so a failed plan ends instead of hanging (kt_plan_status reports it). */
 #include "kt_gemv.h"
@@ -28,35 +27,40 @@ __device__ __forceinline__ const KtPStage& kt_stage_at(const uint8_t* plan, int 
   return ((const KtPStage*)(plan + KT_PLAN_HDR))[s];
 }
 
-/* the grid barrier of the control wave before stage k + 1 (k = 0, 1, ...): release; arrive on the sub-counter of
-   the block's group of KT_BAR_GROUP blocks; the group's last arriver arrives on the root counter, and the root's
-   last arriver raises the flag to k + 1; every block spins (bounded) until the flag reaches k + 1; acquire. Counts
-   only grow (targets (k + 1) x size), so one set of counters serves every stage; a block cannot arrive at barrier
-   k + 1 before all have arrived at k. The counters sit on their own 128-byte lines. */
+/* the grid barrier of the control wave before stage k + 1 (k = 0, 1, ...). Block b arrives on counter b % 32 (32
+   counters on their own 128-byte lines, so arrivals do not queue on one address); lanes 0..31 then poll one counter
+   each until every counter has reached its count for barrier k ((k + 1) x its blocks: counts only grow, and no
+   block arrives at barrier k + 1 before all have arrived at k). No cache-wide maintenance: what crosses stages is
+   made coherent where it is written and read instead (agent-scope stores of the output rows; agent-scope loads of
+   a stage's inputs when they overlap an earlier stage's outputs), and the workgroup-scope fences wait for this
+   wave's own stores before it arrives. */
 __device__ __forceinline__ void kt_plan_barrier(unsigned* ctr, unsigned k, unsigned G, int lane){
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  if(lane == 0){
-    unsigned* flag = ctr + KT_BAR_FLAG * 32;
-    unsigned* root = ctr + KT_BAR_ROOT * 32;
-    unsigned* status = ctr + KT_BAR_STATUS * 32;
-    const unsigned g = blockIdx.x / KT_BAR_GROUP, ng = (G + KT_BAR_GROUP - 1) / KT_BAR_GROUP;
-    const unsigned gsize = min((unsigned)KT_BAR_GROUP, G - g * KT_BAR_GROUP);
-    unsigned* sub = ctr + (KT_BAR_SUB + g) * 32;
-    if(__hip_atomic_fetch_add(sub, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (k + 1) * gsize - 1u &&
-       __hip_atomic_fetch_add(root, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (k + 1) * ng - 1u)
-      __hip_atomic_store(flag, k + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if(__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u){
-      unsigned n = 0;
-      while(__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < k + 1u){
-        __builtin_amdgcn_s_sleep(1);
-        if(++n == KT_SPIN_MAX){
-          __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          break;
-        }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  unsigned* status = ctr + KT_BAR_STATUS * 32;
+  if(lane == 0)
+    __hip_atomic_fetch_add(ctr + (KT_BAR_SUB + blockIdx.x % KT_BAR_SHARDS) * 32, 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  if(__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u){
+    const unsigned want = lane < KT_BAR_SHARDS ? (k + 1u) * ((G - lane + KT_BAR_SHARDS - 1) / KT_BAR_SHARDS) : 0u;
+    unsigned* mine = ctr + (KT_BAR_SUB + (lane < KT_BAR_SHARDS ? lane : 0)) * 32;
+    for(unsigned n = 0;; ++n){
+      const unsigned v = lane < KT_BAR_SHARDS ? __hip_atomic_load(mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+      if(__ballot(v < want) == 0) break;
+      if(n == KT_SPIN_MAX){
+        if(lane == 0) __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
       }
+      __builtin_amdgcn_s_sleep(1);
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+/* the block barrier of the plan: LDS traffic of the wave done, then s_barrier. Unlike __syncthreads it does not
+   wait for the wave's global loads and stores (the data waves' prefetch, the control wave's output stores), which
+   nothing across this barrier needs: the slice sums meet in LDS, and the stage ordering is the grid barrier's. */
+__device__ __forceinline__ void kt_block_sync(){
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 /* one task of a data wave: item i of stage s */
@@ -97,28 +101,27 @@ __global__ void __launch_bounds__(1024) k_plan(const uint8_t* __restrict__ plan,
     int par = 0;
     for(int s = 0; s < nS; ++s){
       if(s > 0) kt_plan_barrier(ctr, (unsigned)(s - 1), (unsigned)G, lane);
-      __syncthreads();                                           /* B1: stage s may start */
+      kt_block_sync();                                           /* B1: stage s may start */
       const KtPStage& S = kt_stage_at(plan, s);
       for(int i = b; i < S.nitems; i += G){
         {
           const int t0 = 0, nt = S.M;
-          __syncthreads();                                       /* B2: the slice sums of item i are in LDS */
-          for(int p = lane; p < S.rgpi * 8; p += 64){
-            const int ri = p >> 3, rr = p & 7, rg = i * S.rgpi + ri;
-            if(rg < S.ngroups){
-              int mi = 0;
-              if(S.nmat > 1 && rg >= S.mat[1].rg0) mi = 1;
-              if(S.nmat > 2 && rg >= S.mat[2].rg0) mi = 2;
-              const KtMat& m = S.mat[mi];
-              const int row = (rg - m.rg0) * KT_RG + rr;
-              if(row < m.R){
-                for(int t = 0; t < nt; ++t){
-                  const float* q = red + ((size_t)(par * W + ri * S.KS) * MT + t) * 8 + rr;
-                  float v = q[0];
-                  for(int k = 1; k < S.KS; ++k) v += q[(size_t)k * MT * 8];
-                  kt_stg<float>(m.y + (long long)(t0 + t) * m.ldy + row, v);
-                }
-              }
+          kt_block_sync();                                       /* B2: the slice sums of item i are in LDS */
+          const int t = lane >> 3, rr = lane & 7;                /* lane = 8 t + r: token t, row r of a group */
+          for(int ri = 0; ri < S.rgpi; ++ri){                    /* uniform: the matrix fields are scalar */
+            const int rg = i * S.rgpi + ri;
+            if(rg >= S.ngroups) break;
+            int mi = 0;
+            if(S.nmat > 1 && rg >= S.mat[1].rg0) mi = 1;
+            if(S.nmat > 2 && rg >= S.mat[2].rg0) mi = 2;
+            const KtMat& m = S.mat[__builtin_amdgcn_readfirstlane(mi)];
+            const int row = (rg - m.rg0) * KT_RG + rr;
+            if(t < nt && row < m.R){
+              const float* q = red + ((size_t)(par * W + ri * S.KS) * MT + t) * 8 + rr;
+              float v = q[0];
+              for(int k = 1; k < S.KS; ++k) v += q[(size_t)k * MT * 8];
+              __hip_atomic_store((KT_G float*)(m.y + (long long)(t0 + t) * m.ldy + row), v, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
             }
           }
           par ^= 1;
@@ -128,21 +131,72 @@ __global__ void __launch_bounds__(1024) k_plan(const uint8_t* __restrict__ plan,
     return;
   }
 
-  /* ------------------------------------------------------------------ data wave dw */
+  /* ------------------------------------------------------------------ data wave dw
+     A wave's K slice (dw % KS) is the same for every item of a stage, so its activations are staged once per stage
+     (into the wave's LDS region, the unit scales and sums into registers). Weights run through a ring of three
+     register sets: while task k computes, tasks k + 1 and k + 2 are in flight, and the set of task k is refilled
+     with task k + 3 after it. The activations of the next stage are fetched with the weights that first reach it,
+     unless that stage reads what an earlier stage writes (then after its barrier). */
   const int dw = wave;
   uint8_t* xw = kt_lds + (size_t)dw * F::XW;
-  int par = 0, s_done = -1;                                       /* stages whose B1 this wave has passed */
-  KtStep WA[SL], WB[SL];
+  int par = 0, s_done = -1, s_in = -1, s_pend = -1;             /* B1 passed; stage staged; stage fetched early */
+  KtStep W0[SL], W1[SL], W2[SL];
+  uint32_t saC[2][SL][MT], saP[2][SL][MT];                      /* unit scale (f32 bits) and sum: staged, early */
+  uint4 stgP[SL][MT];
+
+  /* the loads of stage s's activations for this wave's slice: its steps' rows (16 bytes a lane) and unit values */
+  auto load_x = [&](int s, uint4 (&stg)[SL][MT], uint32_t (&sa)[2][SL][MT]) __attribute__((always_inline)) {
+    const KtPStage& S = kt_stage_at(plan, s);
+    const int ks = dw % S.KS, NU = S.NU, St = kt_steps(NU), s_lo = ks * St / S.KS, ns = (ks + 1) * St / S.KS - s_lo;
+    const int o = lane * 16;
+#pragma unroll
+    for(int j = 0; j < SL; ++j){
+      const int st = s_lo + (j < ns ? j : 0), u = st * KT_KL + c, uu = (j < ns && u < NU) ? u : 0;
+      const int nc = NU - st * KT_KL < KT_KL ? NU - st * KT_KL : KT_KL;
+#pragma unroll
+      for(int tt = 0; tt < MT; ++tt){
+        const int n = tt < S.M ? tt : 0;
+        const int oc = o < nc * UW ? o : 0;
+        const float* px = S.xs + (long long)n * S.ldxs + uu;
+        const int* pa = S.xa + (long long)n * S.ldxs + uu;
+        const int8_t* pq = S.xq + (long long)n * S.ldq + (long long)st * KT_KL * UW + oc;
+        if(S.coh){                                                  /* written in this launch: coherent loads */
+          sa[0][j][tt] = __hip_atomic_load((const KT_G unsigned*)px, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          sa[1][j][tt] = __hip_atomic_load((const KT_G unsigned*)pa, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const KT_G unsigned* q4 = (const KT_G unsigned*)pq;
+          stg[j][tt] = make_uint4(__hip_atomic_load(q4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                                  __hip_atomic_load(q4 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                                  __hip_atomic_load(q4 + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                                  __hip_atomic_load(q4 + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        } else {
+          sa[0][j][tt] = kt_ldg<uint32_t>(px);
+          sa[1][j][tt] = kt_ldg<uint32_t>(pa);
+          stg[j][tt] = kt_ldg4(pq);
+        }
+      }
+    }
+  };
+  /* the staged rows into the wave's LDS region (every slot written; the ones of absent units are never read) */
+  auto put_x = [&](const uint4 (&stg)[SL][MT]) __attribute__((always_inline)) {
+    const int o = lane * 16, lo = (o / UW) * UP + o % UW;
+#pragma unroll
+    for(int j = 0; j < SL; ++j)
+#pragma unroll
+      for(int tt = 0; tt < MT; ++tt)
+        *(uint4*)(xw + (j * MT + tt) * KT_KL * UP + lo) = stg[j][tt];
+    kt_wave_sync();
+  };
 
   /* the weight loads of a task (every offset first, then every load; a lane without a unit reads offset 0) */
   auto load_w = [&](const KtTask& t, KtStep (&w)[SL]) __attribute__((always_inline)) {
-    const KtPStage& S = kt_stage_at(plan, t.s);
+    const bool live = t.s < nS;                                     /* past the last task: the same loads, offset 0 */
+    const KtPStage& S = kt_stage_at(plan, live ? t.s : 0);
     const int ri = dw / S.KS, ks = dw - ri * S.KS, rg = t.i * S.rgpi + ri;
-    const bool act = ri < S.rgpi && rg < S.ngroups;
+    const bool act = live && ri < S.rgpi && rg < S.ngroups;
     int mi = 0;
     if(act && S.nmat > 1 && rg >= S.mat[1].rg0) mi = 1;
     if(act && S.nmat > 2 && rg >= S.mat[2].rg0) mi = 2;
-    const KtMat& m = S.mat[mi];
+    const KtMat& m = S.mat[__builtin_amdgcn_readfirstlane(mi)];
     const int NU = S.NU, St = kt_steps(NU), s_lo = ks * St / S.KS, ns = (ks + 1) * St / S.KS - s_lo;
     const int lrg = rg - m.rg0;
     unsigned o0[SL], o1[SL], os[SL];
@@ -163,87 +217,89 @@ __global__ void __launch_bounds__(1024) k_plan(const uint8_t* __restrict__ plan,
       w[j].hs = kt_ldg<uint16_t>(sb + os[j]);
     }
   };
-
-  /* run task t with weights w; the next task's weights go to wn */
-  auto run = [&](const KtTask& t, const KtStep (&w)[SL], const KtTask& tn, KtStep (&wn)[SL]) __attribute__((always_inline)) {
-    while(s_done < t.s){ __syncthreads(); ++s_done; }             /* B1 of every stage up to t's */
-    const KtPStage& S = kt_stage_at(plan, t.s);
-    const int ri = dw / S.KS, ks = dw - ri * S.KS, rg = t.i * S.rgpi + ri;
-    const bool act = ri < S.rgpi && rg < S.ngroups;              /* wave-uniform */
-    const int NU = S.NU, St = kt_steps(NU), s_lo = ks * St / S.KS, ns = (ks + 1) * St / S.KS - s_lo;
-    {                                                               /* one pass: M <= MT tokens */
-      const int t0 = 0, nt = S.M;
-      uint32_t sa[2][SL][MT];
-      uint4 stg[SL][MT];
-      const int o = lane * 16;
-#pragma unroll
-      for(int j = 0; j < SL; ++j){
-        const int st = s_lo + (j < ns ? j : 0), u = st * KT_KL + c, uu = (j < ns && u < NU) ? u : 0;
-        const int nc = NU - st * KT_KL < KT_KL ? NU - st * KT_KL : KT_KL;
-#pragma unroll
-        for(int tt = 0; tt < MT; ++tt){
-          const int n = t0 + (tt < nt ? tt : 0);
-          sa[0][j][tt] = kt_ldg<uint32_t>(S.xs + (long long)n * S.ldxs + uu);
-          sa[1][j][tt] = kt_ldg<uint32_t>(S.xa + (long long)n * S.ldxs + uu);
-          const int oc = o < nc * UW ? o : 0;
-          stg[j][tt] = kt_ldg4(S.xq + (long long)n * S.ldq + (long long)st * KT_KL * UW + oc);
-        }
-      }
-      kt_pin<SL * MT>(&stg[0][0], &sa[0][0][0]);
-      const int lo = (o / UW) * UP + o % UW;
-#pragma unroll
-      for(int j = 0; j < SL; ++j)
-#pragma unroll
-        for(int tt = 0; tt < MT; ++tt)
-          *(uint4*)(xw + (j * MT + tt) * KT_KL * UP + lo) = stg[j][tt];
-      /* the next task's weights: issued after this task's activations have arrived (a wait for those is then a wait
-         for nothing else) and before its compute, so they travel during this task and the barriers that follow */
-      if(tn.s < nS) load_w(tn, wn);
-      kt_wave_sync();
-      if(act){
-        float acc[MT];
-#pragma unroll
-        for(int tt = 0; tt < MT; ++tt) acc[tt] = 0.0f;
-#pragma unroll
-        for(int j = 0; j < SL; ++j){
-          const int u = (s_lo + j) * KT_KL + c;
-          if(j < ns){                                               /* wave-uniform */
-            const bool uok = u < NU;
-            const float d = uok ? kt_h2f(w[j].hs) : 0.0f;
-#pragma unroll
-            for(int tt = 0; tt < MT; ++tt){
-              if(tt < nt){
-                int v = kt_unit_lds<KT_FMT_TERN>(w[j].c0, w[j].c1, xw + ((j * MT + tt) * KT_KL + (uok ? c : 0)) * UP)
-                        - (int)sa[1][j][tt];
-                v = uok ? v : 0;
-                acc[tt] = fmaf((float)v, __uint_as_float(sa[0][j][tt]) * d, acc[tt]);
-              }
-            }
-          }
-        }
-#pragma unroll
-        for(int tt = 0; tt < MT; ++tt){
-          const float y = kt_row_sum(acc[tt]);
-          if(c == 0) red[((size_t)(par * W + dw) * MT + tt) * 8 + r] = y;
-        }
-      }
-      kt_wave_sync();                                               /* the staging is rewritten next */
-      __syncthreads();                                              /* B2 */
-      par ^= 1;
+  /* a task's weights (the same loads when there is no task: every path issues as many, so the compiler's wait
+     counts for the ring stay exact), and the activations of its stage when it is a later stage seen ahead */
+  auto prefetch = [&](const KtTask& t, KtStep (&w)[SL]) __attribute__((always_inline)) {
+    load_w(t, w);                                                   /* always issued: exact wait counts */
+    if(t.s < nS && t.s != s_in && s_pend < 0 && !kt_stage_at(plan, t.s).coh){
+      load_x(t.s, stgP, saP);
+      s_pend = t.s;
     }
   };
 
-  KtTask t = kt_first_task(plan, nS, b);
-  if(t.s < nS) load_w(t, WA);
-  while(t.s < nS){
-    const KtTask u = kt_next_task(plan, nS, b, G, t);
-    run(t, WA, u, WB);
-    if(u.s >= nS) break;
-    const KtTask v = kt_next_task(plan, nS, b, G, u);
-    run(u, WB, v, WA);
-    t = v;
+  /* run task t with weights w; then refill w with task tr */
+  auto run = [&](const KtTask& t, KtStep (&w)[SL], const KtTask& tr) __attribute__((always_inline)) {
+    const KtPStage& S = kt_stage_at(plan, t.s);
+    if(t.s != s_in){                                                /* the first task of a stage for this wave */
+      while(s_done < t.s){ kt_block_sync(); ++s_done; }           /* B1 of every stage up to t's */
+      if(s_pend == t.s){
+        put_x(stgP);
+#pragma unroll
+        for(int j = 0; j < SL; ++j)
+#pragma unroll
+          for(int tt = 0; tt < MT; ++tt){ saC[0][j][tt] = saP[0][j][tt]; saC[1][j][tt] = saP[1][j][tt]; }
+        s_pend = -1;
+      } else {
+        uint4 stg[SL][MT];
+        load_x(t.s, stg, saC);
+        put_x(stg);
+      }
+      s_in = t.s;
+    }
+    const int ri = dw / S.KS, ks = dw - ri * S.KS, rg = t.i * S.rgpi + ri;
+    const bool act = ri < S.rgpi && rg < S.ngroups;                /* wave-uniform */
+    const int NU = S.NU, St = kt_steps(NU), s_lo = ks * St / S.KS, ns = (ks + 1) * St / S.KS - s_lo;
+    const int nt = S.M;
+    if(act){
+      float acc[MT];
+#pragma unroll
+      for(int tt = 0; tt < MT; ++tt) acc[tt] = 0.0f;
+#pragma unroll
+      for(int j = 0; j < SL; ++j){
+        const int u = (s_lo + j) * KT_KL + c;
+        if(j < ns){                                                 /* wave-uniform */
+          const bool uok = u < NU;
+          const float d = uok ? kt_h2f(w[j].hs) : 0.0f;
+#pragma unroll
+          for(int tt = 0; tt < MT; ++tt){
+            if(tt < nt){
+              int v = kt_unit_lds<KT_FMT_TERN>(w[j].c0, w[j].c1, xw + ((j * MT + tt) * KT_KL + (uok ? c : 0)) * UP)
+                      - (int)saC[1][j][tt];
+              v = uok ? v : 0;
+              acc[tt] = fmaf((float)v, __uint_as_float(saC[0][j][tt]) * d, acc[tt]);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for(int tt = 0; tt < MT; ++tt){
+        const float y = kt_row_sum(acc[tt]);
+        if(c == 0) red[((size_t)(par * W + dw) * MT + tt) * 8 + r] = y;
+      }
+    }
+    kt_block_sync();                                                /* B2 */
+    par ^= 1;
+    prefetch(tr, w);
+  };
+
+  KtTask t0 = kt_first_task(plan, nS, b);
+  KtTask t1 = kt_next_task(plan, nS, b, G, t0);
+  KtTask t2 = kt_next_task(plan, nS, b, G, t1);
+  prefetch(t0, W0);
+  prefetch(t1, W1);
+  prefetch(t2, W2);
+  while(t0.s < nS){
+    const KtTask t3 = kt_next_task(plan, nS, b, G, t2);
+    run(t0, W0, t3);
+    if(t1.s >= nS) break;
+    const KtTask t4 = kt_next_task(plan, nS, b, G, t3);
+    run(t1, W1, t4);
+    if(t2.s >= nS) break;
+    const KtTask t5 = kt_next_task(plan, nS, b, G, t4);
+    run(t2, W2, t5);
+    t0 = t3; t1 = t4; t2 = t5;
   }
-  while(s_done < nS - 1){ __syncthreads(); ++s_done; }              /* the remaining stages' B1 */
+  while(s_done < nS - 1){ kt_block_sync(); ++s_done; }              /* the remaining stages' B1 */
 }
 
 extern "C" __global__ void k_plan_reset(unsigned* ctr, int n){

@@ -45,9 +45,10 @@ class TernaryMatrix(object):
     """One ternary tensor resident in HBM in the kt2 layout (2.125 bits per weight).
 
     bcodes: the reference pack's codes [C/4, R] (byte = d0 + 3 d1 + 9 d2 + 27 d3, convert.py:49-52);
-    dpm: its fp16 scales [C/128, R] as uint16 bits. Numpy arrays are uploaded; device tensors are used as they are."""
+    dpm: its fp16 scales [C/128, R] as uint16 bits. Numpy arrays are uploaded; device tensors are used as they are.
+    W: an optional uint8 device buffer (a slice of a larger pool) to pack into."""
 
-    def __init__(self, bcodes, dpm, R, C, device="cuda"):
+    def __init__(self, bcodes, dpm, R, C, device="cuda", W=None):
         lib = gpudrv.load()
         self.R, self.C = int(R), int(C)
         nbytes = lib.kt_tern_weight_bytes(self.R, self.C)
@@ -57,7 +58,9 @@ class TernaryMatrix(object):
         dp = _dev_u16(dpm, device).reshape(-1)
         if bc.numel() != self.R * self.C // 4 or dp.numel() != self.R * (self.C // 128):
             raise ValueError("pack arrays do not match %d x %d" % (R, C))
-        self.W = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        self.W = torch.empty(nbytes, dtype=torch.uint8, device=device) if W is None else W[:nbytes]
+        if self.W.numel() < nbytes or self.W.data_ptr() % 16:
+            raise ValueError("weight buffer too small or not 16-byte aligned")
         gpudrv.check(lib.kt_tern_pack(ptr(bc), ptr(dp), self.R, self.C, ptr(self.W), stream()), "kt_tern_pack")
 
     @property
