@@ -16,8 +16,9 @@ extern "C" __global__ void k_q8_pack(const uint8_t*, int, int, uint32_t*, uint16
 extern "C" __global__ void k_quant_tern(const float*, int, int, int, int8_t*, int, float*, int*);
 extern "C" __global__ void k_quant_q8(const float*, int, int, int, int8_t*, int, float*, int);
 extern "C" __global__ void k_tern_sum(const float*, float*, int, int, int);
-extern "C" __global__ void k_tern_gemm(const uint32_t*, const uint16_t*, int, int, const int8_t*, int, const float*,
-                                       int, float*, uint16_t*, int, int32_t*);
+template <bool DBG>
+__global__ void k_tern_gemm(const uint32_t*, const uint16_t*, int, int, const int8_t*, int, const float*, int, float*,
+                            uint16_t*, int, int32_t*);
 extern "C" __global__ void k_moe_topk(const float*, int, int, int*, float*);
 extern "C" __global__ void k_moe_sort(const int*, int, int, int*, int*, int*, int*, int*, int*, int);
 extern "C" __global__ void k_moe_combine(const float*, const float*, const int*, const float*, int, int, float*);
@@ -257,7 +258,9 @@ int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const f
   const uint32_t* codes = (const uint32_t*)W;
   const uint16_t* scales = (const uint16_t*)((const uint8_t*)W + kt_code_bytes(R, NG));
   const dim3 grid((R + 127) / 128, (M + 127) / 128);
-  hipLaunchKernelGGL(k_tern_gemm, grid, dim3(256), 0, kt_stream(stream), codes, scales, R, NG, XQ, ldq, XS, M,
+  if(dbg) hipLaunchKernelGGL(k_tern_gemm<true>, grid, dim3(256), 0, kt_stream(stream), codes, scales, R, NG, XQ, ldq, XS, M,
+                     Y, Y16, ldy, dbg);
+  else hipLaunchKernelGGL(k_tern_gemm<false>, grid, dim3(256), 0, kt_stream(stream), codes, scales, R, NG, XQ, ldq, XS, M,
                      Y, Y16, ldy, dbg);
   KT_LAUNCH_CHECK();
   return 0;

@@ -5,8 +5,10 @@
 
    Block: 256 threads (4 waves) own 128 tokens x 128 weight rows; wave (wt, wr) owns tokens 64 wt .., rows 64 wr ..
    as 2 x 2 MFMA tiles of 32 x 32. Per group: the block loads the 128 rows' packed trits (4 KB: one 16-byte load
-   per thread, 32 lines of 128 bytes of the kt2 layout), unpacks them to signed int8 once (shift, mask, v_perm byte lookup)
-   into LDS, stages the 128 tokens' int8 activations in LDS, and each wave runs 4 k-steps of 2 x 2 MFMAs. The
+   per thread, 32 lines of 128 bytes of the kt2 layout), unpacks them to signed int8 once (shift, mask, v_perm byte
+   lookup) into LDS, stages the 128 tokens' int8 activations in LDS, and each wave runs 4 k-steps of 2 x 2 MFMAs.
+   Two LDS stages: the loads of group g + 1 are issued before group g's products and unpacked into the other stage
+   after its epilogue, so one barrier a group separates the stages and the memory latency overlaps the products. The
    MFMA A operand is the activations (rows = tokens), B the weights (columns = weight rows), so a lane's 16
    accumulators share one weight row: its group scale is one register. After the group the int32 accumulators are
    scaled into fp32 accumulators in the reference expression and cleared.
@@ -26,13 +28,15 @@ typedef int kt_v16i __attribute__((ext_vector_type(16)));
 /* 4 digits (0/1/2, one per byte) -> 4 signed trits (-1/0/+1): byte lookup in 0x000100FF */
 __device__ __forceinline__ uint32_t kt_trits(uint32_t dig){ return __builtin_amdgcn_perm(0x000100FFu, 0x000100FFu, dig); }
 
-extern "C" __global__ void __launch_bounds__(256) k_tern_gemm(const uint32_t* __restrict__ codes,
+template <bool DBG>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k_tern_gemm(const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, int R, int NG, const int8_t* __restrict__ XQ, int ldq,
     const float* __restrict__ XS, int M, float* __restrict__ Y, uint16_t* __restrict__ Y16, int ldy,
     int32_t* __restrict__ dbg){
-  __shared__ __attribute__((aligned(16))) uint8_t Xl[PF_BT * PF_LD];
-  __shared__ __attribute__((aligned(16))) uint8_t Wl[PF_BR * PF_LD];
-  __shared__ float xs_l[PF_BT];
+  /* two LDS stages: group g's operands are read while group g + 1's are written; one barrier a group */
+  __shared__ __attribute__((aligned(16))) uint8_t Xl[2][PF_BT * PF_LD];
+  __shared__ __attribute__((aligned(16))) uint8_t Wl[2][PF_BR * PF_LD];
+  __shared__ float xs_l[2][PF_BT];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wt = wv >> 1, wr = wv & 1;
   const int r0 = blockIdx.x * PF_BR, n0 = blockIdx.y * PF_BT;
@@ -44,18 +48,46 @@ extern "C" __global__ void __launch_bounds__(256) k_tern_gemm(const uint32_t* __
   const int grg = (r0 >> 3) + lrg;
   const bool wvalid = grg < R8;
   const uint4* __restrict__ wsrc = (const uint4*)codes;
-  uint8_t* wdst = Wl + (lrg * 8 + lr) * PF_LD + lh * 64;
+  const int woff = (lrg * 8 + lr) * PF_LD + lh * 64;
 
   /* this thread's activation chunk: token tid/2, 64 bytes at (tid&1)*64 */
   const int xt = tid >> 1, xh = tid & 1;
   const bool xvalid = n0 + xt < M;
-  const int8_t* __restrict__ xsrc = XQ + (long long)(n0 + xt) * ldq + xh * 64;
-  uint8_t* xdst = Xl + xt * PF_LD + xh * 64;
+  const int8_t* __restrict__ xsrc = XQ + (long long)(n0 + (xvalid ? xt : 0)) * ldq + xh * 64;
+  const int xoff = xt * PF_LD + xh * 64;
 
   /* scales of this lane's two weight rows (columns of the 2 B tiles) */
   const int cr0 = r0 + wr * 64 + (lane & 31), cr1 = cr0 + 32;
   const int crg0 = cr0 >> 3, crg1 = cr1 >> 3;
   const bool c0v = (cr0 >> 3) < R8, c1v = (cr1 >> 3) < R8;
+
+  /* the global loads of one group (registers), then their unpack into LDS stage b */
+  struct Grp { uint4 wc; uint4 xv[4]; uint16_t h0, h1; float xs; };
+  auto load = [&](int g, Grp& q){
+    q.wc = wvalid ? kt_ldnt(wsrc + kt_widx(NG, grg, g >> 3, lh, g & 7, lr))
+                  : make_uint4(0x55555555u, 0x55555555u, 0x55555555u, 0x55555555u);
+#pragma unroll
+    for(int k = 0; k < 4; ++k) q.xv[k] = xvalid ? ((const uint4*)(xsrc + g * 128))[k] : make_uint4(0u, 0u, 0u, 0u);
+    q.h0 = c0v ? scales[kt_sidx(NG, crg0, g, cr0 & 7)] : (uint16_t)0;
+    q.h1 = c1v ? scales[kt_sidx(NG, crg1, g, cr1 & 7)] : (uint16_t)0;
+    q.xs = (tid < PF_BT && n0 + tid < M) ? XS[(long long)(n0 + tid) * NG + g] : 0.0f;
+  };
+  auto store = [&](const Grp& q, int b){
+    /* unpack: word j of the chunk = columns 16j .. +15 of the half; slot s = columns 16j + 4s .. +3 */
+    const uint32_t ww[4] = {q.wc.x, q.wc.y, q.wc.z, q.wc.w};
+#pragma unroll
+    for(int j = 0; j < 4; ++j){
+      uint4 o;
+      o.x = kt_trits(ww[j] & 0x03030303u);
+      o.y = kt_trits((ww[j] >> 2) & 0x03030303u);
+      o.z = kt_trits((ww[j] >> 4) & 0x03030303u);
+      o.w = kt_trits((ww[j] >> 6) & 0x03030303u);
+      *(uint4*)(Wl[b] + woff + 16 * j) = o;
+    }
+#pragma unroll
+    for(int k = 0; k < 4; ++k) *(uint4*)(Xl[b] + xoff + 16 * k) = q.xv[k];
+    if(tid < PF_BT) xs_l[b][tid] = q.xs;
+  };
 
   float acc[2][2][16];
 #pragma unroll
@@ -65,33 +97,14 @@ extern "C" __global__ void __launch_bounds__(256) k_tern_gemm(const uint32_t* __
 #pragma unroll
       for(int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
+  Grp cur, nxt;
+  load(0, cur);
+  store(cur, 0);
+  float d0 = kt_h2f(cur.h0), d1 = kt_h2f(cur.h1);
+  __syncthreads();
   for(int g = 0; g < NG; ++g){
-    /* global -> registers */
-    uint4 wc = make_uint4(0x55555555u, 0x55555555u, 0x55555555u, 0x55555555u);
-    if(wvalid) wc = kt_ldnt(wsrc + kt_widx(NG, grg, g >> 3, lh, g & 7, lr));   /* step g / 8, k-lane g % 8 */
-    uint4 xv[4];
-#pragma unroll
-    for(int k = 0; k < 4; ++k) xv[k] = xvalid ? ((const uint4*)(xsrc + g * 128))[k] : make_uint4(0u, 0u, 0u, 0u);
-    const float d0 = c0v ? kt_h2f(scales[kt_sidx(NG, crg0, g, cr0 & 7)]) : 0.0f;
-    const float d1 = c1v ? kt_h2f(scales[kt_sidx(NG, crg1, g, cr1 & 7)]) : 0.0f;
-
-    __syncthreads();                                          /* the previous group's operands are consumed */
-    /* unpack: word j of the chunk = columns 16j .. +15 of the half; slot s = columns 16j + 4s .. +3 */
-    const uint32_t ww[4] = {wc.x, wc.y, wc.z, wc.w};
-#pragma unroll
-    for(int j = 0; j < 4; ++j){
-      uint4 o;
-      o.x = kt_trits(ww[j] & 0x03030303u);
-      o.y = kt_trits((ww[j] >> 2) & 0x03030303u);
-      o.z = kt_trits((ww[j] >> 4) & 0x03030303u);
-      o.w = kt_trits((ww[j] >> 6) & 0x03030303u);
-      *(uint4*)(wdst + 16 * j) = o;
-    }
-#pragma unroll
-    for(int k = 0; k < 4; ++k) *(uint4*)(xdst + 16 * k) = xv[k];
-    if(tid < PF_BT) xs_l[tid] = n0 + tid < M ? XS[(long long)(n0 + tid) * NG + g] : 0.0f;
-    __syncthreads();
-
+    const int b = g & 1;
+    if(g + 1 < NG) load(g + 1, nxt);                          /* in flight during this group's products */
     kt_v16i c[2][2];
 #pragma unroll
     for(int i = 0; i < 2; ++i)
@@ -104,9 +117,9 @@ extern "C" __global__ void __launch_bounds__(256) k_tern_gemm(const uint32_t* __
       const int koff = ks * 32 + (lane >> 5) * 16;
       kt_v4i A[2], B[2];
 #pragma unroll
-      for(int i = 0; i < 2; ++i) A[i] = *(const kt_v4i*)(Xl + (wt * 64 + i * 32 + (lane & 31)) * PF_LD + koff);
+      for(int i = 0; i < 2; ++i) A[i] = *(const kt_v4i*)(Xl[b] + (wt * 64 + i * 32 + (lane & 31)) * PF_LD + koff);
 #pragma unroll
-      for(int j = 0; j < 2; ++j) B[j] = *(const kt_v4i*)(Wl + (wr * 64 + j * 32 + (lane & 31)) * PF_LD + koff);
+      for(int j = 0; j < 2; ++j) B[j] = *(const kt_v4i*)(Wl[b] + (wr * 64 + j * 32 + (lane & 31)) * PF_LD + koff);
 #pragma unroll
       for(int i = 0; i < 2; ++i)
 #pragma unroll
@@ -118,10 +131,10 @@ extern "C" __global__ void __launch_bounds__(256) k_tern_gemm(const uint32_t* __
 #pragma unroll
       for(int e = 0; e < 16; ++e){
         const int tl = wt * 64 + i * 32 + (e & 3) + 8 * (e >> 2) + 4 * (lane >> 5);
-        const float xs = xs_l[tl];
+        const float xs = xs_l[b][tl];
         acc[i][0][e] = fmaf((float)c[i][0][e], xs * d0, acc[i][0][e]);
         acc[i][1][e] = fmaf((float)c[i][1][e], xs * d1, acc[i][1][e]);
-        if(dbg){
+        if(DBG){
           const int t = n0 + tl;
           if(t < M){
             if(cr0 < R) dbg[((long long)t * R + cr0) * NG + g] = c[i][0][e];
@@ -129,6 +142,12 @@ extern "C" __global__ void __launch_bounds__(256) k_tern_gemm(const uint32_t* __
           }
         }
       }
+    if(g + 1 < NG){
+      store(nxt, b ^ 1);                                        /* stage b ^ 1 was last read in group g - 1 */
+      d0 = kt_h2f(nxt.h0);
+      d1 = kt_h2f(nxt.h1);
+    }
+    __syncthreads();
   }
   /* store: lanes of one register write 32 consecutive rows of one token */
 #pragma unroll
@@ -148,3 +167,8 @@ extern "C" __global__ void __launch_bounds__(256) k_tern_gemm(const uint32_t* __
       }
     }
 }
+
+template __global__ void k_tern_gemm<false>(const uint32_t*, const uint16_t*, int, int, const int8_t*, int, const float*,
+                                            int, float*, uint16_t*, int, int32_t*);
+template __global__ void k_tern_gemm<true>(const uint32_t*, const uint16_t*, int, int, const int8_t*, int, const float*,
+                                           int, float*, uint16_t*, int, int32_t*);
