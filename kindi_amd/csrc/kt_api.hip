@@ -6,11 +6,11 @@
 #include <vector>
 #include "../../include/kt.h"
 
-template <int FMT, int MT, bool DBG>
-__global__ void k_gemv_flat(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
+template <int FMT, int MT, bool DBG, bool GRP>
+__global__ void k_gemv_flat(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, const int*, int32_t*,
+                            int);
 template <int MT> __global__ void k_plan(const uint8_t*, unsigned*);
 extern "C" __global__ void k_plan_reset(unsigned*, int);
-template <int MT> __global__ void k_q8_grouped(const KtGroupedArgs, const int8_t*, const float*, float*, int32_t*);
 extern "C" __global__ void k_tern_pack(const uint8_t*, const uint16_t*, int, int, uint32_t*, uint16_t*);
 extern "C" __global__ void k_q8_pack(const uint8_t*, int, int, uint32_t*, uint16_t*);
 extern "C" __global__ void k_quant_tern(const float*, int, int, int, int8_t*, int, float*, int*);
@@ -47,9 +47,10 @@ static int kt_launch_gemv(const KtGemvArgs& a, int ngroups, const int8_t* xq, co
   int mt = a.M <= 1 ? 1 : a.M <= 2 ? 2 : 4;
   while(mt > 1 && (mt == 4 ? KtFlat<FMT, 4>::lds(ks) : KtFlat<FMT, 2>::lds(ks)) > 65536) mt >>= 1;
   const dim3 grid(ngroups), block(64 * ks);
+  const KtGroupedArgs ga = {};
 #define KT_F(MT) do { const size_t lds = KtFlat<FMT, MT>::lds(ks); \
-    if(dbg) hipLaunchKernelGGL((k_gemv_flat<FMT, MT, true>), grid, block, lds, s, a, xq, xs, xa, dbg, ks); \
-    else hipLaunchKernelGGL((k_gemv_flat<FMT, MT, false>), grid, block, lds, s, a, xq, xs, xa, dbg, ks); } while(0)
+    if(dbg) hipLaunchKernelGGL((k_gemv_flat<FMT, MT, true, false>), grid, block, lds, s, a, ga, xq, xs, xa, dbg, ks); \
+    else hipLaunchKernelGGL((k_gemv_flat<FMT, MT, false, false>), grid, block, lds, s, a, ga, xq, xs, xa, dbg, ks); } while(0)
   if(mt == 4) KT_F(4); else if(mt == 2) KT_F(2); else KT_F(1);
 #undef KT_F
   KT_LAUNCH_CHECK();
@@ -340,16 +341,24 @@ int kt_q8_grouped(const void* const* Wexp, int R, int C, int E, const int* cnt, 
   a.R = R; a.C = C; a.NU = C / 32;
   a.cnt = cnt; a.off = off; a.act = act; a.nact = nact; a.xrow = xrow;
   a.ldq = ldq; a.ldd = ldd; a.ldy = ldy;
-  const int mt = M <= 1 ? 1 : M <= 4 ? 4 : M <= 8 ? 8 : 16;    /* an expert's list holds at most M tokens */
+  a.y = Y;
+  /* the decode product per (row group, active expert), the expert's list in chunks of up to 4 tokens */
+  const int ks = kt_kslices(a.NU);
+#ifndef KT_GRP_MT
+#define KT_GRP_MT 2                   /* tokens a chunk in the grouped product (registers: more waves resident) */
+#endif
+  int mt = M <= 1 ? 1 : M <= 2 ? 2 : 4;
+  if(mt > KT_GRP_MT) mt = KT_GRP_MT;
+  while(mt > 1 && (mt == 4 ? KtFlat<KT_FMT_Q8, 4>::lds(ks) : KtFlat<KT_FMT_Q8, 2>::lds(ks)) > 65536) mt >>= 1;
   const int ny = E < nentries ? E : nentries;
-  const dim3 grid(kt_r8(R), ny), block(64);
+  const dim3 grid(kt_r8(R), ny), block(64 * ks);
+  const KtGemvArgs da = {};
   hipStream_t s = kt_stream(stream);
-  switch(mt){
-    case 1: hipLaunchKernelGGL(k_q8_grouped<1>, grid, block, 0, s, a, Q, D, Y, dbg); break;
-    case 4: hipLaunchKernelGGL(k_q8_grouped<4>, grid, block, 0, s, a, Q, D, Y, dbg); break;
-    case 8: hipLaunchKernelGGL(k_q8_grouped<8>, grid, block, 0, s, a, Q, D, Y, dbg); break;
-    default: hipLaunchKernelGGL(k_q8_grouped<16>, grid, block, 0, s, a, Q, D, Y, dbg); break;
-  }
+#define KT_G(MT) do { const size_t lds = KtFlat<KT_FMT_Q8, MT>::lds(ks); \
+    if(dbg) hipLaunchKernelGGL((k_gemv_flat<KT_FMT_Q8, MT, true, true>), grid, block, lds, s, da, a, Q, D, nullptr, dbg, ks); \
+    else hipLaunchKernelGGL((k_gemv_flat<KT_FMT_Q8, MT, false, true>), grid, block, lds, s, da, a, Q, D, nullptr, dbg, ks); } while(0)
+  if(mt == 4) KT_G(4); else if(mt == 2) KT_G(2); else KT_G(1);
+#undef KT_G
   KT_LAUNCH_CHECK();
   return 0;
 }

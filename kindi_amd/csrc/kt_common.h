@@ -135,4 +135,5 @@ struct KtGroupedArgs {
   const int* act; const int* nact;    /* active experts (ascending) and their count */
   const int* xrow;                    /* nullable: input row of list entry p (else p itself) */
   int ldq, ldd, ldy, pad2;
+  float* y;                           /* output rows [entries][ldy] */
 };

@@ -83,26 +83,47 @@ __device__ __forceinline__ void kt_wave_sync(){
   __builtin_amdgcn_wave_barrier();
 }
 
-template <int FMT, int MT, bool DBG>
-__global__ void __launch_bounds__(64 * KT_KSMAX) k_gemv_flat(const KtGemvArgs a, const int8_t* __restrict__ xq,
+template <int FMT, int MT, bool DBG, bool GRP>
+__global__ void __launch_bounds__(64 * KT_KSMAX) k_gemv_flat(const KtGemvArgs a, const KtGroupedArgs ga,
+                                                             const int8_t* __restrict__ xq,
                                                              const float* __restrict__ xs, const int* __restrict__ xa,
                                                              int32_t* __restrict__ dbg, int KS){
   extern __shared__ __attribute__((aligned(16))) uint8_t kt_lds[];
   using F = KtFlat<FMT, MT>;
   constexpr int UW = F::UW, UP = F::UP, SL = KT_SL;
-  const int NU = a.NU, S = kt_steps(NU);
+  const int NU = GRP ? ga.NU : a.NU, S = kt_steps(NU);
   const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), r = lane & 7, c = lane >> 3;
   const int g = blockIdx.x;
-  int mi = 0;
-  if(a.nmat > 1 && g >= a.mat[1].rg0) mi = 1;
-  if(a.nmat > 2 && g >= a.mat[2].rg0) mi = 2;
-  const KtMat& m = a.mat[mi];
-  const int rg = g - m.rg0, row = rg * KT_RG + r;
+  /* the job of this block: a matrix's row group and its token rows. Dense: row group g of the launch's matrices,
+     tokens 0 .. M - 1, output row t. Grouped (MoE): row group g of active expert act[blockIdx.y], the tokens of its
+     list (entries off .. off + cnt - 1, input row xrow[p] or p), output row = entry p. */
+  const uint4* __restrict__ wb;
+  const uint16_t* __restrict__ sb;
+  float* yout;
+  int R, ldy, rg, M, p0, ldq, ldxs;
+  const int* xrow = nullptr;
+  if(GRP){
+    if((int)blockIdx.y >= *ga.nact) return;
+    const int e = ga.act[blockIdx.y];
+    const uint8_t* base = ga.wexp[e];
+    wb = (const uint4*)base;
+    sb = (const uint16_t*)(base + (long long)kt_r8(ga.R) * NU * 256);
+    R = ga.R; ldy = ga.ldy; rg = g; M = ga.cnt[e]; p0 = ga.off[e]; xrow = ga.xrow; ldq = ga.ldq; ldxs = ga.ldd;
+    yout = ga.y;
+  } else {
+    int mi = 0;
+    if(a.nmat > 1 && g >= a.mat[1].rg0) mi = 1;
+    if(a.nmat > 2 && g >= a.mat[2].rg0) mi = 2;
+    const KtMat& m = a.mat[mi];
+    wb = (const uint4*)m.codes;
+    sb = m.scales;
+    R = m.R; ldy = m.ldy; rg = g - m.rg0; M = a.M; p0 = 0; ldq = a.ldq; ldxs = a.ldxs;
+    yout = m.y;
+  }
+  const int row = rg * KT_RG + r;
   const int s_lo = ks * S / KS, ns = (ks + 1) * S / KS - s_lo;      /* this slice's steps (>= 1) */
   uint8_t* xw = kt_lds + (size_t)ks * F::XW;                         /* [MT][SL][8][UP] */
   float* red = (float*)(kt_lds + (size_t)KS * F::XW);                /* [KS][MT][8] */
-  const uint4* __restrict__ wb = (const uint4*)m.codes;
-  const uint16_t* __restrict__ sb = m.scales;
   const bool one = ns <= SL;                                         /* wave-uniform */
 
   KtStep w[SL];
@@ -127,8 +148,8 @@ __global__ void __launch_bounds__(64 * KT_KSMAX) k_gemv_flat(const KtGemvArgs a,
   };
   if(one) load_w(0);
 
-  for(int t0 = 0; t0 < a.M; t0 += MT){
-    const int nt = min(MT, a.M - t0);
+  for(int t0 = 0; t0 < M; t0 += MT){
+    const int nt = min(MT, M - t0);
     float acc[MT];
 #pragma unroll
     for(int t = 0; t < MT; ++t) acc[t] = 0.0f;
@@ -144,11 +165,11 @@ __global__ void __launch_bounds__(64 * KT_KSMAX) k_gemv_flat(const KtGemvArgs a,
         const int nc = NU - s * KT_KL < KT_KL ? NU - s * KT_KL : KT_KL;
 #pragma unroll
         for(int t = 0; t < MT; ++t){
-          const int n = t0 + (t < nt ? t : 0);
-          sa[0][j][t] = __float_as_uint(xs[(long long)n * a.ldxs + uu]);
-          sa[1][j][t] = FMT == KT_FMT_TERN ? (uint32_t)xa[(long long)n * a.ldxs + uu] : 0u;
+          const int pe = p0 + t0 + (t < nt ? t : 0), n = xrow ? xrow[pe] : pe;
+          sa[0][j][t] = __float_as_uint(xs[(long long)n * ldxs + uu]);
+          sa[1][j][t] = FMT == KT_FMT_TERN ? (uint32_t)xa[(long long)n * ldxs + uu] : 0u;
           const int oc = o < nc * UW ? o : 0;
-          stg[j][t] = *(const uint4*)(xq + (long long)n * a.ldq + (long long)s * KT_KL * UW + oc);
+          stg[j][t] = *(const uint4*)(xq + (long long)n * ldq + (long long)s * KT_KL * UW + oc);
         }
       }
       kt_pin<SL * MT>(&stg[0][0], &sa[0][0][0]);                                  /* every load above is issued before a write */
@@ -174,7 +195,7 @@ __global__ void __launch_bounds__(64 * KT_KSMAX) k_gemv_flat(const KtGemvArgs a,
               int v = kt_unit_lds<FMT>(w[j].c0, w[j].c1, xw + ((t * SL + j) * KT_KL + (uok ? c : 0)) * UP) - (int)sa[1][j][t];
               v = uok ? v : 0;
               acc[t] = fmaf((float)v, FMT == KT_FMT_TERN ? __uint_as_float(sa[0][j][t]) * d : d * __uint_as_float(sa[0][j][t]), acc[t]);
-              if(DBG && uok && row < m.R) dbg[((long long)(t0 + t) * m.R + row) * NU + u] = v;
+              if(DBG && uok && row < R) dbg[((long long)(p0 + t0 + t) * R + row) * NU + u] = v;
             }
           }
         }
@@ -194,7 +215,7 @@ __global__ void __launch_bounds__(64 * KT_KSMAX) k_gemv_flat(const KtGemvArgs a,
       for(int t = 0; t < MT; ++t){
         float v = red[t * 8 + r];
         for(int k = 1; k < KS; ++k) v += red[(k * MT + t) * 8 + r];
-        if(t < nt && row < m.R) m.y[(long long)(t0 + t) * m.ldy + row] = v;
+        if(t < nt && row < R) yout[(long long)(p0 + t0 + t) * ldy + row] = v;
       }
     }
     __syncthreads();

@@ -151,7 +151,14 @@ def test_moe_forward_config4(kt, M):
     assert np.array_equal(host(dbg)[p], acc)
     dq = np.ascontiguousarray(up_rows[e].reshape(F, H // 32, 34)[:, :, :2].copy().view(np.float16)[..., 0]
                               .astype(np.float32).T)
-    assert np.array_equal(host(Y)[p], orc.out_lanes(acc, d[xrow[p]], dq, 8, 1, 1))   # one K slice per wave
+    KS = lib.kt_decode_kslices(H, 1)
+    assert np.array_equal(host(Y)[p], orc.out_lanes(acc, d[xrow[p]], dq, 8, 1, KS))   # the q8_0 decode tree
+    # and every expert's rows equal the dense q8_0 product of the same tokens (one kernel, one tree)
+    for e in np.nonzero(cnt)[0][:8]:
+        p = np.arange(off[e], off[e] + cnt[e])
+        dense = moe.Q8Matrix(up_rows[e], F, H).gemv(st["xq"][torch.from_numpy(xrow[p]).cuda().long()],
+                                                    st["xd"][torch.from_numpy(xrow[p]).cuda().long()])
+        assert np.array_equal(host(dense).view(np.uint32), host(Y)[p].view(np.uint32)), e
 
 
 def test_combine_bit_exact(kt):
