@@ -9,6 +9,9 @@
 template <int FMT, int MT, bool DBG, bool GRP>
 __global__ void k_gemv_flat(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, const int*, int32_t*,
                             int);
+template <int FMT, int MT, bool DBG, bool GRP>
+__global__ void k_gemv_flat1(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, const int*, int32_t*,
+                             int);
 template <int MT> __global__ void k_plan(const uint8_t*, unsigned*);
 extern "C" __global__ void k_plan_reset(unsigned*, int);
 extern "C" __global__ void k_tern_pack(const uint8_t*, const uint16_t*, int, int, uint32_t*, uint16_t*);
@@ -48,10 +51,10 @@ static int kt_launch_gemv(const KtGemvArgs& a, int ngroups, const int8_t* xq, co
   while(mt > 1 && (mt == 4 ? KtFlat<FMT, 4>::lds(ks) : KtFlat<FMT, 2>::lds(ks)) > 65536) mt >>= 1;
   const dim3 grid(ngroups), block(64 * ks);
   const KtGroupedArgs ga = {};
-#define KT_F(MT) do { const size_t lds = KtFlat<FMT, MT>::lds(ks); \
-    if(dbg) hipLaunchKernelGGL((k_gemv_flat<FMT, MT, true, false>), grid, block, lds, s, a, ga, xq, xs, xa, dbg, ks); \
-    else hipLaunchKernelGGL((k_gemv_flat<FMT, MT, false, false>), grid, block, lds, s, a, ga, xq, xs, xa, dbg, ks); } while(0)
-  if(mt == 4) KT_F(4); else if(mt == 2) KT_F(2); else KT_F(1);
+#define KT_F(K, MT) do { const size_t lds = KtFlat<FMT, MT>::lds(ks); \
+    if(dbg) hipLaunchKernelGGL((K<FMT, MT, true, false>), grid, block, lds, s, a, ga, xq, xs, xa, dbg, ks); \
+    else hipLaunchKernelGGL((K<FMT, MT, false, false>), grid, block, lds, s, a, ga, xq, xs, xa, dbg, ks); } while(0)
+  if(mt == 4) KT_F(k_gemv_flat, 4); else if(mt == 2) KT_F(k_gemv_flat, 2); else KT_F(k_gemv_flat1, 1);
 #undef KT_F
   KT_LAUNCH_CHECK();
   return 0;
@@ -354,10 +357,10 @@ int kt_q8_grouped(const void* const* Wexp, int R, int C, int E, const int* cnt, 
   const dim3 grid(kt_r8(R), ny), block(64 * ks);
   const KtGemvArgs da = {};
   hipStream_t s = kt_stream(stream);
-#define KT_G(MT) do { const size_t lds = KtFlat<KT_FMT_Q8, MT>::lds(ks); \
-    if(dbg) hipLaunchKernelGGL((k_gemv_flat<KT_FMT_Q8, MT, true, true>), grid, block, lds, s, da, a, Q, D, nullptr, dbg, ks); \
-    else hipLaunchKernelGGL((k_gemv_flat<KT_FMT_Q8, MT, false, true>), grid, block, lds, s, da, a, Q, D, nullptr, dbg, ks); } while(0)
-  if(mt == 4) KT_G(4); else if(mt == 2) KT_G(2); else KT_G(1);
+#define KT_G(K, MT) do { const size_t lds = KtFlat<KT_FMT_Q8, MT>::lds(ks); \
+    if(dbg) hipLaunchKernelGGL((K<KT_FMT_Q8, MT, true, true>), grid, block, lds, s, da, a, Q, D, nullptr, dbg, ks); \
+    else hipLaunchKernelGGL((K<KT_FMT_Q8, MT, false, true>), grid, block, lds, s, da, a, Q, D, nullptr, dbg, ks); } while(0)
+  if(mt == 4) KT_G(k_gemv_flat, 4); else if(mt == 2) KT_G(k_gemv_flat, 2); else KT_G(k_gemv_flat1, 1);
 #undef KT_G
   KT_LAUNCH_CHECK();
   return 0;

@@ -84,10 +84,9 @@ __device__ __forceinline__ void kt_wave_sync(){
 }
 
 template <int FMT, int MT, bool DBG, bool GRP>
-__global__ void __launch_bounds__(64 * KT_KSMAX) k_gemv_flat(const KtGemvArgs a, const KtGroupedArgs ga,
-                                                             const int8_t* __restrict__ xq,
-                                                             const float* __restrict__ xs, const int* __restrict__ xa,
-                                                             int32_t* __restrict__ dbg, int KS){
+__device__ __forceinline__ void kt_gemv_flat_body(const KtGemvArgs& a, const KtGroupedArgs& ga,
+                                                  const int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                                  const int* __restrict__ xa, int32_t* __restrict__ dbg, int KS){
   extern __shared__ __attribute__((aligned(16))) uint8_t kt_lds[];
   using F = KtFlat<FMT, MT>;
   constexpr int UW = F::UW, UP = F::UP, SL = KT_SL;
@@ -220,4 +219,19 @@ __global__ void __launch_bounds__(64 * KT_KSMAX) k_gemv_flat(const KtGemvArgs a,
     }
     __syncthreads();
   }
+}
+
+/* one token a chunk: held to 64 VGPRs (8 waves a SIMD), so three 9-wave blocks fit a CU and the widest products
+   run in one round of blocks */
+template <int FMT, int MT, bool DBG, bool GRP>
+__global__ void __launch_bounds__(64 * KT_KSMAX) __attribute__((amdgpu_waves_per_eu(8)))
+k_gemv_flat1(const KtGemvArgs a, const KtGroupedArgs ga, const int8_t* __restrict__ xq, const float* __restrict__ xs,
+             const int* __restrict__ xa, int32_t* __restrict__ dbg, int KS){
+  kt_gemv_flat_body<FMT, MT, DBG, GRP>(a, ga, xq, xs, xa, dbg, KS);
+}
+template <int FMT, int MT, bool DBG, bool GRP>
+__global__ void __launch_bounds__(64 * KT_KSMAX)
+k_gemv_flat(const KtGemvArgs a, const KtGroupedArgs ga, const int8_t* __restrict__ xq, const float* __restrict__ xs,
+            const int* __restrict__ xa, int32_t* __restrict__ dbg, int KS){
+  kt_gemv_flat_body<FMT, MT, DBG, GRP>(a, ga, xq, xs, xa, dbg, KS);
 }
