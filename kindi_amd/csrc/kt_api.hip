@@ -12,6 +12,8 @@ __global__ void k_gemv_flat(const KtGemvArgs, const KtGroupedArgs, const int8_t*
 template <int FMT, int MT, bool DBG, bool GRP>
 __global__ void k_gemv_flat1(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, const int*, int32_t*,
                              int);
+template <int NT, bool DBG>
+__global__ void k_gemv_mma(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
 template <int MT> __global__ void k_plan(const uint8_t*, unsigned*);
 extern "C" __global__ void k_plan_reset(unsigned*, int);
 extern "C" __global__ void k_tern_pack(const uint8_t*, const uint16_t*, int, int, uint32_t*, uint16_t*);
@@ -42,10 +44,27 @@ static int kt_kslices(int NU){
   return ks < KT_KSMAX ? ks : KT_KSMAX;
 }
 
+/* 5 .. 32 ternary tokens: the matrix-core product (the same numbers and tree), tiles of 32 rows of one matrix,
+   passes of 16 tokens */
+#define KT_MMA_MIN 5
+#define KT_MMA_MAX 32
+static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, int32_t* dbg, hipStream_t s){
+  const int ks = kt_kslices(a.NU);
+  int tiles = 0;
+  for(int i = 0; i < a.nmat; ++i){ a.mat[i].pad = tiles; tiles += (kt_r8(a.mat[i].R) + 3) / 4; }
+  const dim3 grid(tiles, (a.M + 15) / 16), block(64 * ks);
+  const size_t lds = (size_t)ks * 16 * 32 * 4;
+  if(dbg) hipLaunchKernelGGL((k_gemv_mma<16, true>), grid, block, lds, s, a, xq, xs, dbg, ks);
+  else hipLaunchKernelGGL((k_gemv_mma<16, false>), grid, block, lds, s, a, xq, xs, dbg, ks);
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
 /* one block per row group, every token in the launch (chunks of MT tokens whose staging fits in 64 KB of LDS) */
 template <int FMT>
 static int kt_launch_gemv(const KtGemvArgs& a, int ngroups, const int8_t* xq, const float* xs, const int* xa,
                           int32_t* dbg, hipStream_t s){
+  if(FMT == KT_FMT_TERN && a.M >= KT_MMA_MIN && a.M <= KT_MMA_MAX) return kt_launch_mma(a, xq, xs, dbg, s);
   const int ks = kt_kslices(a.NU);
   int mt = a.M <= 1 ? 1 : a.M <= 2 ? 2 : 4;
   while(mt > 1 && (mt == 4 ? KtFlat<FMT, 4>::lds(ks) : KtFlat<FMT, 2>::lds(ks)) > 65536) mt >>= 1;

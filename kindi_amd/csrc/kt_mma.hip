@@ -1,0 +1,144 @@
+/* kt_mma.hip - the decode product on the matrix cores for 5 .. 32 tokens (passes of 16) (k_tc_mv*, tc_hip.cu:180-240, at
+   the verify widths spec.py:45 takes them): ternary weights (kt2) against int8 token rows, the same numbers and the
+   same summation tree as k_gemv_flat, so a token's bits do not depend on which of the two kernels ran it.
+
+   Block: KS waves over one tile of 32 weight rows (4 row groups of one matrix); wave ks takes the K slice ks (steps
+   [ks S / KS, (ks + 1) S / KS), at most 2); grid.y the passes of 16 tokens. A unit (128 columns) is 4
+   V_MFMA_I32_32X32X32_I8 (token rows 16 .. 31 of the A operand are zero): lane l holds weight row l % 32 (B operand)
+   and token l % 32 (A operand), both for the columns 64 h + 16 i .. + 15 of the unit in
+   MFMA i (h = l / 32), so the 4 MFMAs cover the unit's 128 columns once each and give its exact int32 value
+   v(t, r) (any pairing of columns gives the same integer). A lane's kt2 load is exactly its row's 64 columns of
+   the unit (kt_widx with half h), unpacked to signed trits (shift, mask, v_perm byte lookup); its activations are
+   the same 64 columns of its token, read from L2 (tokens past M are zero and not loaded).
+
+   The fp32 epilogue takes k_gemv_flat's order: for each k-lane c (0..7) of the step layout, the chain over the
+   slice's units 8 s + c in increasing s, fmaf((float)v, XS[t][u] * d[r][u], .); then ((c0 + c1) + (c2 + c3)) +
+   ((c4 + c5) + (c6 + c7)) (the xor butterfly's result) in registers; then the slices in order, in LDS. D register
+   layout (32x32x32 i8 on gfx950): lane l register e holds column l % 32 (the weight row) and row (e % 4) + 8 (e / 4)
+   + 4 (l / 32) (the token). */
+#include "kt_gemv.h"
+
+typedef int kt_v4i __attribute__((ext_vector_type(4)));
+typedef int kt_v16i __attribute__((ext_vector_type(16)));
+
+#define KM_ROWS 32                    /* weight rows a tile */
+#define KM_TOK 16                     /* tokens a pass */
+
+/* 4 digits (0/1/2, one per byte) -> 4 signed trits (-1/0/+1): byte lookup in 0x000100FF */
+__device__ __forceinline__ int km_trits(uint32_t dig){ return (int)__builtin_amdgcn_perm(0x000100FFu, 0x000100FFu, dig); }
+
+/* the token of D register e of lane l */
+__device__ __forceinline__ int km_tok(int e, int lane){ return (e & 3) + 8 * (e >> 2) + 4 * (lane >> 5); }
+
+template <int NT, bool DBG>   /* NT: the token rows of a pass (16: D registers e < 8) */
+__global__ void __launch_bounds__(64 * KT_KSMAX) k_gemv_mma(const KtGemvArgs a, const int8_t* __restrict__ xq,
+                                                            const float* __restrict__ xs,
+                                                            int32_t* __restrict__ dbg, int KS){
+  constexpr int NE = NT / 2;                                     /* D registers that hold used tokens */
+  extern __shared__ __attribute__((aligned(16))) uint8_t kt_lds[];
+  float* red = (float*)kt_lds;                                   /* [KS][NT][32] slice sums */
+  const int NU = a.NU, S = kt_steps(NU);
+  const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = lane >> 5, lr = lane & 31;
+  const int tile = blockIdx.x, t0 = blockIdx.y * KM_TOK;
+  int mi = 0;
+  if(a.nmat > 1 && tile >= a.mat[1].pad) mi = 1;
+  if(a.nmat > 2 && tile >= a.mat[2].pad) mi = 2;
+  const KtMat& m = a.mat[mi];
+  const int rg = (tile - m.pad) * 4 + (lr >> 3), r = lr & 7, row = rg * KT_RG + r;
+  const bool rok = row < m.R;
+  const int nt = min(KM_TOK, a.M - t0);
+  const int tok = t0 + lr;                                        /* this lane's A row (token) */
+  const bool tok_ok = lr < nt;
+  const int s_lo = ks * S / KS, ns = (ks + 1) * S / KS - s_lo;   /* this slice's steps (1 or 2) */
+  const uint4* __restrict__ wb = (const uint4*)m.codes;
+  const uint16_t* __restrict__ sb = m.scales;
+
+  float part[NE];                                                  /* the combined chains of this slice */
+  float t01[NE], t23[NE], t45[NE], pend[NE];
+#pragma unroll
+  for(int e = 0; e < NE; ++e){ part[e] = 0.0f; t01[e] = 0.0f; t23[e] = 0.0f; t45[e] = 0.0f; pend[e] = 0.0f; }
+
+  /* the slice's 16 units in k-lane-major order (c, then the two steps), fully unrolled with unconditional loads
+     (a unit past the slice or the matrix reads offset 0 and a zero token), so loads run ahead of their products */
+  uint4 wq[2][KT_KL];
+  uint16_t hq[2][KT_KL];
+#pragma unroll
+  for(int c = 0; c < KT_KL; ++c)
+#pragma unroll
+    for(int j = 0; j < 2; ++j){
+      const int s = s_lo + j, u = s * KT_KL + c;
+      const bool ok = rok && j < ns && u < NU;
+      wq[j][c] = kt_ldnt(wb + (ok ? kt_widx(NU, rg, s, h, c, r) : 0));
+      hq[j][c] = sb[ok ? kt_sidx(NU, rg, u, r) : 0];
+    }
+#pragma unroll
+  for(int c = 0; c < KT_KL; ++c){
+    float chain[NE];
+#pragma unroll
+    for(int e = 0; e < NE; ++e) chain[e] = 0.0f;
+#pragma unroll
+    for(int j = 0; j < 2; ++j){
+      const int s = s_lo + j, u = s * KT_KL + c;
+      const bool uok = j < ns && u < NU;                        /* wave-uniform */
+      const int uu = uok ? u : 0;
+      /* A: this lane's token, the unit's columns 64 h .. 64 h + 63 */
+      uint4 xa4[4];
+      const uint4* xp = (const uint4*)(xq + (long long)(tok_ok ? tok : t0) * a.ldq + (long long)uu * 128 + 64 * h);
+#pragma unroll
+      for(int i = 0; i < 4; ++i) xa4[i] = xp[i];
+      if(uok){
+        const uint32_t ww[4] = {wq[j][c].x, wq[j][c].y, wq[j][c].z, wq[j][c].w};
+        const float d = rok ? kt_h2f(hq[j][c]) : 0.0f;
+        kt_v16i acc;
+#pragma unroll
+        for(int e = 0; e < 16; ++e) acc[e] = 0;
+#pragma unroll
+        for(int i = 0; i < 4; ++i){
+          kt_v4i B, A;
+          B[0] = km_trits(ww[i] & 0x03030303u);
+          B[1] = km_trits((ww[i] >> 2) & 0x03030303u);
+          B[2] = km_trits((ww[i] >> 4) & 0x03030303u);
+          B[3] = km_trits((ww[i] >> 6) & 0x03030303u);
+          A[0] = tok_ok ? (int)xa4[i].x : 0; A[1] = tok_ok ? (int)xa4[i].y : 0;
+          A[2] = tok_ok ? (int)xa4[i].z : 0; A[3] = tok_ok ? (int)xa4[i].w : 0;
+          acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, acc, 0, 0, 0);
+        }
+        /* epilogue: the k-lane chain, fmaf((float)v, XS * d, .) */
+#pragma unroll
+        for(int e = 0; e < NE; ++e){
+          const int t = t0 + km_tok(e, lane);
+          const int tc = t < a.M ? t : t0;
+          const float sx = xs[(long long)tc * a.ldxs + u];
+          chain[e] = fmaf((float)acc[e], sx * d, chain[e]);
+          if(DBG && t < a.M && rok) dbg[((long long)t * m.R + row) * NU + u] = acc[e];
+        }
+      }
+    }
+    /* the butterfly's tree over c, as it completes */
+#pragma unroll
+    for(int e = 0; e < NE; ++e){
+      if(c == 0 || c == 2 || c == 4 || c == 6) pend[e] = chain[e];
+      else if(c == 1) t01[e] = pend[e] + chain[e];
+      else if(c == 3) t23[e] = t01[e] + (pend[e] + chain[e]);          /* (c0 + c1) + (c2 + c3) */
+      else if(c == 5) t45[e] = pend[e] + chain[e];
+      else part[e] = t23[e] + (t45[e] + (pend[e] + chain[e]));          /* ... + ((c4 + c5) + (c6 + c7)) */
+    }
+  }
+  /* slices in order */
+#pragma unroll
+  for(int e = 0; e < NE; ++e) red[((size_t)ks * NT + km_tok(e, lane)) * 32 + lr] = part[e];
+  __syncthreads();
+  if(ks == 0){
+#pragma unroll
+    for(int e = 0; e < NE; ++e){
+      const int tl = km_tok(e, lane), t = t0 + tl;
+      float v = red[(size_t)tl * 32 + lr];
+      for(int k = 1; k < KS; ++k) v += red[((size_t)k * NT + tl) * 32 + lr];
+      if(t < a.M && rok) m.y[(long long)t * m.ldy + row] = v;
+    }
+  }
+}
+
+template __global__ void k_gemv_mma<16, false>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
+template __global__ void k_gemv_mma<16, true>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
