@@ -1,0 +1,525 @@
+/* kt_api.hip - the C ABI of libkt_gfx950.so: host-side validation and launches. Every entry point takes
+   caller-owned device pointers and a stream (NULL = the null stream), never allocates, never synchronizes, and
+   returns a hipError_t as int (0 = success; hipErrorInvalidValue for shapes or strides the kernels do not take).
+   The declarations and the reference interfaces they replace are in include/kt.h. */
+#include "kt_common.h"
+#include <vector>
+#include <cstring>
+#include <climits>
+#include "../../include/kt.h"
+
+template <int FMT, int MT, bool DBG, bool GRP>
+__global__ void k_gemv_flat(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, const int*, int32_t*,
+                            int);
+template <int FMT, int MT, bool DBG, bool GRP>
+__global__ void k_gemv_flat1(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, const int*, int32_t*,
+                             int);
+template <int NT, bool DBG>
+__global__ void k_gemv_mma(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
+template <int MT> __global__ void k_plan(const uint8_t*, unsigned*);
+extern "C" __global__ void k_plan_reset(unsigned*, int);
+extern "C" __global__ void k_tern_pack(const uint8_t*, const uint16_t*, int, int, uint32_t*, uint16_t*);
+extern "C" __global__ void k_q8_pack(const uint8_t*, int, int, uint32_t*, uint16_t*);
+extern "C" __global__ void k_quant_tern(const float*, int, int, int, int8_t*, int, float*, int*);
+extern "C" __global__ void k_quant_q8(const float*, int, int, int, int8_t*, int, float*, int);
+extern "C" __global__ void k_tern_sum(const float*, float*, int, int, int);
+template <bool DBG>
+__global__ void k_tern_gemm(const uint32_t*, const uint16_t*, int, int, const int8_t*, int, const float*, int, float*,
+                            uint16_t*, int, int32_t*);
+extern "C" __global__ void k_moe_topk(const float*, int, int, int*, float*);
+extern "C" __global__ void k_moe_sort(const int*, int, int, int*, int*, int*, int*, int*, int*, int);
+extern "C" __global__ void k_moe_combine(const float*, const float*, const int*, const float*, int, int, float*);
+
+#define KT_INVALID ((int)hipErrorInvalidValue)
+#define KT_LAUNCH_CHECK() do { const hipError_t _e = hipGetLastError(); if(_e != hipSuccess) return (int)_e; } while(0)
+
+static inline hipStream_t kt_stream(void* s){ return (hipStream_t)s; }
+static inline bool kt_al(const void* p, size_t a){ return ((uintptr_t)p % a) == 0; }
+/* bytes of a matrix's codes and scales (both layouts: 32 bytes and one fp16 per row and unit, rows padded to 8) */
+static inline size_t kt_code_bytes(int R, int NU){ return (size_t)kt_r8(R) * NU * 256; }
+static inline size_t kt_scale_bytes(int R, int NU){ return (size_t)kt_r8(R) * NU * 16; }
+/* K slices of a decode product: a function of the step count S = ceil(units / 8) only (never of M or R), so a
+   token's result does not depend on how many tokens share the pass, and a matrix gives the same bits alone or in a
+   multi-matrix launch: slices of at most KT_SL steps, at most KT_KSMAX of them */
+static int kt_kslices(int NU){
+  const int S = kt_steps(NU), ks = (S + KT_SL - 1) / KT_SL;
+  return ks < KT_KSMAX ? ks : KT_KSMAX;
+}
+
+/* 5 .. 32 ternary tokens: the matrix-core product (the same numbers and tree), tiles of 32 rows of one matrix,
+   passes of 16 tokens */
+#define KT_MMA_MIN 5
+#define KT_MMA_MAX 32
+static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, int32_t* dbg, hipStream_t s){
+  const int ks = kt_kslices(a.NU);
+  int tiles = 0;
+  for(int i = 0; i < a.nmat; ++i){ a.mat[i].pad = tiles; tiles += (kt_r8(a.mat[i].R) + 3) / 4; }
+  const dim3 grid(tiles, (a.M + 15) / 16), block(64 * ks);
+  const size_t lds = (size_t)ks * 16 * 32 * 4;
+  if(dbg) hipLaunchKernelGGL((k_gemv_mma<16, true>), grid, block, lds, s, a, xq, xs, dbg, ks);
+  else hipLaunchKernelGGL((k_gemv_mma<16, false>), grid, block, lds, s, a, xq, xs, dbg, ks);
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
+/* one block per row group, every token in the launch (chunks of MT tokens whose staging fits in 64 KB of LDS) */
+template <int FMT>
+static int kt_launch_gemv(const KtGemvArgs& a, int ngroups, const int8_t* xq, const float* xs, const int* xa,
+                          int32_t* dbg, hipStream_t s){
+  if(FMT == KT_FMT_TERN && a.M >= KT_MMA_MIN && a.M <= KT_MMA_MAX) return kt_launch_mma(a, xq, xs, dbg, s);
+  const int ks = kt_kslices(a.NU);
+  int mt = a.M <= 1 ? 1 : a.M <= 2 ? 2 : 4;
+  while(mt > 1 && (mt == 4 ? KtFlat<FMT, 4>::lds(ks) : KtFlat<FMT, 2>::lds(ks)) > 65536) mt >>= 1;
+  const dim3 grid(ngroups), block(64 * ks);
+  const KtGroupedArgs ga = {};
+#define KT_F(K, MT) do { const size_t lds = KtFlat<FMT, MT>::lds(ks); \
+    if(dbg) hipLaunchKernelGGL((K<FMT, MT, true, false>), grid, block, lds, s, a, ga, xq, xs, xa, dbg, ks); \
+    else hipLaunchKernelGGL((K<FMT, MT, false, false>), grid, block, lds, s, a, ga, xq, xs, xa, dbg, ks); } while(0)
+  if(mt == 4) KT_F(k_gemv_flat, 4); else if(mt == 2) KT_F(k_gemv_flat, 2); else KT_F(k_gemv_flat1, 1);
+#undef KT_F
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
+static int kt_tern_gemv_n(int nmat, const void* const* W, const int* Rs, float* const* Ys, const int* ldys, int C,
+                          const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M, int32_t* dbg,
+                          void* stream){
+  if(M == 0) return 0;
+  if(M < 0 || C <= 0 || C % 128 || !XQ || !XS || !XA || ldq < C || ldq % 16 || !kt_al(XQ, 16)) return KT_INVALID;
+  KtGemvArgs a = {};
+  const int NG = C / 128;
+  int groups = 0;
+  for(int i = 0; i < nmat; ++i){
+    if(!W[i] || !Ys[i] || Rs[i] <= 0 || ldys[i] < Rs[i] || !kt_al(W[i], 16)) return KT_INVALID;
+    a.mat[i].codes = (const uint32_t*)W[i];
+    a.mat[i].scales = (const uint16_t*)((const uint8_t*)W[i] + kt_code_bytes(Rs[i], NG));
+    a.mat[i].y = Ys[i];
+    a.mat[i].R = Rs[i];
+    a.mat[i].ldy = ldys[i];
+    a.mat[i].rg0 = groups;
+    groups += kt_r8(Rs[i]);
+  }
+  if(dbg && nmat != 1) return KT_INVALID;
+  a.nmat = nmat;
+  a.NU = NG;
+  a.ldq = ldq;
+  a.ldxs = NG;
+  a.M = M;
+  return kt_launch_gemv<KT_FMT_TERN>(a, groups, XQ, XS, (const int*)XA, dbg, kt_stream(stream));
+}
+
+extern "C" {
+
+int kt_version(void){ return KT_VERSION; }
+
+int kt_init(int device){ return (int)hipSetDevice(device); }
+
+const char* kt_error_string(int rc){ return hipGetErrorString((hipError_t)rc); }
+
+/* ------------------------------------------------------------------ ternary weights */
+size_t kt_tern_weight_bytes(int R, int C){
+  if(R <= 0 || C <= 0 || C % 128) return 0;
+  return kt_code_bytes(R, C / 128) + kt_scale_bytes(R, C / 128);
+}
+
+int kt_tern_pack(const uint8_t* bcodes, const uint16_t* dpm, int R, int C, void* W, void* stream){
+  if(!bcodes || !dpm || !W || R <= 0 || C <= 0 || C % 128 || !kt_al(W, 16)) return KT_INVALID;
+  const int NG = C / 128;
+  uint32_t* codes = (uint32_t*)W;
+  uint16_t* scales = (uint16_t*)((uint8_t*)W + kt_code_bytes(R, NG));
+  const long long nw = (long long)kt_code_bytes(R, NG) / 4;
+  hipLaunchKernelGGL(k_tern_pack, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, kt_stream(stream),
+                     bcodes, dpm, R, C, codes, scales);
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
+int kt_quant_q8(const float* X, int ldx, int M, int C, int per_row, int8_t* XQ, int ldq, float* XS, int32_t* XA,
+                void* stream){
+  if(M == 0) return 0;
+  if(!X || !XQ || !XS || !XA || M < 0 || C <= 0 || C % 128 || ldx < C || ldq < C || ldx % 2 || ldq % 16
+     || !kt_al(X, 8) || !kt_al(XQ, 16)) return KT_INVALID;
+  hipLaunchKernelGGL(k_quant_tern, dim3(M), dim3(256), 0, kt_stream(stream), X, ldx, C, per_row ? 1 : 0, XQ, ldq,
+                     XS, (int*)XA);
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
+/* ------------------------------------------------------------------ decode products */
+int kt_decode_kslices(int C, int q8){
+  if(C <= 0 || C % (q8 ? 32 : 128)) return 0;
+  return kt_kslices(q8 ? C / 32 : C / 128);
+}
+
+int kt_tern_gemv(const void* W, int R, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M,
+                 float* Y, int ldy, int32_t* dbg, void* stream){
+  const void* w[1] = {W};
+  const int r[1] = {R}, l[1] = {ldy};
+  float* y[1] = {Y};
+  return kt_tern_gemv_n(1, w, r, y, l, C, XQ, ldq, XS, XA, M, dbg, stream);
+}
+
+int kt_tern_gemv3(const void* W0, int R0, float* Y0, const void* W1, int R1, float* Y1, const void* W2, int R2,
+                  float* Y2, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M,
+                  void* stream){
+  const void* w[3] = {W0, W1, W2};
+  const int r[3] = {R0, R1, R2};
+  float* y[3] = {Y0, Y1, Y2};
+  const int n = R1 <= 0 ? 1 : R2 <= 0 ? 2 : 3;
+  return kt_tern_gemv_n(n, w, r, y, r, C, XQ, ldq, XS, XA, M, NULL, stream);
+}
+
+int kt_tern_sum(const float* P, float* y, int R, int M, int sp, void* stream){
+  if(M == 0) return 0;
+  if(!P || !y || R <= 0 || M < 0 || sp <= 0) return KT_INVALID;
+  const long long n = (long long)R * M;
+  hipLaunchKernelGGL(k_tern_sum, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, kt_stream(stream), P, y, R, M, sp);
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
+/* ------------------------------------------------------------------ decode plan */
+/* the stages of a plan checked and described (matrices, units, slices, row groups, coherent inputs) */
+static int kt_plan_stages(const kt_stage* st, int n, std::vector<KtPStage>& S, int& NUX){
+  if(!st || n <= 0 || n > 4095) return KT_INVALID;
+  S.assign(n, KtPStage());
+  const int M = st[0].M;
+  NUX = 0;
+  for(int s = 0; s < n; ++s){
+    const kt_stage& x = st[s];
+    if(x.M != M || M < 1 || M > 4 || x.C <= 0 || x.C % 128 || !x.XQ || !x.XS || !x.XA || x.ldq < x.C ||
+       x.ldq % 16 || !kt_al(x.XQ, 16)) return KT_INVALID;
+    const int NU = x.C / 128;
+    if(NU > 240) return KT_INVALID;                              /* C <= 30720 */
+    KtPStage& d = S[s];
+    memset(&d, 0, sizeof(d));
+    int groups = 0, nmat = 0;
+    for(int i = 0; i < 3 && x.R[i] > 0; ++i){
+      if(!x.W[i] || !x.Y[i] || !kt_al(x.W[i], 16)) return KT_INVALID;
+      if(kt_code_bytes(x.R[i], NU) > (size_t)INT_MAX) return KT_INVALID;   /* scale offsets are 32-bit */
+      d.mat[i].codes = (const uint32_t*)x.W[i];
+      d.mat[i].scales = (const uint16_t*)((const uint8_t*)x.W[i] + kt_code_bytes(x.R[i], NU));
+      d.mat[i].y = x.Y[i];
+      d.mat[i].R = x.R[i];
+      d.mat[i].ldy = x.R[i];
+      d.mat[i].rg0 = groups;
+      groups += kt_r8(x.R[i]);
+      ++nmat;
+    }
+    if(!nmat) return KT_INVALID;
+    d.nmat = nmat; d.NU = NU; d.KS = kt_kslices(NU); d.ngroups = groups; d.S = kt_steps(NU);
+    d.xq = x.XQ; d.xs = x.XS; d.xa = (const int*)x.XA; d.ldq = x.ldq; d.ldxs = NU; d.M = M;
+    /* inputs that overlap an output of an earlier stage are read with coherent loads, after the barrier */
+    const uintptr_t in[3][2] = {{(uintptr_t)x.XQ, (uintptr_t)x.XQ + (size_t)(M - 1) * x.ldq + x.C},
+                                {(uintptr_t)x.XS, (uintptr_t)x.XS + (size_t)M * NU * 4},
+                                {(uintptr_t)x.XA, (uintptr_t)x.XA + (size_t)M * NU * 4}};
+    d.coh = 0;
+    for(int p = 0; p < s && !d.coh; ++p)
+      for(int i = 0; i < 3 && st[p].R[i] > 0; ++i){
+        const uintptr_t y0 = (uintptr_t)st[p].Y[i], y1 = y0 + (size_t)M * st[p].R[i] * 4;
+        for(int q = 0; q < 3; ++q) if(in[q][0] < y1 && y0 < in[q][1]) d.coh = 1;
+      }
+    if(NU > NUX) NUX = NU;
+  }
+  return 0;
+}
+
+static int kt_plan_grid(int* G){
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if(e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if(e != hipSuccess) return (int)e;
+  if(cus <= 0 || cus > KT_PLAN_MAXG) return KT_INVALID;
+  *G = cus;                                                      /* one block per CU */
+  return 0;
+}
+
+/* records of a data wave: its steps, then padding (stage = nstages) to a whole window of 8 and four more windows
+   (the ring and the record windows read up to 31 records past the first padding record) */
+static size_t kt_plan_pad(size_t steps){ return ((steps + 1 + 7) / 8 + 4) * 8; }
+
+size_t kt_plan_bytes(const kt_stage* stages, int nstages){
+  std::vector<KtPStage> S;
+  int NUX = 0, G = 0;
+  if(kt_plan_stages(stages, nstages, S, NUX) || kt_plan_grid(&G)) return 0;
+  size_t steps = 0;
+  for(const KtPStage& x : S) steps += (size_t)x.ngroups * x.S;
+  /* a wave's share differs from the mean by less than a few tasks; bound it by the total plus the padding */
+  return kt_plan_rec_off(nstages) + (steps + (size_t)G * KT_PLAN_WAVES * 64) * 16;
+}
+
+/* the plan image for G blocks (host memory): header, stages, row tables, record index, zeroed barrier words, records.
+   Also returns what the launch needs (tokens a pass, activation buffers, LDS bytes). */
+static int kt_plan_image(const kt_stage* st, int n, int G, std::vector<uint8_t>& buf, int* mt_out, size_t* lds_out){
+  std::vector<KtPStage> S;
+  int NUX = 0, rc = kt_plan_stages(st, n, S, NUX);
+  if(rc) return rc;
+  if(G <= 0 || G > KT_PLAN_MAXG) return KT_INVALID;
+  const int M = S[0].M, W = KT_PLAN_WAVES;
+  /* the deal: per stage, block b takes row groups p, p + G, ... (p = (b - off) mod G); its (row group, slice)
+     tasks go to its data waves in turn, continuing from the previous stage's deal */
+  std::vector<std::vector<uint4>> recs((size_t)G * W);
+  std::vector<int> woff(G, 0);
+  std::vector<KtPCtl> ctl(n);
+  int off = 0, red = 0;
+  for(int s = 0; s < n; ++s){
+    KtPStage& x = S[s];
+    x.off = off;
+    KtPCtl& c = ctl[s];
+    memset(&c, 0, sizeof(c));
+    for(int i = 0; i < KT_MAXMAT; ++i){
+      c.y[i] = i < x.nmat ? x.mat[i].y : x.mat[0].y;
+      c.R[i] = i < x.nmat ? x.mat[i].R : 0;
+    }
+    c.rg1 = x.nmat > 1 ? x.mat[1].rg0 : INT_MAX;
+    c.rg2 = x.nmat > 2 ? x.mat[2].rg0 : INT_MAX;
+    c.KS = x.KS; c.off = off; c.ngroups = x.ngroups; c.coh = x.coh;
+    const int KS = x.KS, NU = x.NU;
+    for(int b = 0; b < G; ++b){
+      int p = b - off;
+      if(p < 0) p += G;
+      const int cnt = p < x.ngroups ? (x.ngroups - 1 - p) / G + 1 : 0;
+      if(cnt * KS > red) red = cnt * KS;
+      for(int t = 0; t < cnt * KS; ++t){
+        const int rgk = t / KS, ks = t % KS, rg = p + rgk * G;
+        const int mi = rg >= c.rg2 ? 2 : rg >= c.rg1 ? 1 : 0;
+        const KtMat& m = x.mat[mi];
+        const int lrg = rg - m.rg0, slo = ks * x.S / KS, ns = (ks + 1) * x.S / KS - slo;
+        std::vector<uint4>& L = recs[(size_t)b * W + (woff[b] + t) % W];
+        for(int j = 0; j < ns; ++j){
+          const int sp = slo + j, nc = NU - sp * KT_KL < KT_KL ? NU - sp * KT_KL : KT_KL;
+          const uintptr_t code = (uintptr_t)m.codes + (uintptr_t)kt_widx(NU, lrg, sp, 0, 0, 0) * 16;
+          const uintptr_t scal = (uintptr_t)m.scales + (uintptr_t)kt_sidx(NU, lrg, sp * KT_KL, 0) * 2;
+          const long long so = (long long)scal - (long long)code;
+          if(so < INT_MIN || so > INT_MAX) return KT_INVALID;
+          const unsigned bits = (unsigned)sp | (unsigned)(nc - 1) << 5 | (j == 0 ? 0x100u : 0u) |
+                                (j == ns - 1 ? 0x200u : 0u) | (unsigned)t << 10 | (unsigned)s << 20;
+          L.push_back(make_uint4((unsigned)code, (unsigned)((uint64_t)code >> 32), (unsigned)(int)so, bits));
+        }
+      }
+      woff[b] = (woff[b] + cnt * KS) % W;
+    }
+    off = (off + x.ngroups) % G;
+  }
+  if(red > 1024) return KT_INVALID;                              /* slice-sum slots are 10 bits */
+  size_t total = 0, steps = 0;
+  for(const auto& L : recs) total += kt_plan_pad(L.size());
+  for(const KtPStage& x : S) steps += (size_t)x.ngroups * x.S;
+  if(total > steps + (size_t)G * W * 64) return KT_INVALID;      /* what kt_plan_bytes promises */
+  const int mt = M <= 1 ? 1 : M <= 2 ? 2 : 4;
+  const size_t per = (size_t)mt * NUX * (144 + 8);               /* one activation buffer */
+  const size_t rb = (size_t)red * mt * 8 * 4;
+  const size_t cap = 160 * 1024;
+  const size_t tab = 64 + (size_t)n * sizeof(KtPCtl);           /* flags, row tables */
+  const int nb = tab + 2 * per + rb <= cap ? 2 : 1;
+  if(tab + nb * per + rb > cap) return KT_INVALID;
+  const size_t need = tab + nb * per + rb;                       /* + activations, slice sums */
+  *lds_out = need > 81 * 1024 ? need : 81 * 1024;                /* at least 81 KB: one block per CU */
+  *mt_out = mt;
+  const size_t roff = kt_plan_rec_off(n);
+  buf.assign(roff + total * 16, 0);
+  KtPlanHdr* H = (KtPlanHdr*)buf.data();
+  H->nstages = n; H->G = G; H->W = W; H->MT = mt; H->NB = nb; H->NUX = NUX; H->RED = red; H->M = M;
+  memcpy(buf.data() + KT_PLAN_HDR, S.data(), (size_t)n * sizeof(KtPStage));
+  memcpy(buf.data() + kt_plan_ctl_off(n), ctl.data(), (size_t)n * sizeof(KtPCtl));
+  unsigned* idx = (unsigned*)(buf.data() + kt_plan_idx_off(n));
+  uint4* R = (uint4*)(buf.data() + roff);
+  const uintptr_t dummy = (uintptr_t)S[0].mat[0].codes;
+  size_t at = 0;
+  for(size_t v = 0; v < recs.size(); ++v){
+    if(at > 0xFFFFFFFFu) return KT_INVALID;
+    idx[v] = (unsigned)at;
+    const auto& L = recs[v];
+    for(size_t i = 0; i < kt_plan_pad(L.size()); ++i)
+      R[at + i] = i < L.size() ? L[i] : make_uint4((unsigned)dummy, (unsigned)((uint64_t)dummy >> 32), 0u,
+                                                   (unsigned)n << 20);
+    at += kt_plan_pad(L.size());
+  }
+  return 0;
+}
+
+int kt_plan_layout(const kt_stage* st, int n, int G, void* out, size_t cap, size_t* used){
+  if(!used) return KT_INVALID;
+  std::vector<uint8_t> buf;
+  int mt = 0;
+  size_t lds = 0;
+  const int rc = kt_plan_image(st, n, G, buf, &mt, &lds);
+  if(rc) return rc;
+  *used = buf.size();
+  if(out){
+    if(cap < buf.size()) return KT_INVALID;
+    memcpy(out, buf.data(), buf.size());
+  }
+  return 0;
+}
+
+int kt_plan_build(const kt_stage* st, int n, void* plan, kt_plan_info* info, void* stream){
+  if(!plan || !info || !kt_al(plan, 256)) return KT_INVALID;
+  int G = 0, rc = kt_plan_grid(&G);
+  if(rc) return rc;
+  std::vector<uint8_t> buf;
+  int mt = 0;
+  size_t lds = 0;
+  if((rc = kt_plan_image(st, n, G, buf, &mt, &lds))) return rc;
+  const void* k = mt == 1 ? (const void*)k_plan<1> : mt == 2 ? (const void*)k_plan<2> : (const void*)k_plan<4>;
+  hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  int occ = 0;
+  if(e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k, 64 * (KT_PLAN_WAVES + 1), lds);
+  if(e != hipSuccess) return (int)e;
+  if(occ < 1) return KT_INVALID;
+  e = hipMemcpyAsync(plan, buf.data(), buf.size(), hipMemcpyHostToDevice, kt_stream(stream));
+  if(e == hipSuccess) e = hipStreamSynchronize(kt_stream(stream));
+  if(e != hipSuccess) return (int)e;
+  info->nstages = n; info->grid = G; info->waves = KT_PLAN_WAVES; info->mt = mt; info->lds = lds;
+  return 0;
+}
+
+int kt_plan_run(const void* plan, const kt_plan_info* info, void* stream){
+  if(!plan || !info || info->nstages <= 0 || info->grid <= 0 || info->waves != KT_PLAN_WAVES) return KT_INVALID;
+  hipStream_t s = kt_stream(stream);
+  unsigned* ctr = (unsigned*)((uint8_t*)plan + kt_plan_ctr_off(info->nstages));
+  hipLaunchKernelGGL(k_plan_reset, dim3(1), dim3(256), 0, s, ctr, (int)KT_BAR_WORDS);
+  const dim3 grid(info->grid), block(64 * (info->waves + 1));
+  const uint8_t* p = (const uint8_t*)plan;
+  if(info->mt == 1) hipLaunchKernelGGL(k_plan<1>, grid, block, info->lds, s, p, ctr);
+  else if(info->mt == 2) hipLaunchKernelGGL(k_plan<2>, grid, block, info->lds, s, p, ctr);
+  else hipLaunchKernelGGL(k_plan<4>, grid, block, info->lds, s, p, ctr);
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
+int kt_plan_status(const void* plan, const kt_plan_info* info, int* status, void* stream){
+  if(!plan || !info || !status || info->nstages <= 0) return KT_INVALID;
+  unsigned v = 0;
+  const uint8_t* p = (const uint8_t*)plan + kt_plan_ctr_off(info->nstages) + (size_t)KT_BAR_STATUS * 32 * 4;
+  hipError_t e = hipMemcpyAsync(&v, p, 4, hipMemcpyDeviceToHost, kt_stream(stream));
+  if(e == hipSuccess) e = hipStreamSynchronize(kt_stream(stream));
+  *status = (int)v;
+  return (int)e;
+}
+
+/* ------------------------------------------------------------------ prefill product */
+int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M,
+                 float* Y, uint16_t* Y16, int ldy, int32_t* dbg, void* stream){
+  (void)XA;                                                  /* signed trits on the matrix cores: no digit offset */
+  if(M == 0) return 0;
+  if(!W || !XQ || !XS || (!Y && !Y16) || R <= 0 || M < 0 || C <= 0 || C % 128 || ldq < C || ldq % 16 || ldy < R
+     || !kt_al(W, 16) || !kt_al(XQ, 16)) return KT_INVALID;
+  const int NG = C / 128;
+  const uint32_t* codes = (const uint32_t*)W;
+  const uint16_t* scales = (const uint16_t*)((const uint8_t*)W + kt_code_bytes(R, NG));
+  const dim3 grid((R + 127) / 128, (M + 127) / 128);
+  if(dbg) hipLaunchKernelGGL(k_tern_gemm<true>, grid, dim3(256), 0, kt_stream(stream), codes, scales, R, NG, XQ, ldq, XS, M,
+                     Y, Y16, ldy, dbg);
+  else hipLaunchKernelGGL(k_tern_gemm<false>, grid, dim3(256), 0, kt_stream(stream), codes, scales, R, NG, XQ, ldq, XS, M,
+                     Y, Y16, ldy, dbg);
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
+/* ------------------------------------------------------------------ q8_0 */
+size_t kt_q8_weight_bytes(int R, int C){
+  if(R <= 0 || C <= 0 || C % 32) return 0;
+  return kt_code_bytes(R, C / 32) + kt_scale_bytes(R, C / 32);
+}
+
+int kt_q8_pack(const uint8_t* rows, int R, int C, void* W, void* stream){
+  if(!rows || !W || R <= 0 || C <= 0 || C % 32 || !kt_al(W, 16)) return KT_INVALID;
+  const int NB = C / 32;
+  uint32_t* codes = (uint32_t*)W;
+  uint16_t* scales = (uint16_t*)((uint8_t*)W + kt_code_bytes(R, NB));
+  const long long nw = (long long)kt_code_bytes(R, NB) / 4;
+  hipLaunchKernelGGL(k_q8_pack, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, kt_stream(stream), rows, R, C,
+                     codes, scales);
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
+int kt_q8_quant(const float* X, int ldx, int M, int C, int act, int8_t* Q, int ldq, float* D, int ldd, void* stream){
+  if(M == 0) return 0;
+  if(!X || !Q || !D || M < 0 || C <= 0 || C % 32 || ldx < C || ldq < C || ldd < C / 32) return KT_INVALID;
+  const int NB = C / 32;
+  hipLaunchKernelGGL(k_quant_q8, dim3((NB + 7) / 8, M), dim3(256), 0, kt_stream(stream), X, ldx, C, act ? 1 : 0, Q,
+                     ldq, D, ldd);
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
+int kt_q8_gemv(const void* W, int R, int C, const int8_t* Q, int ldq, const float* D, int ldd, int M, float* Y,
+               int ldy, int32_t* dbg, void* stream){
+  if(M == 0) return 0;
+  if(!W || !Q || !D || !Y || R <= 0 || M < 0 || C <= 0 || C % 32 || ldq < C || ldq % 16 || ldd < C / 32 || ldy < R
+     || !kt_al(W, 16) || !kt_al(Q, 16)) return KT_INVALID;
+  const int NB = C / 32;
+  KtGemvArgs a = {};
+  a.mat[0].codes = (const uint32_t*)W;
+  a.mat[0].scales = (const uint16_t*)((const uint8_t*)W + kt_code_bytes(R, NB));
+  a.mat[0].y = Y; a.mat[0].R = R; a.mat[0].ldy = ldy; a.mat[0].rg0 = 0;
+  a.nmat = 1; a.NU = NB;
+  a.ldq = ldq; a.ldxs = ldd;
+  a.M = M;
+  return kt_launch_gemv<KT_FMT_Q8>(a, kt_r8(R), Q, D, NULL, dbg, kt_stream(stream));
+}
+
+/* ------------------------------------------------------------------ MoE */
+int kt_moe_topk(const float* logits, int M, int E, int k, int* ids, float* gw, void* stream){
+  if(M == 0) return 0;
+  if(!logits || !ids || !gw || M < 0 || E <= 0 || E > 1024 || k <= 0 || k > 16 || k > E) return KT_INVALID;
+  hipLaunchKernelGGL(k_moe_topk, dim3(M), dim3(64), 0, kt_stream(stream), logits, E, k, ids, gw);
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
+int kt_moe_sort(const int* ids, int M, int k, int E, int* cnt, int* off, int* xrow, int* where, int* act, int* nact,
+                void* stream){
+  if(!ids || !cnt || !off || !xrow || !where || !act || !nact || M < 0 || k <= 0 || E <= 0 || E > 1024) return KT_INVALID;
+  hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(1024), 0, kt_stream(stream), ids, M * k, E, cnt, off, xrow, where, act,
+                     nact, k);
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
+int kt_q8_grouped(const void* const* Wexp, int R, int C, int E, const int* cnt, const int* off, const int* act,
+                  const int* nact, const int* xrow, int nentries, int M, const int8_t* Q, int ldq, const float* D,
+                  int ldd, float* Y, int ldy, int32_t* dbg, void* stream){
+  if(nentries == 0) return 0;
+  if(!Wexp || !cnt || !off || !act || !nact || !Q || !D || !Y || R <= 0 || C <= 0 || C % 32 || E <= 0
+     || nentries < 0 || M <= 0 || ldq < C || ldq % 16 || ldd < C / 32 || ldy < R || !kt_al(Q, 16))
+    return KT_INVALID;
+  KtGroupedArgs a = {};
+  a.wexp = (const uint8_t* const*)Wexp;
+  a.R = R; a.C = C; a.NU = C / 32;
+  a.cnt = cnt; a.off = off; a.act = act; a.nact = nact; a.xrow = xrow;
+  a.ldq = ldq; a.ldd = ldd; a.ldy = ldy;
+  a.y = Y;
+  /* the decode product per (row group, active expert), the expert's list in chunks of up to 4 tokens */
+  const int ks = kt_kslices(a.NU);
+#ifndef KT_GRP_MT
+#define KT_GRP_MT 2                   /* tokens a chunk in the grouped product (registers: more waves resident) */
+#endif
+  int mt = M <= 1 ? 1 : M <= 2 ? 2 : 4;
+  if(mt > KT_GRP_MT) mt = KT_GRP_MT;
+  while(mt > 1 && (mt == 4 ? KtFlat<KT_FMT_Q8, 4>::lds(ks) : KtFlat<KT_FMT_Q8, 2>::lds(ks)) > 65536) mt >>= 1;
+  const int ny = E < nentries ? E : nentries;
+  const dim3 grid(kt_r8(R), ny), block(64 * ks);
+  const KtGemvArgs da = {};
+  hipStream_t s = kt_stream(stream);
+#define KT_G(K, MT) do { const size_t lds = KtFlat<KT_FMT_Q8, MT>::lds(ks); \
+    if(dbg) hipLaunchKernelGGL((K<KT_FMT_Q8, MT, true, true>), grid, block, lds, s, da, a, Q, D, nullptr, dbg, ks); \
+    else hipLaunchKernelGGL((K<KT_FMT_Q8, MT, false, true>), grid, block, lds, s, da, a, Q, D, nullptr, dbg, ks); } while(0)
+  if(mt == 4) KT_G(k_gemv_flat, 4); else if(mt == 2) KT_G(k_gemv_flat, 2); else KT_G(k_gemv_flat1, 1);
+#undef KT_G
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
+int kt_moe_combine(const float* yd, const float* ysh, const int* where, const float* gw, int M, int k, int cols,
+                   float* x, void* stream){
+  if(M == 0) return 0;
+  if(!yd || !where || !gw || !x || M < 0 || k <= 0 || cols <= 0) return KT_INVALID;
+  hipLaunchKernelGGL(k_moe_combine, dim3(M), dim3(256), 0, kt_stream(stream), yd, ysh, where, gw, k, cols, x);
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
+}  /* extern "C" */

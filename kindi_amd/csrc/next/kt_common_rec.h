@@ -1,0 +1,164 @@
+/* kt_common.h - device layouts and shared helpers of the gfx950 quantized linear-layer library.
+
+   Weights are stored per matrix in one buffer: codes, then scales. Rows are padded to a multiple of 8 (a "row
+   group", one wave of a decode product; padding rows hold zero weights and scales). The K units (ternary:
+   128-column groups; q8_0: 32-column blocks) are taken 8 at a time (a "step": the 8 lanes that share a row take 8
+   consecutive units); the last step holds only the units that exist (nc = min(8, NU - 8 s)), so a matrix is
+   exactly 32 bytes of codes and 2 bytes of scale per row and unit.
+
+   Ternary ("kt2", 2 bits + 1/8 bit per weight, the reference pack's 2.125 b/w):
+     codes  u32 [R8][S][2][nc][8][4]  row group rg, step s, half h (columns 64h .. 64h+63 of a unit), k-lane c,
+                                      row r, word j: unit u = 8 s + c, row 8 rg + r, columns 128 u + 64 h + 16 j ..
+                                      +15; inside a word, byte b bits 2k..2k+1 hold the digit d = t + 1 in {0,1,2}
+                                      of column 16 j + 4 k + b, so (word >> 2k) & 0x03030303 is the digit vector of
+                                      four consecutive columns (activation word 4 j + k of the half)
+     scales fp16 [R8][NU][8]          per unit and row
+   A wave (lane = 8 c + r) reads a (rg, s, h) with one 16-byte load per lane: 1 KB contiguous (full steps).
+
+   q8_0 ("kq8", 8 bits + 1/2 bit per weight, GGUF Q8_0's 1.0625 B/w):
+     codes  i8  [R8][S][2][nc][8][16] as above with 32-column units, half h = columns 16 h .. 16 h + 15
+     scales fp16 [R8][NU][8]
+
+   Activations are int8 in natural column order, row-major [M][ldq] (ldq a multiple of 16).
+   Ternary: XS f32 / XA i32 [M][NG] per 128-column group. q8_0: D f32 [M][ldd] per 32-column block. */
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#define KT_RG 8                       /* rows per row group (one decode wave) */
+#define KT_KL 8                       /* lanes along K per row = units per step */
+#define KT_MAXMAT 3                   /* matrices sharing one input in a launch (q/k/v, gate/up) */
+
+enum { KT_FMT_TERN = 0, KT_FMT_Q8 = 1 };
+
+/* the one-round-trip decode product (kt_flat.h): slice length and LDS sizes */
+#ifndef KT_SL
+#define KT_SL 2                       /* steps of a K slice (one register set per step) */
+#endif
+#define KT_KSMAX 16                   /* waves per block */
+
+template <int FMT, int MT>
+struct KtFlat {
+  static constexpr int UW = FMT == KT_FMT_TERN ? 128 : 32;   /* bytes of a unit's activations */
+  static constexpr int UP = UW + 16;                         /* staged stride (the 8 units of a read on other banks) */
+  static constexpr int XW = MT * KT_SL * KT_KL * UP + 16;    /* one wave's staging (+ a dump slot) */
+  static size_t lds(int ks){ return (size_t)ks * XW + (size_t)ks * MT * 8 * 4; }
+};
+
+
+__host__ __device__ __forceinline__ int kt_r8(int R){ return (R + KT_RG - 1) / KT_RG; }
+__host__ __device__ __forceinline__ int kt_steps(int NU){ return (NU + KT_KL - 1) / KT_KL; }
+/* 16-byte index of (row group rg, step s, half h, k-lane c, row r) in a matrix with NU units */
+__host__ __device__ __forceinline__ long long kt_widx(int NU, int rg, int s, int h, int c, int r){
+  const int nc = NU - s * KT_KL < KT_KL ? NU - s * KT_KL : KT_KL;
+  return (long long)rg * NU * 16 + (long long)s * 128 + (h * nc + c) * 8 + r;
+}
+/* index of the fp16 scale of (rg, unit u, row r) */
+__host__ __device__ __forceinline__ long long kt_sidx(int NU, int rg, int u, int r){ return ((long long)rg * NU + u) * 8 + r; }
+
+__device__ __forceinline__ float kt_h2f(uint16_t h){ return __half2float(__ushort_as_half(h)); }
+
+typedef unsigned int kt_u32x4 __attribute__((ext_vector_type(4)));
+/* a streaming 128-bit load (each weight byte is read once per product: keep it out of the caches' way) */
+__device__ __forceinline__ uint4 kt_ldnt(const uint4* p){
+  const kt_u32x4 v = __builtin_nontemporal_load((const kt_u32x4*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+/* global-memory (address space 1) views: pointers read from memory (a plan's tables) are generic to the compiler,
+   and generic loads are FLAT instructions, which also count against the LDS wait counter */
+#define KT_G __attribute__((address_space(1)))
+__device__ __forceinline__ uint4 kt_ldnt_g(const void* p){
+  const kt_u32x4 v = __builtin_nontemporal_load((const KT_G kt_u32x4*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+template <typename T>
+__device__ __forceinline__ T kt_ldg(const void* p){ return *(const KT_G T*)p; }
+__device__ __forceinline__ uint4 kt_ldg4(const void* p){
+  const kt_u32x4 v = *(const KT_G kt_u32x4*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+template <typename T>
+__device__ __forceinline__ void kt_stg(void* p, T v){ *(KT_G T*)p = v; }
+
+__device__ __forceinline__ int kt_dot4(int a, int b, int c){ return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+/* one matrix of a decode launch: its weights, output and the first global row group it owns */
+struct KtMat {
+  const uint32_t* codes;
+  const uint16_t* scales;
+  float* y;
+  int R, ldy, rg0, pad;
+};
+
+struct KtGemvArgs {
+  KtMat mat[KT_MAXMAT];
+  int nmat, NU;                       /* matrices; units (groups / blocks) along C */
+  int ldq, ldxs;                      /* activation row stride (bytes); xs / xa row stride (units) */
+  int M, pad;                         /* tokens */
+};
+
+/* a decode plan in device memory: header, stages, then the stage counters and the status word */
+struct KtPStage {
+  KtMat mat[KT_MAXMAT];
+  const int8_t* xq;
+  const float* xs;
+  const int* xa;
+  int nmat, NU, KS, ngroups;          /* matrices, units along C, K slices, row groups of all matrices */
+  int S, off;                         /* steps along C; block that takes the stage's first row group */
+  int ldq, ldxs, M, coh;              /* coh: the inputs overlap an earlier stage's outputs */
+};
+struct KtPlanHdr {
+  int nstages, G, W, MT;              /* stages, blocks, data waves a block, tokens a pass */
+  int NB, NUX, RED, M;                /* activation buffers (1 or 2), units a staged row, slice sums a block, tokens */
+  int pad[8];
+};
+/* a stage as the plan's control wave reduces it (the table is copied to LDS at launch) */
+struct KtPCtl {
+  float* y[KT_MAXMAT];                /* outputs [M][R_i] */
+  int R[KT_MAXMAT];
+  int rg1, rg2;                       /* first row group of matrices 1 and 2 (INT_MAX when absent) */
+  int KS, off, ngroups, coh;          /* K slices; block that takes row group 0; row groups; inputs read coherently */
+  int pad;
+};
+static_assert(sizeof(KtPCtl) == 64, "KtPCtl is 64 bytes");
+#define KT_PLAN_HDR 64
+#define KT_PLAN_WAVES 8               /* data waves of a plan block */
+#define KT_PLAN_MAXG 1024             /* blocks (CUs) a plan can use */
+/* plan layout: header, stages, row tables, record index [G x KT_PLAN_WAVES] (first record of each data wave), barrier
+   words, then the step records (16 bytes each) */
+__host__ __device__ __forceinline__ size_t kt_r256(size_t n){ return (n + 255) / 256 * 256; }
+__host__ __device__ __forceinline__ size_t kt_plan_ctl_off(int nstages){
+  return kt_r256((size_t)KT_PLAN_HDR + (size_t)nstages * sizeof(KtPStage));
+}
+__host__ __device__ __forceinline__ size_t kt_plan_idx_off(int nstages){
+  return kt_plan_ctl_off(nstages) + kt_r256((size_t)nstages * sizeof(KtPCtl));
+}
+__host__ __device__ __forceinline__ size_t kt_plan_ctr_off(int nstages){
+  return kt_plan_idx_off(nstages) + kt_r256((size_t)KT_PLAN_MAXG * KT_PLAN_WAVES * 4);
+}
+/* barrier words (128-byte lines of 32 words): status, then KT_BAR_SHARDS arrival counters (block b arrives on
+   shard b % KT_BAR_SHARDS) */
+#define KT_BAR_STATUS 0
+#define KT_BAR_SUB 1
+#define KT_BAR_SHARDS 32
+#define KT_BAR_WORDS ((KT_BAR_SUB + KT_BAR_SHARDS) * 32)
+__host__ __device__ __forceinline__ size_t kt_plan_rec_off(int nstages){
+  return kt_plan_ctr_off(nstages) + kt_r256((size_t)KT_BAR_WORDS * 4)
+#ifdef KT_PLAN_TRACE
+         + (size_t)KT_PLAN_MAXG * nstages * 16 * 4
+#endif
+         ;
+}
+
+/* grouped (MoE) launch over the token-sorted lists */
+struct KtGroupedArgs {
+  const uint8_t* const* wexp;         /* device table: expert e's kq8 buffer */
+  int R, C, NU, pad;                  /* rows, columns, blocks */
+  const int* cnt; const int* off;     /* per expert: list length and start */
+  const int* act; const int* nact;    /* active experts (ascending) and their count */
+  const int* xrow;                    /* nullable: input row of list entry p (else p itself) */
+  int ldq, ldd, ldy, pad2;
+  float* y;                           /* output rows [entries][ldy] */
+};

@@ -1,0 +1,162 @@
+/* kt.h - C ABI of libkt_gfx950.so, the MI355X (gfx950) kernel library for Kindi's quantized linear layer.
+
+   It replaces the kernel module Kindi compiles at run time (cp.RawModule over kindi.cu + tc_hip.cu + ...,
+   spec.py:144-151, 187-195; engine.py:88-92) and launches through gpudrv.driver() (gpudrv.py:24-101): a prebuilt
+   shared library, loaded with ctypes, exporting host launchers with plain pointers and sizes.
+
+   Conventions (all entry points):
+   - every pointer argument is a device pointer owned by the caller (as Kindi's CuPy buffers, engine.py:193-204,
+     spec.py:523-593); the library never allocates, frees or synchronizes, and keeps no device state;
+   - `stream` is a hipStream_t (NULL = the null stream); launches are asynchronous and graph-capturable;
+   - the return value is a hipError_t as int: 0 on success, hipErrorInvalidValue (1) for a shape, stride or
+     alignment the kernels do not take (Kindi raises SystemExit / RuntimeError there: spec.py:195-196,
+     layout.py:38-39, tp.py:944-945), else the launch error;
+   - M = 0 tokens is a no-op returning 0.
+
+   Numbers (the reference's, tc.cu:1-18, tc_hip.cu:8-15): activations are int8 per 128-column group (XS = amax/127,
+   q = round-to-nearest-even(x * 127 / amax), XA = sum q); a group's value v = sum t q over its 128 columns is an
+   exact int32 (t in {-1, 0, +1}); the fp32 output adds fmaf((float)v, XS * d, acc) group after group (the prefill
+   product in exactly that order; the decode products in the fixed tree documented at kt_tern_gemv), so a token's
+   result is the same on every run. */
+#ifndef KT_H
+#define KT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#define KT_VERSION 1
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+int kt_version(void);
+/* hipSetDevice(device). gpudrv.py:83-85 (cuCtxSetCurrent) */
+int kt_init(int device);
+const char* kt_error_string(int rc);
+
+/* ---------------------------------------------------------------- ternary weights
+   Device layout "kt2": 2-bit digits + fp16 scale per 128 columns, the same 2.125 bits per weight as the pack.
+   kt_tern_weight_bytes: the size of one matrix (rows padded to a multiple of 8), 0 if C % 128 != 0.
+   kt_tern_pack: the reference pack of one tensor, unchanged (bcodes [C/4][R]: byte = d0 + 3 d1 + 9 d2 + 27 d3 of
+   4 columns, convert.py:49-52, 144-159; dpm [C/128][R] fp16 bits, convert.py:155) -> W (16-byte aligned).
+   Replaces layout.repack (layout.py:32-48) and spec.repack / k_tc_pack (spec.py:327-383, tc_hip.cu:31-40). */
+size_t kt_tern_weight_bytes(int R, int C);
+int kt_tern_pack(const uint8_t* bcodes, const uint16_t* dpm, int R, int C, void* W, void* stream);
+
+/* ---------------------------------------------------------------- activations
+   X fp32 [M][ldx] -> XQ int8 [M][ldq] (natural column order, ldq % 16 == 0), XS f32 / XA i32 [M][C/128].
+   per_row = 0: the reference's per-128-group scale (k_tc_q8, tc_hip.cu:43-74; tcq128 tc.cu:160-194; k_q8x_T
+   chunk.cu:781-802). per_row = 1: one amax per token row (the same formula; XS repeated per group). */
+int kt_quant_q8(const float* X, int ldx, int M, int C, int per_row, int8_t* XQ, int ldq, float* XS, int32_t* XA,
+                void* stream);
+
+/* ---------------------------------------------------------------- decode products (1 .. 16 tokens a pass)
+   Y[n][ldy] = W x_n for tokens n < M. dbg (nullable): the exact group values v, int32 [M][R][C/128].
+   Every output row's sum is formed inside one block in a fixed order that depends only on C (never on M or R), so
+   a token's result does not depend on how many tokens share the pass. The order: the row's K units are split into
+   KS = kt_decode_kslices(C, 0) contiguous slices of whole steps (a step = 8 consecutive units, S steps; KS =
+   min(ceil(S / 2), 16); slice k = steps [k S / KS, (k + 1) S / KS)); in a slice, lane c (0..7) chains fmaf over its
+   units 8 s + c in increasing order, the 8 lane sums are added by the xor butterfly ((l0 + l1) + (l2 + l3)) +
+   ((l4 + l5) + (l6 + l7)), and the slice sums are added left to right. No workspace, no second pass.
+   Replaces k_tc_mv{2,4,8} + k_tc_sum (tc_hip.cu:180-199, 236-240, 271-279; spec.py:619-657). */
+int kt_decode_kslices(int C, int q8);
+int kt_tern_gemv(const void* W, int R, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M,
+                 float* Y, int ldy, int32_t* dbg, void* stream);
+
+/* up to three matrices sharing one input (q/k/v, gate/up) in one launch; Y_i is [M][R_i]; R_i <= 0 ends the list.
+   Each matrix's outputs are bit-identical to its own kt_tern_gemv. Replaces k_tc_mv3_{2,4,8} (tc_hip.cu:201-234;
+   spec.py:659-673). */
+int kt_tern_gemv3(const void* W0, int R0, float* Y0, const void* W1, int R1, float* Y1, const void* W2, int R2,
+                  float* Y2, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M,
+                  void* stream);
+
+/* y[n R + r] = sum over parts p < sp of P[(n sp + p) R + r], in part order. k_tc_sum (tc_hip.cu:271-279). */
+int kt_tern_sum(const float* P, float* y, int R, int M, int sp, void* stream);
+
+/* ---------------------------------------------------------------- decode plan (one launch per decode step)
+   A sequence of ternary products run in order by one persistent launch: stage s starts after every earlier stage
+   has finished and its stores are visible (the ordering of separate stream-ordered launches, so a stage may read
+   what an earlier stage wrote), while the weight loads of later stages are already in flight. Each stage is what
+   kt_tern_gemv3 takes (1 .. 3 matrices with one quantized input, Y_i [M][R_i]) and gives the same bits.
+   Replaces the plan replay of a decode step (Plan.add / replay, tp.py:282-302; spec.py:250-325, 619-673).
+   kt_plan_bytes: the device bytes of a plan of these stages on the current device (caller-allocated, 256-byte
+   aligned; 0 when the stages are not valid). The plan holds one 16-byte record per 8-row step of every product.
+   kt_plan_build: checks the stages, sizes the launch for the current device (every block resident at once) and
+   writes the plan (synchronous on `stream`; not for graph capture). `info` receives what kt_plan_run needs.
+   Stages take C % 128 == 0 and C <= 30720, M 1 .. 4 tokens (the same for every stage), at most 4095 stages
+   (the stage tables live in LDS: fewer for large C).
+   kt_plan_run: one plan execution (a small reset kernel, then the plan kernel; graph-capturable). Nothing else
+   may run on the GPU at the same time (the plan's blocks wait for each other).
+   kt_plan_status: after the run (synchronizes `stream`): 0, or 1 if a stage barrier timed out (results invalid). */
+typedef struct kt_stage {
+  const void* W[3];                   /* up to three kt2 matrices; R[i] <= 0 ends the list */
+  int R[3];
+  float* Y[3];                        /* [M][R_i] */
+  int C;
+  const int8_t* XQ;                   /* kt_quant_q8 output [M][ldq], XS / XA [M][C/128] */
+  int ldq;
+  const float* XS;
+  const int32_t* XA;
+  int M;
+} kt_stage;
+typedef struct kt_plan_info {
+  int nstages, grid, waves, mt;
+  size_t lds;
+} kt_plan_info;
+size_t kt_plan_bytes(const kt_stage* stages, int nstages);
+int kt_plan_build(const kt_stage* stages, int nstages, void* plan, kt_plan_info* info, void* stream);
+int kt_plan_run(const void* plan, const kt_plan_info* info, void* stream);
+int kt_plan_status(const void* plan, const kt_plan_info* info, int* status, void* stream);
+/* kt_plan_layout: the plan image kt_plan_build would write for a device of G compute units, in host memory (no
+   device call): *used receives its size; out (nullable) of cap bytes receives the image. No counterpart in the
+   reference: for tests and inspection of the work deal (header, stages, row tables, record index, records). */
+int kt_plan_layout(const kt_stage* stages, int nstages, int G, void* out, size_t cap, size_t* used);
+
+/* ---------------------------------------------------------------- prefill product (any M, matrix cores)
+   Y and/or Y16 [M][ldy] (fp32 / fp16 bits); dbg as kt_tern_gemv. XA is accepted for the reference's argument list
+   and not read (the matrix cores take signed trits). Replaces k_tc_mm2 / k_tc_mm{4,8,16} (tc_hip.cu:243-269,
+   chunk.py:273-296) and k_mm_g5q (chunk.cu:858-918, chunk.py:245-271). */
+int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M,
+                 float* Y, uint16_t* Y16, int ldy, int32_t* dbg, void* stream);
+
+/* ---------------------------------------------------------------- q8_0
+   Device layout "kq8": int8 codes + fp16 scale per 32 columns (1.0625 B/w, as GGUF Q8_0).
+   kt_q8_pack: GGUF Q8_0 rows (34-byte blocks: fp16 d, 32 int8; dsv41_cpu.c:77-78) -> W. Replaces dg_mat_q8
+   (dsv41_gpu.cu:66-88) and the Q8_0 repack of lightning.py.
+   kt_q8_quant: X fp32 -> Q int8 [M][ldq] + D f32 [M][ldd] per 32 columns, llama.cpp's CPU rounding
+   (d = fp16(amax/127), q = rne(x * 127 / amax); quant_q8 dsv41_cpu.c:251-280, moe_cpu.c:84-112); act = 1 applies
+   relu^2 first (lt_quant2, lightning.cu:470).
+   kt_q8_gemv: Y = W x for M tokens: per block v = sum w q exact, acc = fmaf((float)v, dw * dx, acc) (lt_mv_q8
+   lightning.cu:258-284, k_q8 dsv41_gpu.cu:131-296), summed in kt_tern_gemv's order over 32-column units
+   (KS = kt_decode_kslices(C, 1)); dbg int32 [M][R][C/32]. */
+size_t kt_q8_weight_bytes(int R, int C);
+int kt_q8_pack(const uint8_t* rows, int R, int C, void* W, void* stream);
+int kt_q8_quant(const float* X, int ldx, int M, int C, int act, int8_t* Q, int ldq, float* D, int ldd, void* stream);
+int kt_q8_gemv(const void* W, int R, int C, const int8_t* Q, int ldq, const float* D, int ldd, int M, float* Y,
+               int ldy, int32_t* dbg, void* stream);
+
+/* ---------------------------------------------------------------- MoE
+   kt_moe_topk: logits [M][E] -> ids / gw [M][k]: softmax, the k largest (ties to the lower index), weights
+   normalized over the chosen k (the reference's Lightning router lt_topk / lt_router_topk,
+   lightning.cu:373-468, is sigmoid + bias: same interface, other scoring). E <= 1024, k <= 16.
+   kt_moe_sort: lt_moe_lists (lightning.cu:1318-1349): cnt / off [E], xrow / where [M k], plus act [E] (experts with
+   cnt > 0, ascending) and nact [1]; entries of an expert in ascending t k + j. One block; E <= 1024.
+   kt_q8_grouped: per active expert e, Y[p] = W_e x[xrow[p]] for its entries p (xrow NULL: x[p]); Wexp = device
+   table of E kq8 buffers (the pointer tables of lt_mv_q2 / lt_mm_*, lightning.cu:154-195, 958-961); M = tokens
+   (bounds an expert's list); dbg int32 [entries][R][C/32].
+   kt_moe_combine: x[t] += sum_j fmaf(gw[t k + j], yd[where[t k + j]], .) (+ ysh[t]) (lt_moe_combine,
+   lightning.cu:1352-1361). */
+int kt_moe_topk(const float* logits, int M, int E, int k, int* ids, float* gw, void* stream);
+int kt_moe_sort(const int* ids, int M, int k, int E, int* cnt, int* off, int* xrow, int* where, int* act, int* nact,
+                void* stream);
+int kt_q8_grouped(const void* const* Wexp, int R, int C, int E, const int* cnt, const int* off, const int* act,
+                  const int* nact, const int* xrow, int nentries, int M, const int8_t* Q, int ldq, const float* D,
+                  int ldd, float* Y, int ldy, int32_t* dbg, void* stream);
+int kt_moe_combine(const float* yd, const float* ysh, const int* where, const float* gw, int M, int k, int cols,
+                   float* x, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
