@@ -24,11 +24,15 @@ extern "C" __global__ void k_tern_sum(const float*, float*, int, int, int);
 template <bool DBG>
 __global__ void k_tern_gemm(const uint32_t*, const uint16_t*, int, int, const int8_t*, int, const float*, int, float*,
                             uint16_t*, int, int32_t*);
+template <int WT, int WR, int PD, bool DBG>
+__global__ void k_tern_gemm_rs1(const uint32_t*, const uint16_t*, int, int, const int8_t*, int, const float*, int,
+                                float*, uint16_t*, int, int32_t*);
 extern "C" __global__ void k_moe_topk(const float*, int, int, int*, float*);
 extern "C" __global__ void k_moe_sort(const int*, int, int, int*, int*, int*, int*, int*, int*, int);
 extern "C" __global__ void k_moe_combine(const float*, const float*, const int*, const float*, int, int, float*);
 
 #define KT_INVALID ((int)hipErrorInvalidValue)
+#define KT_RS_ROWS 8192                /* per-row prefill order below this many rows (include/kt.h) */
 #define KT_LAUNCH_CHECK() do { const hipError_t _e = hipGetLastError(); if(_e != hipSuccess) return (int)_e; } while(0)
 
 static inline hipStream_t kt_stream(void* s){ return (hipStream_t)s; }
@@ -271,19 +275,33 @@ int kt_plan_status(const void* plan, const kt_plan_info* info, int* status, void
 }
 
 /* ------------------------------------------------------------------ prefill product */
-int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M,
-                 float* Y, uint16_t* Y16, int ldy, int32_t* dbg, void* stream){
+/* per-row scales: 256 tokens x 128 rows (8 waves of 2 x 2 tiles) when that gives every CU a block, else 128 x 128
+   (16 waves of one tile); both run the same per-element chain, so the bits do not depend on the choice */
+int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA,
+                 int per_row, int M, float* Y, uint16_t* Y16, int ldy, int32_t* dbg, void* stream){
   (void)XA;                                                  /* signed trits on the matrix cores: no digit offset */
   if(M == 0) return 0;
   if(!W || !XQ || !XS || (!Y && !Y16) || R <= 0 || M < 0 || C <= 0 || C % 128 || ldq < C || ldq % 16 || ldy < R
-     || !kt_al(W, 16) || !kt_al(XQ, 16)) return KT_INVALID;
+     || !kt_al(W, 16) || !kt_al(XQ, 16) || (per_row != 0 && per_row != 1)) return KT_INVALID;
   const int NG = C / 128;
   const uint32_t* codes = (const uint32_t*)W;
   const uint16_t* scales = (const uint16_t*)((const uint8_t*)W + kt_code_bytes(R, NG));
+  hipStream_t s = kt_stream(stream);
+  if(per_row && R < KT_RS_ROWS){
+    /* per-row order on small blocks (one 32 x 32 tile a wave, 8 waves: 128 tokens x 64 rows); the choice depends on
+       the shape of W only, so a token's result does not depend on M */
+    const dim3 grid((R + 63) / 64, (M + 127) / 128);
+    if(dbg) hipLaunchKernelGGL((k_tern_gemm_rs1<4, 2, 3, true>), grid, dim3(512), 0, s, codes, scales, R, NG, XQ, ldq,
+                               XS, M, Y, Y16, ldy, dbg);
+    else hipLaunchKernelGGL((k_tern_gemm_rs1<4, 2, 3, false>), grid, dim3(512), 0, s, codes, scales, R, NG, XQ, ldq,
+                            XS, M, Y, Y16, ldy, dbg);
+    KT_LAUNCH_CHECK();
+    return 0;
+  }
   const dim3 grid((R + 127) / 128, (M + 127) / 128);
-  if(dbg) hipLaunchKernelGGL(k_tern_gemm<true>, grid, dim3(256), 0, kt_stream(stream), codes, scales, R, NG, XQ, ldq, XS, M,
+  if(dbg) hipLaunchKernelGGL(k_tern_gemm<true>, grid, dim3(256), 0, s, codes, scales, R, NG, XQ, ldq, XS, M,
                      Y, Y16, ldy, dbg);
-  else hipLaunchKernelGGL(k_tern_gemm<false>, grid, dim3(256), 0, kt_stream(stream), codes, scales, R, NG, XQ, ldq, XS, M,
+  else hipLaunchKernelGGL(k_tern_gemm<false>, grid, dim3(256), 0, s, codes, scales, R, NG, XQ, ldq, XS, M,
                      Y, Y16, ldy, dbg);
   KT_LAUNCH_CHECK();
   return 0;
@@ -376,11 +394,11 @@ int kt_q8_grouped(const void* const* Wexp, int R, int C, int E, const int* cnt, 
   const dim3 grid(kt_r8(R), ny), block(64 * ks);
   const KtGemvArgs da = {};
   hipStream_t s = kt_stream(stream);
-#define KT_G(K, MT) do { const size_t lds = KtFlat<KT_FMT_Q8, MT>::lds(ks); \
+#define KT_GL(K, MT) do { const size_t lds = KtFlat<KT_FMT_Q8, MT>::lds(ks); \
     if(dbg) hipLaunchKernelGGL((K<KT_FMT_Q8, MT, true, true>), grid, block, lds, s, da, a, Q, D, nullptr, dbg, ks); \
     else hipLaunchKernelGGL((K<KT_FMT_Q8, MT, false, true>), grid, block, lds, s, da, a, Q, D, nullptr, dbg, ks); } while(0)
-  if(mt == 4) KT_G(k_gemv_flat, 4); else if(mt == 2) KT_G(k_gemv_flat, 2); else KT_G(k_gemv_flat1, 1);
-#undef KT_G
+  if(mt == 4) KT_GL(k_gemv_flat, 4); else if(mt == 2) KT_GL(k_gemv_flat, 2); else KT_GL(k_gemv_flat1, 1);
+#undef KT_GL
   KT_LAUNCH_CHECK();
   return 0;
 }

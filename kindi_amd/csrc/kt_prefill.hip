@@ -172,3 +172,141 @@ template __global__ void k_tern_gemm<false>(const uint32_t*, const uint16_t*, in
                                             int, float*, uint16_t*, int, int32_t*);
 template __global__ void k_tern_gemm<true>(const uint32_t*, const uint16_t*, int, int, const int8_t*, int, const float*,
                                            int, float*, uint16_t*, int, int32_t*);
+
+/* ------------------------------------------------------------------ per-row activation scales
+   The prefill product when the activations are quantized per token (kt_quant_q8 per_row: one XS a token, the
+   quantization BASELINE's prefill config names): XS factors out of the group sum, so
+     Y[t][r] = XS[t] * sum_g fmaf((float)v(t, r, g), d[r][g], .)      (groups in order)
+   and the per-group epilogue is two VALU operations per element (convert, fma) instead of three. v(t, r, g) is the
+   same exact int32 as above. One 32 x 32 tile a wave and WT x WR waves a block (32 WT tokens x 32 WR rows): small
+   blocks, for matrices whose row count leaves the 128 x 128 kernel's grid short of the CUs. Both operands go through
+   LDS (two stages, one barrier a group); every thread's global loads of group g + PD (32 bytes of activations, one
+   word of packed trits, its tile column's scale) are issued PD groups before the group is stored to LDS, so the
+   memory latency is covered by PD - 1 groups of products. The loads are unconditional (past the last group they
+   read it again), so the loop issues the same loads every group. */
+template <int WT, int WR, int PD, bool DBG>
+__global__ void __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_eu(4))) k_tern_gemm_rs1(const uint32_t* __restrict__ codes,
+    const uint16_t* __restrict__ scales, int R, int NG, const int8_t* __restrict__ XQ, int ldq,
+    const float* __restrict__ XS, int M, float* __restrict__ Y, uint16_t* __restrict__ Y16, int ldy,
+    int32_t* __restrict__ dbg){
+  constexpr int NT = 64 * WT * WR, BT = 32 * WT, BR = 32 * WR, NW = BR * 8;
+  static_assert(NT == BT * 4 && NW <= NT, "one activation quarter-row and at most one packed word a thread");
+  __shared__ __attribute__((aligned(16))) uint8_t Xl[2][BT * PF_LD];
+  __shared__ __attribute__((aligned(16))) uint8_t Wl[2][BR * PF_LD];
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wt = wv / WR, wr = wv % WR;
+  const int r0 = blockIdx.x * BR, n0 = blockIdx.y * BT;
+  const int R8 = kt_r8(R);
+
+  /* activations: token tid / 4 of the block, 32 bytes at (tid % 4) 32 of each group (clamped to a real row) */
+  const int xt = tid >> 2, xq = tid & 3;
+  const int8_t* xsrc = XQ + (long long)(n0 + xt < M ? n0 + xt : M - 1) * ldq + xq * 32;
+  const int xdst = xt * PF_LD + xq * 32;
+  /* packed trits: word tid of the group's NW (chunk tid / 4 = (row group, half, row), word tid % 4) */
+  const bool wown = tid < NW;
+  const int ch = (tid >> 2) & (2 * BR - 1), wj = tid & 3;
+  const int lrg = ch >> 4, lh = (ch >> 3) & 1, lr = ch & 7;
+  const int grg = (r0 >> 3) + lrg;
+  const bool wvalid = grg < R8;
+  const int wdst = (lrg * 8 + lr) * PF_LD + lh * 64 + 16 * wj;
+  /* this lane's tile: tokens 32 wt + .., weight row cr (its scale row clamped to a real one) */
+  const int cr = r0 + 32 * wr + (lane & 31);
+  const int srow = cr < R8 * KT_RG ? cr : 0;
+
+  /* the global loads of group g (clamped: past the last group it is read again) into registers X0 X1 W H; the
+     LDS stores of such a set into stage b. Macros with named registers, not a struct: the three sets must stay in
+     registers (a struct by reference let the compiler merge the three steps behind a pointer select) */
+#define KT_RS1_LOAD(g, X0, X1, W, H) do { \
+    const int gg_ = (g) < NG ? (g) : NG - 1; \
+    const uint4* xp_ = (const uint4*)(xsrc + gg_ * 128); \
+    X0 = xp_[0]; X1 = xp_[1]; \
+    W = codes[wvalid ? kt_widx(NG, grg, gg_ >> 3, lh, gg_ & 7, lr) * 4 + wj : 0]; \
+    H = scales[kt_sidx(NG, srow >> 3, gg_, srow & 7)]; } while(0)
+  auto store = [&](const uint4 x0, const uint4 x1, const uint32_t wraw, int b){
+    *(uint4*)(Xl[b] + xdst) = x0;
+    *(uint4*)(Xl[b] + xdst + 16) = x1;
+    if(wown){
+      const uint32_t w = wvalid ? wraw : 0x55555555u;           /* rows past the matrix: digit 1, trit 0 */
+      uint4 o;
+      o.x = kt_trits(w & 0x03030303u);
+      o.y = kt_trits((w >> 2) & 0x03030303u);
+      o.z = kt_trits((w >> 4) & 0x03030303u);
+      o.w = kt_trits((w >> 6) & 0x03030303u);
+      *(uint4*)(Wl[b] + wdst) = o;
+    }
+  };
+
+  float acc[16];
+#pragma unroll
+  for(int e = 0; e < 16; ++e) acc[e] = 0.0f;
+  float dcur;
+  {
+    uint4 x0, x1;
+    uint32_t w;
+    uint16_t h;
+    KT_RS1_LOAD(0, x0, x1, w, h);
+    store(x0, x1, w, 0);
+    dcur = kt_h2f(h);
+  }
+  /* group g: products and epilogue from stage g % 2 */
+  auto prod = [&](int g){
+    const int b = g & 1;
+    kt_v16i c;
+#pragma unroll
+    for(int e = 0; e < 16; ++e) c[e] = 0;
+#pragma unroll
+    for(int ks = 0; ks < 4; ++ks){
+      const int koff = ks * 32 + (lane >> 5) * 16;
+      const kt_v4i A = *(const kt_v4i*)(Xl[b] + (32 * wt + (lane & 31)) * PF_LD + koff);
+      const kt_v4i B = *(const kt_v4i*)(Wl[b] + (32 * wr + (lane & 31)) * PF_LD + koff);
+      c = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, c, 0, 0, 0);
+    }
+#pragma unroll
+    for(int e = 0; e < 16; ++e){
+      acc[e] = fmaf((float)c[e], dcur, acc[e]);
+      if(DBG){
+        const int t = n0 + 32 * wt + (e & 3) + 8 * (e >> 2) + 4 * (lane >> 5);
+        if(t < M && cr < R) dbg[((long long)t * R + cr) * NG + g] = c[e];
+      }
+    }
+  };
+  /* one group, then group g + 1 (loaded PD groups ago, in set S) into the other stage and g + 1 + PD into set S */
+#define KT_RS1_STEP(g, X0, X1, W, H) do { \
+    prod(g); \
+    store(X0, X1, W, ((g) & 1) ^ 1); \
+    dcur = kt_h2f(H); \
+    KT_RS1_LOAD((g) + 1 + PD, X0, X1, W, H); \
+    __syncthreads(); } while(0)
+  static_assert(PD == 3, "three prefetch sets");
+  uint4 xa0, xa1, xb0, xb1, xc0, xc1;
+  uint32_t wa, wb, wc;
+  uint16_t ha, hb, hc;
+  KT_RS1_LOAD(1, xa0, xa1, wa, ha);
+  KT_RS1_LOAD(2, xb0, xb1, wb, hb);
+  KT_RS1_LOAD(3, xc0, xc1, wc, hc);
+  __syncthreads();
+  int g = 0;
+  for(; g + 3 <= NG; g += 3){                                    /* the same loads every group: exact waits */
+    KT_RS1_STEP(g, xa0, xa1, wa, ha);
+    KT_RS1_STEP(g + 1, xb0, xb1, wb, hb);
+    KT_RS1_STEP(g + 2, xc0, xc1, wc, hc);
+  }
+  if(g < NG) KT_RS1_STEP(g, xa0, xa1, wa, ha);
+  if(g + 1 < NG) KT_RS1_STEP(g + 1, xb0, xb1, wb, hb);
+#undef KT_RS1_STEP
+#undef KT_RS1_LOAD
+#pragma unroll
+  for(int e = 0; e < 16; ++e){
+    const int t = n0 + 32 * wt + (e & 3) + 8 * (e >> 2) + 4 * (lane >> 5);
+    if(t < M && cr < R){
+      const float y = acc[e] * XS[(long long)t * NG];
+      if(Y) Y[(long long)t * ldy + cr] = y;
+      if(Y16) Y16[(long long)t * ldy + cr] = __half_as_ushort(__float2half_rn(y));
+    }
+  }
+}
+
+#define KT_RS1(WT, WR, PD, DBG) template __global__ void k_tern_gemm_rs1<WT, WR, PD, DBG>(const uint32_t*, \
+    const uint16_t*, int, int, const int8_t*, int, const float*, int, float*, uint16_t*, int, int32_t*);
+KT_RS1(4, 2, 3, false) KT_RS1(4, 2, 3, true)
+

@@ -42,7 +42,7 @@ SIGNATURES = [
     ("kt_plan_build", I, [ctypes.POINTER(KtStage), I, P, ctypes.POINTER(KtPlanInfo), P]),
     ("kt_plan_run", I, [P, ctypes.POINTER(KtPlanInfo), P]),
     ("kt_plan_status", I, [P, ctypes.POINTER(KtPlanInfo), ctypes.POINTER(I), P]),
-    ("kt_tern_gemm", I, [P, I, I, P, I, P, P, I, P, P, I, P, P]),
+    ("kt_tern_gemm", I, [P, I, I, P, I, P, P, I, I, P, P, I, P, P]),
     ("kt_q8_weight_bytes", S, [I, I]),
     ("kt_q8_pack", I, [P, I, I, P, P]),
     ("kt_q8_quant", I, [P, I, I, I, I, P, I, P, I, P]),

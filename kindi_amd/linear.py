@@ -150,8 +150,8 @@ class Linear(object):
             Y = torch.empty((act.M, m.R), dtype=torch.float32, device=act.XQ.device)
         ldy = (Y if Y is not None else Y16).stride(0)
         y16 = Y16.view(torch.int16) if Y16 is not None else None
-        rc = lib.kt_tern_gemm(ptr(m.W), m.R, m.C, ptr(act.XQ), act.XQ.stride(0), ptr(act.XS), ptr(act.XA), act.M,
-                              ptr(Y), ptr(y16), ldy, ptr(dbg), stream())
+        rc = lib.kt_tern_gemm(ptr(m.W), m.R, m.C, ptr(act.XQ), act.XQ.stride(0), ptr(act.XS), ptr(act.XA),
+                              1 if act.per_row else 0, act.M, ptr(Y), ptr(y16), ldy, ptr(dbg), stream())
         gpudrv.check(rc, "kt_tern_gemm")
         return Y if Y is not None else Y16
 

@@ -137,6 +137,20 @@ void or_tern_out(const int32_t* acc, const float* XS, const uint16_t* dpm, int R
     }
 }
 
+/* The prefill product's order for per-row activation scales (one XS per token, kt_quant_q8 per_row): the weight
+   scale alone goes into the group chain, a = fmaf((float)v_g, d_g, a) over g in order, and the token's scale
+   multiplies the sum once: Y = a * XS[n][0]. The same real value as or_tern_out when XS[n][g] does not depend on g;
+   only the fp32 rounding order differs. */
+void or_tern_out_rs(const int32_t* acc, const float* XS, const uint16_t* dpm, int R, int NG, int M, float* Y, int ldy){
+  for(int n = 0; n < M; ++n)
+    for(int r = 0; r < R; ++r){
+      float a = 0.0f;
+      for(int g = 0; g < NG; ++g)
+        a = fmaf((float)acc[((size_t)n * R + r) * NG + g], or_h2f(dpm[(size_t)g * R + r]), a);
+      Y[(size_t)n * ldy + r] = a * XS[(size_t)n * NG];
+    }
+}
+
 /* The same sums added in a fixed tree: the K units split into nsplit contiguous ranges, each range into nwave
    contiguous slices (slice bounds floor(i * n / parts)); a slice is a sequential fma chain from 0, the slices of a
    range are added left to right, then the ranges left to right. nsplit = nwave = 1 is or_tern_out itself. This is

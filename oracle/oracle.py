@@ -48,6 +48,7 @@ def lib():
         h.or_quant_q8.argtypes = [P, I, I, I, I, P, I, P, P]
         h.or_tern_acc.argtypes = [P, I, I, P, I, I, P]
         h.or_tern_out.argtypes = [P, P, P, I, I, I, P, I]
+        h.or_tern_out_rs.argtypes = [P, P, P, I, I, I, P, I]
         h.or_tern_sum.argtypes = [P, P, I, I, I]
         h.or_out_tree.argtypes = [P, P, I, P, I, I, I, I, I, I, P, I]
         h.or_out_lanes.argtypes = [P, P, I, P, I, I, I, I, I, I, P, I]
@@ -215,6 +216,15 @@ def tern_out(acc, XS, dpm, R, C):
     M = acc.shape[0]
     Y = np.empty((M, R), np.float32)
     lib().or_tern_out(_p(_c(acc, np.int32)), _p(_c(XS, np.float32)), _p(_c(dpm, np.uint16)), R, C // 128, M, _p(Y), R)
+    return Y
+
+
+def tern_out_rs(acc, XS, dpm, R, C):
+    """the prefill order for per-row activation scales: Y = XS[n][0] * (fma chain of v_g * d_g over the groups)"""
+    M = acc.shape[0]
+    Y = np.empty((M, R), np.float32)
+    lib().or_tern_out_rs(_p(_c(acc, np.int32)), _p(_c(XS, np.float32)), _p(_c(dpm, np.uint16)), R, C // 128, M,
+                         _p(Y), R)
     return Y
 
 

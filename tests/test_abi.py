@@ -63,7 +63,8 @@ def test_validation_rejects_bad_shapes(lib):
     # ldy < R
     assert lib.kt_tern_gemv(fake, 64, 256, fake, 256, fake, fake, 1, fake, 63, None, None) == INVALID
     # null output
-    assert lib.kt_tern_gemm(fake, 64, 256, fake, 256, fake, fake, 4, None, None, 64, None, None) == INVALID
+    assert lib.kt_tern_gemm(fake, 64, 256, fake, 256, fake, fake, 0, 4, None, None, 64, None, None) == INVALID
+    assert lib.kt_tern_gemm(fake, 64, 256, fake, 256, fake, fake, 2, 4, fake, None, 256, None, None) == INVALID
     # q8: C % 32
     assert lib.kt_q8_gemv(fake, 64, 48, fake, 48, fake, 1, 1, fake, 64, None, None) == INVALID
     # moe: k > 16, E > 1024

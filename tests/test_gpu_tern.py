@@ -136,6 +136,36 @@ def test_gemm_small(kt, R, C, M):
     assert np.array_equal(host(Y16), seq.astype(np.float16))
 
 
+@pytest.mark.parametrize("R,C,M", [(128, 256, 128), (100, 384, 5), (256, 512, 300), (384, 1024, 200),
+                                   (8192, 128, 1024), (8100, 256, 1000)])
+def test_gemm_per_row(kt, R, C, M):
+    """per-row activation scales (below 8192 rows the small-block kernel in the per-row order, above it the 128 x 128
+    kernel in the reference's order; ragged rows and tokens): int32 group values exact, fp32 bit-exact in the
+    documented order, fp16 its rounding, and within the tolerance of the reference's sequential order"""
+    lib, linear = kt
+    say("gemm per-row", R, C, M)
+    W, dig, bc, dpm = upload(linear, R, C, R * 7 + M)
+    L = linear.Linear({"w": W})
+    X = rng(M + 2).normal(0, 1, (M, C)).astype(np.float32)
+    act = linear.quantize(dev(X), per_row=True)
+    Y = torch.empty((M, R), dtype=torch.float32, device="cuda")
+    Y16 = torch.empty((M, R), dtype=torch.float16, device="cuda")
+    dbg = torch.empty((M, R, C // 128), dtype=torch.int32, device="cuda")
+    L.gemm("w", act, Y=Y, Y16=Y16, dbg=dbg)
+    Q, XS, XA = orc.quant_q8(X, per_row=True)
+    acc = orc.tern_acc(bc, R, C, Q)
+    assert np.array_equal(host(dbg), acc), "int32 group values"
+    seq = orc.tern_out(acc, XS, dpm, R, C)
+    want = orc.tern_out_rs(acc, XS, dpm, R, C) if R < 8192 else seq      # the per-row order below 8192 rows
+    y = host(Y)
+    assert np.array_equal(y, want), "fp32 in the documented order"
+    assert np.array_equal(host(Y16), want.astype(np.float16))
+    assert max_rel(y, seq) < TOL
+    # without the debug output (the other instantiation) the same bits
+    Y2 = L.gemm("w", act)
+    assert np.array_equal(host(Y2), y)
+
+
 @pytest.mark.parametrize("R,C,M", [(12288, 4096, 512), (4096, 12288, 512)])
 def test_gemm_config2_sampled(kt, R, C, M):
     """config 2 shapes at M = 512: int32 group values and outputs of 96 sampled rows against the oracle, all rows
@@ -157,8 +187,10 @@ def test_gemm_config2_sampled(kt, R, C, M):
     assert np.array_equal(host(act.XQ), Q)
     acc = orc.tern_acc(np.ascontiguousarray(bc), len(rows), C, Q)
     seq = orc.tern_out(acc, XS, np.ascontiguousarray(dpm), len(rows), C)
+    want = orc.tern_out_rs(acc, XS, np.ascontiguousarray(dpm), len(rows), C) if R < 8192 else seq
     y = host(Y)
-    assert np.array_equal(y[:, rows], seq)
+    assert np.array_equal(y[:, rows], want), "documented order"
+    assert max_rel(y[:, rows], seq) < TOL
     Yd = torch.empty((16, R), dtype=torch.float32, device="cuda")
     sub = linear.quantize(Xd[:16], per_row=True)
     L.gemv_q(["w"], sub, [Yd])

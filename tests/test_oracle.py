@@ -178,6 +178,35 @@ def test_tern_out_float64(orc):
     assert np.allclose(Y, deq @ W.T, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
 
 
+def test_tern_out_rs(orc):
+    """the per-row prefill order: float64 value, agreement with the reference order on per-row inputs, and a
+    hand-computed case where the chain order shows (fp32 rounding of each step)"""
+    R, C, M = 48, 768, 3
+    dig = rand_digits(R, C, 41)
+    dpm = rand_scales((C // 128, R), 42)
+    X = rng(43).normal(0, 1, (M, C)).astype(np.float32)
+    bc = orc.pack_from_digits(dig)
+    Q, XS, XA = orc.quant_q8(X, per_row=True)
+    assert np.all(XS == XS[:, :1])                                   # per-row: one scale a token
+    acc = orc.tern_acc(bc, R, C, Q)
+    Y = orc.tern_out_rs(acc, XS, dpm, R, C)
+    d = dpm.view(np.float16).astype(np.float64)
+    ref = np.einsum("mrg,mg,gr->mr", acc.astype(np.float64), XS.astype(np.float64), d)
+    assert np.allclose(Y, ref, rtol=2e-6, atol=1e-6 * np.abs(ref).max())
+    Yseq = orc.tern_out(acc, XS, dpm, R, C)
+    assert np.allclose(Y, Yseq, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
+    # hand case where the order shows: v = (2^24, 1, 1), d = 1, XS = 0.5. In group order the chain rounds 2^24 + 1
+    # back to 2^24 twice (ties to even), so Y = 2^23; the float64 value (and the reverse order) is 2^23 + 1
+    acc1 = np.array([[[2 ** 24, 1, 1]]], np.int32)
+    XS1 = np.full((1, 3), 0.5, np.float32)
+    one = orc.f2h(1.0)
+    assert orc.tern_out_rs(acc1, XS1, np.full((3, 1), one, np.uint16), 1, 384)[0, 0] == 2.0 ** 23
+    # and XS multiplies the sum, not each term: v = (3), d = 1, XS = 1/3 gives fp32(3 * fp32(1/3)) = 1
+    third = np.float32(1.0) / np.float32(3.0)
+    assert orc.tern_out_rs(np.array([[[3]]], np.int32), np.array([[third]], np.float32),
+                           np.full((1, 1), one, np.uint16), 1, 128)[0, 0] == np.float32(3.0) * third
+
+
 def test_out_tree_cases(orc):
     """the split tree with one split and one slice is the sequential chain; other trees differ only in rounding"""
     R, C, M = 64, 2048, 2
