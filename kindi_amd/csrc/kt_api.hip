@@ -48,10 +48,18 @@ static int kt_kslices(int NU){
   return ks < KT_KSMAX ? ks : KT_KSMAX;
 }
 
-/* 5 .. 32 ternary tokens: the matrix-core product (the same numbers and tree), tiles of 32 rows of one matrix,
-   passes of 16 tokens */
-#define KT_MMA_MIN 5
+/* up to 32 ternary tokens: the matrix-core product (the same numbers and tree, so the same bits), tiles of 32 rows
+   of one matrix, passes of 16 tokens. It pays from 12 tokens on launches of 2^24 weights or more and from 24 tokens
+   on any (measured on MI355X: 27B-class layers from 12 tokens, 2B-class layers from about 24) */
+#define KT_MMA_MIN 12
+#define KT_MMA_ANY 24
 #define KT_MMA_MAX 32
+static bool kt_use_mma(const KtGemvArgs& a){
+  if(a.M < KT_MMA_MIN || a.M > KT_MMA_MAX) return false;
+  long long w = 0;
+  for(int i = 0; i < a.nmat; ++i) w += (long long)a.mat[i].R * a.NU * 128;
+  return a.M >= KT_MMA_ANY || w >= (1ll << 24);
+}
 static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, int32_t* dbg, hipStream_t s){
   const int ks = kt_kslices(a.NU);
   int tiles = 0;
@@ -68,7 +76,7 @@ static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, int32_
 template <int FMT>
 static int kt_launch_gemv(const KtGemvArgs& a, int ngroups, const int8_t* xq, const float* xs, const int* xa,
                           int32_t* dbg, hipStream_t s){
-  if(FMT == KT_FMT_TERN && a.M >= KT_MMA_MIN && a.M <= KT_MMA_MAX) return kt_launch_mma(a, xq, xs, dbg, s);
+  if(FMT == KT_FMT_TERN && kt_use_mma(a)) return kt_launch_mma(a, xq, xs, dbg, s);
   const int ks = kt_kslices(a.NU);
   int mt = a.M <= 1 ? 1 : a.M <= 2 ? 2 : 4;
   while(mt > 1 && (mt == 4 ? KtFlat<FMT, 4>::lds(ks) : KtFlat<FMT, 2>::lds(ks)) > 65536) mt >>= 1;

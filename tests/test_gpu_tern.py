@@ -72,20 +72,21 @@ def test_gemv_m1(kt, R, C):
     assert np.array_equal(host(Y2), y)
 
 
-@pytest.mark.parametrize("R,C", [(640, 1024), (2048, 6144)])
+@pytest.mark.parametrize("R,C", [(640, 1024), (2048, 6144), (4096, 4096)])
 def test_gemv_token_invariance(kt, R, C):
-    """a token's output does not depend on how many tokens share the pass (tc_hip.cu:14-15), for M = 1 .. 20"""
+    """a token's output does not depend on how many tokens share the pass (tc_hip.cu:14-15), for M = 1 .. 32: the
+    bandwidth kernel and the matrix-core kernel (from 12 tokens at 2^24 weights, from 24 on any) give the same bits"""
     lib, linear = kt
     say("gemv T-invariance", R, C)
     W, dig, bc, dpm = upload(linear, R, C, 5 + R)
     L = linear.Linear({"w": W})
-    X = rng(9).normal(0, 1, (20, C)).astype(np.float32)
+    X = rng(9).normal(0, 1, (32, C)).astype(np.float32)
     Xd = dev(X)
     Q, XS, XA = orc.quant_q8(X)
     acc = orc.tern_acc(bc, R, C, Q)
     dq = dpm.view(np.float16).astype(np.float32)
     tree = orc.out_lanes(acc, XS, dq, 8, 0, lib.kt_decode_kslices(C, 0))
-    for M in (1, 2, 3, 4, 5, 8, 9, 13, 16, 17, 20):
+    for M in (1, 2, 3, 4, 5, 8, 9, 12, 13, 16, 17, 20, 24, 32):
         act = linear.quantize(Xd[:M])
         Y = torch.empty((M, R), dtype=torch.float32, device="cuda")
         dbg = torch.empty((M, R, C // 128), dtype=torch.int32, device="cuda")
