@@ -14,6 +14,8 @@ __global__ void k_gemv_flat1(const KtGemvArgs, const KtGroupedArgs, const int8_t
                              int);
 template <int NT, bool DBG>
 __global__ void k_gemv_mma(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
+template <bool GRP, bool DBG>
+__global__ void k_q8_mma(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
 template <int MT> __global__ void k_plan(const uint8_t*, unsigned*);
 extern "C" __global__ void k_plan_reset(unsigned*, int);
 extern "C" __global__ void k_tern_pack(const uint8_t*, const uint16_t*, int, int, uint32_t*, uint16_t*);
@@ -54,6 +56,7 @@ static int kt_kslices(int NU){
 #define KT_MMA_MIN 12
 #define KT_MMA_ANY 24
 #define KT_MMA_MAX 32
+#define KT_Q8_MMA_KS 8                 /* q8_0 matrix-core product: K slices a block (kt_mma.hip KM_Q8_KS) */
 static bool kt_use_mma(const KtGemvArgs& a){
   if(a.M < KT_MMA_MIN || a.M > KT_MMA_MAX) return false;
   long long w = 0;
@@ -356,6 +359,17 @@ int kt_q8_gemv(const void* W, int R, int C, const int8_t* Q, int ldq, const floa
   a.nmat = 1; a.NU = NB;
   a.ldq = ldq; a.ldxs = ldd;
   a.M = M;
+  const int ks = kt_kslices(NB);
+  if(M >= KT_MMA_MIN && ks <= KT_Q8_MMA_KS){
+    /* the matrix-core product (the same numbers and tree): tiles of 32 rows, all tokens a block */
+    const dim3 grid((kt_r8(R) + 3) / 4), block(64 * ks);
+    const size_t lds = (size_t)ks * 16 * 32 * 4;
+    const KtGroupedArgs ga = {};
+    if(dbg) hipLaunchKernelGGL((k_q8_mma<false, true>), grid, block, lds, kt_stream(stream), a, ga, Q, D, dbg, ks);
+    else hipLaunchKernelGGL((k_q8_mma<false, false>), grid, block, lds, kt_stream(stream), a, ga, Q, D, dbg, ks);
+    KT_LAUNCH_CHECK();
+    return 0;
+  }
   return kt_launch_gemv<KT_FMT_Q8>(a, kt_r8(R), Q, D, NULL, dbg, kt_stream(stream));
 }
 
@@ -390,18 +404,29 @@ int kt_q8_grouped(const void* const* Wexp, int R, int C, int E, const int* cnt, 
   a.cnt = cnt; a.off = off; a.act = act; a.nact = nact; a.xrow = xrow;
   a.ldq = ldq; a.ldd = ldd; a.ldy = ldy;
   a.y = Y;
-  /* the decode product per (row group, active expert), the expert's list in chunks of up to 4 tokens */
   const int ks = kt_kslices(a.NU);
+  const int ny = E < nentries ? E : nentries;
+  hipStream_t s = kt_stream(stream);
+  if(nentries >= 4 * ny && ks <= KT_Q8_MMA_KS){
+    /* 4 or more entries an active expert on average: the matrix-core product per (32-row tile, active expert), the
+       expert's whole list in passes of 16 (the same numbers and tree) */
+    const dim3 grid((kt_r8(R) + 3) / 4, ny), block(64 * ks);
+    const size_t lds = (size_t)ks * 16 * 32 * 4;
+    const KtGemvArgs da = {};
+    if(dbg) hipLaunchKernelGGL((k_q8_mma<true, true>), grid, block, lds, s, da, a, Q, D, dbg, ks);
+    else hipLaunchKernelGGL((k_q8_mma<true, false>), grid, block, lds, s, da, a, Q, D, dbg, ks);
+    KT_LAUNCH_CHECK();
+    return 0;
+  }
+  /* the decode product per (row group, active expert), the expert's list in chunks of up to 4 tokens */
 #ifndef KT_GRP_MT
 #define KT_GRP_MT 2                   /* tokens a chunk in the grouped product (registers: more waves resident) */
 #endif
   int mt = M <= 1 ? 1 : M <= 2 ? 2 : 4;
   if(mt > KT_GRP_MT) mt = KT_GRP_MT;
   while(mt > 1 && (mt == 4 ? KtFlat<KT_FMT_Q8, 4>::lds(ks) : KtFlat<KT_FMT_Q8, 2>::lds(ks)) > 65536) mt >>= 1;
-  const int ny = E < nentries ? E : nentries;
   const dim3 grid(kt_r8(R), ny), block(64 * ks);
   const KtGemvArgs da = {};
-  hipStream_t s = kt_stream(stream);
 #define KT_GL(K, MT) do { const size_t lds = KtFlat<KT_FMT_Q8, MT>::lds(ks); \
     if(dbg) hipLaunchKernelGGL((K<KT_FMT_Q8, MT, true, true>), grid, block, lds, s, da, a, Q, D, nullptr, dbg, ks); \
     else hipLaunchKernelGGL((K<KT_FMT_Q8, MT, false, true>), grid, block, lds, s, da, a, Q, D, nullptr, dbg, ks); } while(0)

@@ -142,3 +142,137 @@ __global__ void __launch_bounds__(64 * KT_KSMAX) k_gemv_mma(const KtGemvArgs a, 
 
 template __global__ void k_gemv_mma<16, false>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
 template __global__ void k_gemv_mma<16, true>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
+
+/* ------------------------------------------------------------------ q8_0 on the matrix cores
+   The q8_0 product (kq8 weights against int8 rows with per-32 scales, lt_mv_q8 lightning.cu:258-284, k_q8
+   dsv41_gpu.cu:131-296) with the same numbers and tree as k_gemv_flat's q8_0 mode, dense (one matrix, tokens 0 ..
+   M - 1) or grouped (GRP: one active expert a block row, its token list: entry p reads input row xrow[p] or p and
+   writes output row p, lt_mm_* lightning.cu:958-1168). A q8_0 unit (32 columns) is one V_MFMA_I32_32X32X32_I8:
+   lane l holds weight row l % 32 and token l % 32, columns 16 h .. 16 h + 15 of the unit (h = l / 32), which is
+   exactly one 16-byte load of the kq8 layout (kt_widx with half h). Block: KS waves over one tile of 32 weight rows
+   (4 row groups), wave ks the K slice ks; the slice's weights are loaded once and serve every pass of 16 tokens of
+   the block's list. Epilogue as k_gemv_flat: per k-lane c the chain fmaf((float)v, d * D[t][u], .) over the slice's
+   units 8 s + c, the butterfly's tree over c, the slices in order. */
+#define KM_Q8_KS 8                    /* at most 8 K slices (q8_0 C <= 4096): 256 VGPRs a lane */
+template <bool GRP, bool DBG>
+__global__ void __launch_bounds__(64 * KM_Q8_KS) k_q8_mma(const KtGemvArgs a, const KtGroupedArgs ga,
+                                                          const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                          int32_t* __restrict__ dbg, int KS){
+  constexpr int NT = KM_TOK, NE = NT / 2;
+  extern __shared__ __attribute__((aligned(16))) uint8_t kt_lds[];
+  float* red = (float*)kt_lds;                                   /* [KS][NT][32] slice sums */
+  const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = lane >> 5, lr = lane & 31;
+  const int tile = blockIdx.x;
+  const uint4* __restrict__ wb;
+  const uint16_t* __restrict__ sb;
+  float* yout;
+  int R, ldy, NU, ldq, ldd, cntM, p0;
+  const int* xrow = nullptr;
+  if(GRP){
+    if((int)blockIdx.y >= *ga.nact) return;
+    const int e = ga.act[blockIdx.y];
+    const uint8_t* base = ga.wexp[e];
+    NU = ga.NU; R = ga.R;
+    wb = (const uint4*)base;
+    sb = (const uint16_t*)(base + (long long)kt_r8(R) * NU * 256);
+    ldy = ga.ldy; ldq = ga.ldq; ldd = ga.ldd; cntM = ga.cnt[e]; p0 = ga.off[e]; xrow = ga.xrow;
+    yout = ga.y;
+  } else {
+    NU = a.NU; R = a.mat[0].R;
+    wb = (const uint4*)a.mat[0].codes;
+    sb = a.mat[0].scales;
+    ldy = a.mat[0].ldy; ldq = a.ldq; ldd = a.ldxs; cntM = a.M; p0 = 0;
+    yout = a.mat[0].y;
+  }
+  const int S = kt_steps(NU);
+  const int rg = tile * 4 + (lr >> 3), r = lr & 7, row = rg * KT_RG + r;
+  const bool rok = row < R;
+  const int s_lo = ks * S / KS, ns = (ks + 1) * S / KS - s_lo;   /* this slice's steps (1 or 2) */
+
+  /* the slice's 16 units in k-lane-major order, loaded once (unconditional: a unit past the slice or the matrix
+     reads offset 0) */
+  uint4 wq[2][KT_KL];
+  uint16_t hq[2][KT_KL];
+#pragma unroll
+  for(int c = 0; c < KT_KL; ++c)
+#pragma unroll
+    for(int j = 0; j < 2; ++j){
+      const int s = s_lo + j, u = s * KT_KL + c;
+      const bool ok = rok && j < ns && u < NU;
+      wq[j][c] = kt_ldnt(wb + (ok ? kt_widx(NU, rg, s, h, c, r) : 0));
+      hq[j][c] = sb[ok ? kt_sidx(NU, rg, u, r) : 0];
+    }
+
+  for(int t0 = 0; t0 < cntM; t0 += NT){                          /* uniform: the block's list in passes */
+    const int nt = min(NT, cntM - t0);
+    const bool tok_ok = lr < nt;
+    const int pe = p0 + t0 + (tok_ok ? lr : 0);
+    const int n_a = xrow ? xrow[pe] : pe;                        /* this lane's A row */
+    int n_e[NE];                                                 /* the input rows of this lane's D registers */
+#pragma unroll
+    for(int e = 0; e < NE; ++e){
+      const int t = km_tok(e, lane), pt = p0 + t0 + (t < nt ? t : 0);
+      n_e[e] = xrow ? xrow[pt] : pt;
+    }
+    float part[NE], t01[NE], t23[NE], t45[NE], pend[NE];
+#pragma unroll
+    for(int e = 0; e < NE; ++e){ part[e] = 0.0f; t01[e] = 0.0f; t23[e] = 0.0f; t45[e] = 0.0f; pend[e] = 0.0f; }
+#pragma unroll
+    for(int c = 0; c < KT_KL; ++c){
+      float chain[NE];
+#pragma unroll
+      for(int e = 0; e < NE; ++e) chain[e] = 0.0f;
+#pragma unroll
+      for(int j = 0; j < 2; ++j){
+        const int s = s_lo + j, u = s * KT_KL + c;
+        const bool uok = j < ns && u < NU;                      /* wave-uniform */
+        const int uu = uok ? u : 0;
+        const uint4 xa = *(const uint4*)(xq + (long long)n_a * ldq + (long long)uu * 32 + 16 * h);
+        if(uok){
+          const float d = rok ? kt_h2f(hq[j][c]) : 0.0f;
+          kt_v4i A, B;
+          A[0] = tok_ok ? (int)xa.x : 0; A[1] = tok_ok ? (int)xa.y : 0;
+          A[2] = tok_ok ? (int)xa.z : 0; A[3] = tok_ok ? (int)xa.w : 0;
+          B[0] = (int)wq[j][c].x; B[1] = (int)wq[j][c].y; B[2] = (int)wq[j][c].z; B[3] = (int)wq[j][c].w;
+          const kt_v16i acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, (kt_v16i){}, 0, 0, 0);
+#pragma unroll
+          for(int e = 0; e < NE; ++e){
+            const float sx = xd[(long long)n_e[e] * ldd + u];
+            chain[e] = fmaf((float)acc[e], d * sx, chain[e]);
+            if(DBG){
+              const int t = t0 + km_tok(e, lane);
+              if(t < cntM && rok) dbg[((long long)(p0 + t) * R + row) * NU + u] = acc[e];
+            }
+          }
+        }
+      }
+#pragma unroll
+      for(int e = 0; e < NE; ++e){
+        if(c == 0 || c == 2 || c == 4 || c == 6) pend[e] = chain[e];
+        else if(c == 1) t01[e] = pend[e] + chain[e];
+        else if(c == 3) t23[e] = t01[e] + (pend[e] + chain[e]);
+        else if(c == 5) t45[e] = pend[e] + chain[e];
+        else part[e] = t23[e] + (t45[e] + (pend[e] + chain[e]));
+      }
+    }
+#pragma unroll
+    for(int e = 0; e < NE; ++e) red[((size_t)ks * NT + km_tok(e, lane)) * 32 + lr] = part[e];
+    __syncthreads();
+    if(ks == 0){
+#pragma unroll
+      for(int e = 0; e < NE; ++e){
+        const int tl = km_tok(e, lane), t = t0 + tl;
+        float v = red[(size_t)tl * 32 + lr];
+        for(int k = 1; k < KS; ++k) v += red[((size_t)k * NT + tl) * 32 + lr];
+        if(t < cntM && rok) yout[(long long)(p0 + t) * ldy + row] = v;
+      }
+    }
+    __syncthreads();                                             /* red is rewritten by the next pass */
+  }
+}
+
+template __global__ void k_q8_mma<false, false>(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
+template __global__ void k_q8_mma<false, true>(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
+template __global__ void k_q8_mma<true, false>(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
+template __global__ void k_q8_mma<true, true>(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);

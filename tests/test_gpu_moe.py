@@ -32,7 +32,8 @@ def test_q8_quant_bit_exact(kt, M, C, act):
     assert np.array_equal(host(D), d)
 
 
-@pytest.mark.parametrize("R,C,M", [(64, 32, 1), (100, 96, 3), (1856, 2688, 1), (2688, 1856, 6), (1856, 2688, 16)])
+@pytest.mark.parametrize("R,C,M", [(64, 32, 1), (100, 96, 3), (1856, 2688, 1), (2688, 1856, 6), (1856, 2688, 16),
+                                   (100, 96, 13), (2688, 1856, 40)])
 def test_q8_gemv(kt, R, C, M):
     lib, moe = kt
     say("q8 gemv", R, C, M)
@@ -99,7 +100,7 @@ def oracle_moe(x, lg, up_rows, down_rows, H, F, k):
     return orc.moe_combine(yd, None, where, gw, x), yd, u, ids, gw
 
 
-@pytest.mark.parametrize("M", [1, 64])
+@pytest.mark.parametrize("M", [1, 64, 256])
 def test_moe_forward_config4(kt, M):
     """config 4 shapes: 128 experts, up [1856 x 2688], down [2688 x 1856], top-6. Stage by stage, each oracle stage
     fed the GPU's previous stage: routing and lists exact, up / down within 1e-3 (their unit values exact), the
