@@ -239,6 +239,63 @@ def config4(torch, moe, synth, timer, steps, use_graph):
     return res
 
 
+def producers(torch, linear, synth, timer, steps, use_graph):
+    """the fused input producers (kt_rmsfold_q8 / kt_fold_q8 / kt_smfold_q8): a 27B-class decode layer's four
+    (attention rmsfold with one residual part, o-input fold, FFN rmsfold with one part, down-input smfold over
+    17408 columns) at M = 1 / 16, and a 9B-class prefill pair (rmsfold 4096, smfold 12288, HB 4096) at M = 2048.
+    Bytes: fp32 inputs and parts read once, weights/signs once, x + parts and the int8 row with XS/XA written."""
+    def sgn(C, seed):
+        return torch.where(torch.rand(C, device="cuda", generator=torch.Generator("cuda").manual_seed(seed)) < 0.5,
+                           -1.0, 1.0).float()
+
+    def qbytes(M, C):
+        return M * C + M * (C // 128) * 8
+
+    res = {}
+    mats = synth.CFG["c3"]["mats"]
+    H, F = mats[0][2], mats[4][1]                       # hidden 5120, FFN 17408
+    for M in (1, 16):
+        x = synth.activations(M, H, 60, device="cuda")
+        r = synth.activations(M, H, 61, device="cuda")
+        a = synth.activations(M, F, 62, device="cuda")
+        b2 = synth.activations(M, F, 63, device="cuda")
+        w, sgH, sgF = torch.ones(H, device="cuda"), sgn(H, 1), sgn(F, 2)
+        xw = torch.empty_like(x)
+        oH = linear._act_out(M, H, "cuda")
+        oF = linear._act_out(M, F, "cuda")
+        reps = 20
+
+        def fn():
+            for _ in range(reps):
+                linear.rmsfold(x, w, sgH, 1024, r=r, nparts=1, xw=xw, out=oH)
+                linear.fold(x, sgH, 1024, out=oH)
+                linear.rmsfold(x, w, sgH, 1024, r=r, nparts=1, xw=xw, out=oH)
+                linear.smfold(a, b2, sgF, 1024, out=oF)
+
+        ms = timer.run(graphed(torch, fn, use_graph), steps, 2) / reps
+        nb = 2 * (3 * M * H * 4 + 2 * H * 4 + qbytes(M, H)) + (M * H * 4 + H * 4 + qbytes(M, H)) \
+            + (2 * M * F * 4 + F * 4 + qbytes(M, F))
+        res["27B layer M=%d" % M] = {"us_per_layer": round(ms * 1e3, 2), "launches": 4, "bytes": nb,
+                                     "GB/s": round(nb / ms / 1e6, 1)}
+    M, H9, F9 = 2048, 4096, 12288
+    x = synth.activations(M, H9, 64, device="cuda")
+    r = synth.activations(M, H9, 65, device="cuda")
+    a = synth.activations(M, F9, 66, device="cuda")
+    b2 = synth.activations(M, F9, 67, device="cuda")
+    w, sgH, sgF = torch.ones(H9, device="cuda"), sgn(H9, 3), sgn(F9, 4)
+    xw = torch.empty_like(x)
+    oH, oF = linear._act_out(M, H9, "cuda"), linear._act_out(M, F9, "cuda")
+    ms_r = timer.run(lambda: linear.rmsfold(x, w, sgH, 4096, r=r, nparts=1, xw=xw, out=oH), max(steps // 2, 3), 2)
+    ms_s = timer.run(lambda: linear.smfold(a, b2, sgF, 4096, out=oF), max(steps // 2, 3), 2)
+    nr = 3 * M * H9 * 4 + 2 * H9 * 4 + qbytes(M, H9)
+    ns = 2 * M * F9 * 4 + F9 * 4 + qbytes(M, F9)
+    res["9B prefill M=2048 rmsfold"] = {"us": round(ms_r * 1e3, 1), "GB/s": round(nr / ms_r / 1e6, 1),
+                                        "frac_hbm": round(nr / ms_r / 1e6 / HBM_PEAK, 4)}
+    res["9B prefill M=2048 smfold"] = {"us": round(ms_s * 1e3, 1), "GB/s": round(ns / ms_s / 1e6, 1),
+                                       "frac_hbm": round(ns / ms_s / 1e6 / HBM_PEAK, 4)}
+    return res
+
+
 # ----------------------------------------------------------------------------------------------- CPU baseline
 def cpu_baseline(synth, budget_s=12.0, nlayers=4):
     """kcpu.c's pair-table GEMV over 27B layers (7 matrices each), on the host's cores. nlayers distinct layers
@@ -380,6 +437,8 @@ def main():
         cfgs["c1"] = config1(torch, linear, synth, timer, a.steps, use_graph)
         cfgs["c2"] = config2(torch, linear, synth, timer, a.steps)
         cfgs["c4"] = config4(torch, moe, synth, timer, a.steps, use_graph)
+        log("input producers")
+        cfgs["producers"] = producers(torch, linear, synth, timer, a.steps, use_graph)
         out["configs"] = cfgs
     if not a.no_cpu:
         log("cpu baseline")

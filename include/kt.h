@@ -153,6 +153,27 @@ int kt_q8_grouped(const void* const* Wexp, int R, int C, int E, const int* cnt, 
 int kt_moe_combine(const float* yd, const float* ysh, const int* where, const float* gw, int M, int k, int cols,
                    float* x, void* stream);
 
+/* ---------------------------------------------------------------- fused input producers
+   One launch makes a product's int8 input from the fp32 stream, with the reference's numbers bit for bit:
+   kt_rmsfold_q8 replaces k_rmsfold_qT (tcf.cu:370-390; k_rmsfold kindi.cu:350-394): per token row n,
+     xf = x + (r_0 + r_1 + ... + r_{nparts-1})   (parts C apart: token n's part p at r + n ldr + p C; 0 <= nparts <= 8)
+     xn = (xf * s) * w,  s = 1 / sqrt((float)(S / C) + 1e-6), S the double sum of squares in the reference's order
+     xo = fold(sg * xn),  then XQ / XS / XA of xo as kt_quant_q8 (per_row = 0) makes them.
+   kt_fold_q8 replaces k_fold_fwht_qT (tcf.cu:410-426): xo = fold(sg * x).
+   kt_smfold_q8 replaces k_smfold_qT (tcf.cu:392-408): xo[e] = fold(sg[e] * SiLU(a[s]) * b[s]) with s the grouped-head
+     source column of e (rep > 1: e = h + hd (i + rep k) reads h + hd (k + nk i), hd nk rep = C; rep = 1: s = e).
+   fold = the unnormalised Walsh-Hadamard transform of each HB-column block times 1/sqrt(HB), HB in {512, 1024,
+   4096}. C % HB == 0; rmsfold takes C <= 8192 (one block holds the row for the norm), fold / smfold any width up to
+   2^20 (chunks of whole HB blocks). M <= 65535. xw (x + parts, only with nparts > 0), xn and xo are nullable;
+   xw may be x itself. The reference's two-row high-precision mode (hp) is not offered. */
+int kt_rmsfold_q8(const float* x, int ldx, const float* r, int ldr, int nparts, const float* w, const float* sg, int M,
+                  int C, int HB, float* xw, int ldxw, float* xn, int ldxn, float* xo, int ldxo, int8_t* XQ, int ldq,
+                  float* XS, int32_t* XA, void* stream);
+int kt_fold_q8(const float* x, int ldx, const float* sg, int M, int C, int HB, float* xo, int ldxo, int8_t* XQ,
+               int ldq, float* XS, int32_t* XA, void* stream);
+int kt_smfold_q8(const float* a, int lda, const float* b, int ldb, const float* sg, int hd, int nk, int rep, int M,
+                 int C, int HB, float* xo, int ldxo, int8_t* XQ, int ldq, float* XS, int32_t* XA, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,6 +5,7 @@
 #include "kt_common.h"
 #include <vector>
 #include "../../include/kt.h"
+#include "kt_fold.h"
 
 template <int FMT, int MT, bool DBG, bool GRP>
 __global__ void k_gemv_flat(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, const int*, int32_t*,
@@ -443,6 +444,44 @@ int kt_moe_combine(const float* yd, const float* ysh, const int* where, const fl
   hipLaunchKernelGGL(k_moe_combine, dim3(M), dim3(256), 0, kt_stream(stream), yd, ysh, where, gw, k, cols, x);
   KT_LAUNCH_CHECK();
   return 0;
+}
+
+/* ------------------------------------------------------------------ fused input producers (kt_fold.hip) */
+static bool kt_fold_shape(int M, int C, int HB, const float* sg, int8_t* XQ, int ldq, float* XS, int32_t* XA){
+  return M >= 0 && M <= 65535 && C >= 512 && C <= (1 << 20) && (HB == 512 || HB == 1024 || HB == 4096)
+      && C % HB == 0 && sg && XQ && XS && XA && ldq >= C;
+}
+
+static int kt_fold_run(int mode, const KtFoldArgs& a, int M, void* stream){
+  if(M == 0) return 0;
+  return (int)kt_fold_launch(mode, a, M, kt_stream(stream));
+}
+
+int kt_rmsfold_q8(const float* x, int ldx, const float* r, int ldr, int nparts, const float* w, const float* sg, int M,
+                  int C, int HB, float* xw, int ldxw, float* xn, int ldxn, float* xo, int ldxo, int8_t* XQ, int ldq,
+                  float* XS, int32_t* XA, void* stream){
+  if(!kt_fold_shape(M, C, HB, sg, XQ, ldq, XS, XA) || C > 8192 || !x || !w || ldx < C || nparts < 0 || nparts > 8
+     || (nparts > 0 && (!r || ldr < nparts * C)) || (xw && ldxw < C) || (xn && ldxn < C) || (xo && ldxo < C))
+    return KT_INVALID;
+  KtFoldArgs a = {x, ldx, r, ldr, nparts, w, sg, 1, 1, 1, xw, ldxw, xn, ldxn, xo, ldxo, C, HB, XQ, ldq, XS, XA};
+  return kt_fold_run(0, a, M, stream);
+}
+
+int kt_fold_q8(const float* x, int ldx, const float* sg, int M, int C, int HB, float* xo, int ldxo, int8_t* XQ,
+               int ldq, float* XS, int32_t* XA, void* stream){
+  if(!kt_fold_shape(M, C, HB, sg, XQ, ldq, XS, XA) || !x || ldx < C || (xo && ldxo < C)) return KT_INVALID;
+  KtFoldArgs a = {x, ldx, nullptr, 0, 0, nullptr, sg, 1, 1, 1, nullptr, 0, nullptr, 0, xo, ldxo, C, HB, XQ, ldq, XS, XA};
+  return kt_fold_run(1, a, M, stream);
+}
+
+int kt_smfold_q8(const float* a_, int lda, const float* b, int ldb, const float* sg, int hd, int nk, int rep, int M,
+                 int C, int HB, float* xo, int ldxo, int8_t* XQ, int ldq, float* XS, int32_t* XA, void* stream){
+  if(!kt_fold_shape(M, C, HB, sg, XQ, ldq, XS, XA) || !a_ || !b || lda < C || ldb < C || (xo && ldxo < C) || rep < 1
+     || (rep > 1 && (hd <= 0 || nk <= 0 || (long long)hd * nk * rep != C)))
+    return KT_INVALID;
+  KtFoldArgs a = {a_, lda, b, ldb, 0, nullptr, sg, hd, nk, rep, nullptr, 0, nullptr, 0, xo, ldxo, C, HB, XQ, ldq, XS,
+                  XA};
+  return kt_fold_run(2, a, M, stream);
 }
 
 }  /* extern "C" */

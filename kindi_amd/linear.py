@@ -88,6 +88,62 @@ def quantize(X, per_row=False, out=None):
     return Act(out.XQ, out.XS, out.XA, M, C, per_row)
 
 
+def _act_out(M, C, device):
+    return Act(torch.empty((M, C), dtype=torch.int8, device=device),
+               torch.empty((M, C // 128), dtype=torch.float32, device=device),
+               torch.empty((M, C // 128), dtype=torch.int32, device=device), M, C, False)
+
+
+def _f32_rows(t, what):
+    if t is None:
+        return None
+    if t.dtype != torch.float32 or t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError("%s: fp32 rows with unit column stride" % what)
+    return t
+
+
+def rmsfold(x, w, sg, HB, r=None, nparts=0, xw=None, xn=None, xo=None, out=None):
+    """k_rmsfold_qT (tcf.cu:370-390; k_rmsfold kindi.cu:350-394) as one launch: x [M, C] fp32 (+ the nparts residual
+    parts of r [M, >= nparts C], C apart, in part order) -> RMS norm (weights w) -> sign sg -> Hadamard fold of each
+    HB block -> int8 row. Returns the Act; xw (x + parts), xn (normed) and xo (folded) are written when given."""
+    x = _f32_rows(x.reshape(1, -1) if x.dim() == 1 else x, "x")
+    M, C = x.shape
+    _f32_rows(r, "r"), _f32_rows(xw, "xw"), _f32_rows(xn, "xn"), _f32_rows(xo, "xo")
+    out = out or _act_out(M, C, x.device)
+    gpudrv.check(gpudrv.load().kt_rmsfold_q8(
+        ptr(x), x.stride(0), ptr(r), r.stride(0) if r is not None else 0, nparts, ptr(w), ptr(sg), M, C, HB,
+        ptr(xw), xw.stride(0) if xw is not None else 0, ptr(xn), xn.stride(0) if xn is not None else 0,
+        ptr(xo), xo.stride(0) if xo is not None else 0, ptr(out.XQ), out.XQ.stride(0), ptr(out.XS), ptr(out.XA),
+        stream()), "kt_rmsfold_q8")
+    return Act(out.XQ, out.XS, out.XA, M, C, False)
+
+
+def fold(x, sg, HB, xo=None, out=None):
+    """k_fold_fwht_qT (tcf.cu:410-426): sign, Hadamard fold of each HB block, int8 row"""
+    x = _f32_rows(x.reshape(1, -1) if x.dim() == 1 else x, "x")
+    M, C = x.shape
+    _f32_rows(xo, "xo")
+    out = out or _act_out(M, C, x.device)
+    gpudrv.check(gpudrv.load().kt_fold_q8(ptr(x), x.stride(0), ptr(sg), M, C, HB, ptr(xo),
+                                          xo.stride(0) if xo is not None else 0, ptr(out.XQ), out.XQ.stride(0),
+                                          ptr(out.XS), ptr(out.XA), stream()), "kt_fold_q8")
+    return Act(out.XQ, out.XS, out.XA, M, C, False)
+
+
+def smfold(a, b, sg, HB, perm=(1, 1, 1), xo=None, out=None):
+    """k_smfold_qT (tcf.cu:392-408): SiLU(a) * b in the grouped-head order perm = (hd, nk, rep), sign, fold, int8"""
+    a = _f32_rows(a.reshape(1, -1) if a.dim() == 1 else a, "a")
+    b = _f32_rows(b.reshape(1, -1) if b.dim() == 1 else b, "b")
+    M, C = a.shape
+    _f32_rows(xo, "xo")
+    out = out or _act_out(M, C, a.device)
+    gpudrv.check(gpudrv.load().kt_smfold_q8(ptr(a), a.stride(0), ptr(b), b.stride(0), ptr(sg), perm[0], perm[1],
+                                            perm[2], M, C, HB, ptr(xo), xo.stride(0) if xo is not None else 0,
+                                            ptr(out.XQ), out.XQ.stride(0), ptr(out.XS), ptr(out.XA), stream()),
+                 "kt_smfold_q8")
+    return Act(out.XQ, out.XS, out.XA, M, C, False)
+
+
 class Linear(object):
     """The ternary tensors of a model and the products over them (Kindi's linear-call surface).
 

@@ -430,3 +430,127 @@ void or_router_topk(const float* logits, int M, int E, int k, int* ids, float* g
     for(int j = 0; j < k; ++j) gw[t * k + j] = p[j] / s;
   }
 }
+
+/* ------------------------------------------------------------------ fused producers of a product's input
+   k_rmsfold_qT / k_fold_fwht_qT / k_smfold_qT (tcf.cu:370-426; the numbers of k_rmsfold kindi.cu:350-394 and the
+   fast forms ff_rmsfold / ff_fold / ff_smfold tcf.cu:218-312, which are bit-identical to them). Per token row:
+     rmsfold: xf = x + (r_0 + r_1 + ... + r_{n-1})          parts summed in part order (rsum kindi.cu:344-348)
+              s  = 1 / sqrt((float)(S / C) + 1e-6)            S: the double sum of squares in the reference's order
+              xn = (xf * s) * w;  v = sg * xn
+     fold:    v = sg * x
+     smfold:  v = sg[e] * ((a / (1 + exp(-a))) * b) at the permuted source column (tcf.cu:284-291)
+   then v goes through the unnormalised Walsh-Hadamard transform of each HB-column block (stages h = 1, 2, 4, ... in
+   order, pair (i, i + h) -> (a + b, a - b): fwht_chunks / fwht_n kindi.cu:91-116, ff_fwht tcf.cu:60-96), is scaled by
+   1/sqrt(HB) (the fp32 constant 0.044194173824159220878 for HB = 512, exactly 2^-5 / 2^-6 for 1024 / 4096,
+   ff_scale_store tcf.cu:98-104), stored as xo, and quantized to int8 per 128-column group with k_tc_q8's numbers
+   (or_quant_q8 above; ff_q8_row tcf.cu:106-150).
+   The double sum of squares: thread j of 512 adds (double)xf[j + 512 m]^2 for m = 0, 1, ... in order; each warp of
+   32 threads combines by the xor butterfly (offsets 16, 8, 4, 2, 1: wsum_d kindi.cu:81-84); warp 0 takes the 16 warp
+   sums (lanes 16..31 zero) through the same butterfly (kindi.cu:367-373). */
+static double or_bfly32(double* a){
+  double b[32];
+  for(int o = 16; o > 0; o >>= 1){
+    for(int l = 0; l < 32; ++l) b[l] = a[l] + a[l ^ o];
+    memcpy(a, b, sizeof(b));
+  }
+  return a[0];
+}
+
+double or_sumsq(const float* xf, int C){
+  double warp[32], red[32];
+  for(int w = 0; w < 16; ++w){
+    for(int l = 0; l < 32; ++l){
+      const int j = 32 * w + l;
+      double acc = 0.0;
+      for(int e = j; e < C; e += 512){ const double d = (double)xf[e]; acc += d * d; }
+      warp[l] = acc;
+    }
+    red[w] = or_bfly32(warp);
+  }
+  for(int l = 16; l < 32; ++l) red[l] = 0.0;
+  return or_bfly32(red);
+}
+
+static float or_fold_scale(int HB){
+  return HB == 512 ? 0.044194173824159220878f : (float)(1.0 / sqrt((double)HB));
+}
+
+/* in place: the unnormalised transform of each HB block of v[0..C), then the scale */
+void or_fwht_blocks(float* v, int C, int HB){
+  const float sc = or_fold_scale(HB);
+  for(int b0 = 0; b0 < C; b0 += HB){
+    float* u = v + b0;
+    for(int h = 1; h < HB; h <<= 1)
+      for(int i = 0; i < HB; ++i)
+        if(!(i & h)){ const float a = u[i], b = u[i + h]; u[i] = a + b; u[i + h] = a - b; }
+  }
+  for(int e = 0; e < C; ++e) v[e] = v[e] * sc;
+}
+
+/* r: token n's parts at r + n ldr + p C (the parts of a column-split product, C apart, tc.cu:403) */
+void or_rmsfold_q8(const float* x, int ldx, const float* r, int ldr, int nparts, const float* w, const float* sg,
+                   int M, int C, int HB, float* xw, int ldxw, float* xn, int ldxn, float* xo, int ldxo,
+                   int8_t* Q, int ldq, float* XS, int* XA){
+  float* xf = (float*)malloc(sizeof(float) * C);
+  float* v = (float*)malloc(sizeof(float) * C);
+  for(int n = 0; n < M; ++n){
+    for(int e = 0; e < C; ++e){
+      float f = x[(size_t)n * ldx + e];
+      if(nparts > 0){
+        const float* rn = r + (size_t)n * ldr;
+        float rv = rn[e];
+        for(int p = 1; p < nparts; ++p) rv += rn[(size_t)p * C + e];
+        f = f + rv;
+      }
+      xf[e] = f;
+    }
+    const double S = or_sumsq(xf, C);
+    const float s = 1.0f / sqrtf((float)(S / C) + 1e-6f);
+    for(int e = 0; e < C; ++e){
+      const float nv = (xf[e] * s) * w[e];
+      if(nparts > 0 && xw) xw[(size_t)n * ldxw + e] = xf[e];
+      if(xn) xn[(size_t)n * ldxn + e] = nv;
+      v[e] = sg[e] * nv;
+    }
+    or_fwht_blocks(v, C, HB);
+    if(xo) memcpy(xo + (size_t)n * ldxo, v, sizeof(float) * C);
+    or_quant_q8(v, C, 1, C, 0, Q + (size_t)n * ldq, ldq, XS + (size_t)n * (C / 128), XA + (size_t)n * (C / 128));
+  }
+  free(xf); free(v);
+}
+
+void or_fold_q8(const float* x, int ldx, const float* sg, int M, int C, int HB, float* xo, int ldxo,
+                int8_t* Q, int ldq, float* XS, int* XA){
+  float* v = (float*)malloc(sizeof(float) * C);
+  for(int n = 0; n < M; ++n){
+    for(int e = 0; e < C; ++e) v[e] = sg[e] * x[(size_t)n * ldx + e];
+    or_fwht_blocks(v, C, HB);
+    if(xo) memcpy(xo + (size_t)n * ldxo, v, sizeof(float) * C);
+    or_quant_q8(v, C, 1, C, 0, Q + (size_t)n * ldq, ldq, XS + (size_t)n * (C / 128), XA + (size_t)n * (C / 128));
+  }
+  free(v);
+}
+
+/* the source column of output column e under the grouped-head order (tcf.cu:284-289; perm_rep <= 1: none) */
+int or_perm_src(int e, int hd, int nk, int rep){
+  if(rep <= 1) return e;
+  const int h = e % hd, g = e / hd, rp = g % rep, k = g / rep;
+  return h + hd * (k + nk * rp);
+}
+
+void or_smfold_q8(const float* a, int lda, const float* b, int ldb, const float* sg, int hd, int nk, int rep,
+                  int M, int C, int HB, float* xo, int ldxo, int8_t* Q, int ldq, float* XS, int* XA){
+  float* v = (float*)malloc(sizeof(float) * C);
+  for(int n = 0; n < M; ++n){
+    for(int e = 0; e < C; ++e){
+      const int src = or_perm_src(e, hd, nk, rep);
+      const float xa = a[(size_t)n * lda + src];
+      const float m = (xa / (1.0f + expf(-xa))) * b[(size_t)n * ldb + src];
+      v[e] = sg[e] * m;
+    }
+    or_fwht_blocks(v, C, HB);
+    if(xo) memcpy(xo + (size_t)n * ldxo, v, sizeof(float) * C);
+    or_quant_q8(v, C, 1, C, 0, Q + (size_t)n * ldq, ldq, XS + (size_t)n * (C / 128), XA + (size_t)n * (C / 128));
+  }
+  free(v);
+}

@@ -61,6 +61,13 @@ def lib():
         h.or_moe_sort.argtypes = [P, I, I, I, P, P, P, P]
         h.or_moe_combine.argtypes = [P, P, P, P, I, I, I, P]
         h.or_router_topk.argtypes = [P, I, I, I, P, P]
+        h.or_sumsq.argtypes = [P, I]
+        h.or_sumsq.restype = ctypes.c_double
+        h.or_fwht_blocks.argtypes = [P, I, I]
+        h.or_rmsfold_q8.argtypes = [P, I, P, I, I, P, P, I, I, I, P, I, P, I, P, I, P, I, P, P]
+        h.or_fold_q8.argtypes = [P, I, P, I, I, I, P, I, P, I, P, P]
+        h.or_perm_src.argtypes = [I, I, I, I]
+        h.or_smfold_q8.argtypes = [P, I, P, I, P, I, I, I, I, I, I, P, I, P, I, P, P]
         _lib[0] = h
     return _lib[0]
 
@@ -400,3 +407,55 @@ def ref_k_q8g(g4, R, C, q, d):
     for g in range(R // 4):
         h.ref_k_q8g(g4[g].ctypes.data_as(P), nb, 1, _p(q), _p(d), C, y[4 * g:].ctypes.data_as(P), 1)
     return y
+
+
+# ----------------------------------------------------------------------------------------------- fused producers
+def _prod_out(M, C):
+    return (np.empty((M, C), np.float32), np.empty((M, C), np.int8), np.empty((M, C // 128), np.float32),
+            np.empty((M, C // 128), np.int32))
+
+
+def sumsq(xf):
+    """the reference's double sum of squares of one row (512 threads, 32-lane butterflies)"""
+    xf = _c(xf, np.float32)
+    return lib().or_sumsq(_p(xf), xf.size)
+
+
+def fwht_blocks(v, HB):
+    """per-HB-block unnormalised Walsh-Hadamard transform, then the 1/sqrt(HB) scale (returns a new array)"""
+    v = np.array(v, dtype=np.float32, copy=True)
+    lib().or_fwht_blocks(_p(v), v.size, HB)
+    return v
+
+
+def rmsfold_q8(x, r, nparts, w, sg, HB):
+    """k_rmsfold_qT: x [M, C]; r [M, nparts * C] (parts C apart) or None -> dict xw, xn, xo, Q, XS, XA"""
+    x = _c(x, np.float32)
+    M, C = x.shape
+    rr = _c(r, np.float32).reshape(M, -1) if nparts else None
+    xw = np.empty((M, C), np.float32)
+    xn = np.empty((M, C), np.float32)
+    xo, Q, XS, XA = _prod_out(M, C)
+    lib().or_rmsfold_q8(_p(x), C, _p(rr), rr.shape[1] if nparts else 0, nparts, _p(_c(w, np.float32)),
+                        _p(_c(sg, np.float32)), M, C, HB, _p(xw), C, _p(xn), C, _p(xo), C, _p(Q), C, _p(XS), _p(XA))
+    return dict(xw=xw if nparts else None, xn=xn, xo=xo, Q=Q, XS=XS, XA=XA)
+
+
+def fold_q8(x, sg, HB):
+    """k_fold_fwht_qT: x [M, C] -> dict xo, Q, XS, XA"""
+    x = _c(x, np.float32)
+    M, C = x.shape
+    xo, Q, XS, XA = _prod_out(M, C)
+    lib().or_fold_q8(_p(x), C, _p(_c(sg, np.float32)), M, C, HB, _p(xo), C, _p(Q), C, _p(XS), _p(XA))
+    return dict(xo=xo, Q=Q, XS=XS, XA=XA)
+
+
+def smfold_q8(a, b, sg, HB, perm=(1, 1, 1)):
+    """k_smfold_qT: SiLU(a) * b at the permuted columns (perm = (hd, nk, rep)) -> dict xo, Q, XS, XA"""
+    a = _c(a, np.float32)
+    b = _c(b, np.float32)
+    M, C = a.shape
+    xo, Q, XS, XA = _prod_out(M, C)
+    lib().or_smfold_q8(_p(a), C, _p(b), C, _p(_c(sg, np.float32)), perm[0], perm[1], perm[2], M, C, HB, _p(xo), C,
+                       _p(Q), C, _p(XS), _p(XA))
+    return dict(xo=xo, Q=Q, XS=XS, XA=XA)

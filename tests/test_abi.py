@@ -27,7 +27,7 @@ def lib():
 
 def test_exports_every_declared_symbol(lib):
     names = declared()
-    assert len(names) == 23
+    assert len(names) == 26
     for n in names:
         assert hasattr(lib, n), n
     from kindi_amd import gpudrv
@@ -100,3 +100,29 @@ def test_plan_validation(lib):
     assert build(stage(R=0)) == INVALID                    # no matrix
     assert build(stage(ldq=5128)) == INVALID               # ldq % 16
     assert lib.kt_plan_run(None, ctypes.byref(info), None) == INVALID
+
+
+def test_fold_validation(lib):
+    f = ctypes.c_void_p(0x1000)
+    ok = (f, 5120, None, 0, 0, f, f, 1, 5120, 1024, None, 0, None, 0, None, 0, f, 5120, f, f, None)
+
+    def call(**kw):
+        a = list(ok)
+        names = ["x", "ldx", "r", "ldr", "nparts", "w", "sg", "M", "C", "HB", "xw", "ldxw", "xn", "ldxn", "xo", "ldxo",
+                 "XQ", "ldq", "XS", "XA", "stream"]
+        for k, v in kw.items():
+            a[names.index(k)] = v
+        return lib.kt_rmsfold_q8(*a)
+    assert call(M=0) == 0                                       # nothing to do: no launch
+    assert call(HB=2048) == INVALID                             # fold sizes 512 / 1024 / 4096 only
+    assert call(HB=4096) == INVALID                             # 5120 % 4096
+    assert call(C=8704, ldx=8704, ldq=8704) == INVALID          # wider than one block's row
+    assert call(nparts=9, r=f, ldr=9 * 5120) == INVALID
+    assert call(nparts=2, r=None) == INVALID
+    assert call(nparts=2, r=f, ldr=5120) == INVALID             # ldr < nparts C
+    assert call(sg=None) == INVALID
+    assert call(w=None) == INVALID
+    assert call(ldq=5000) == INVALID
+    assert lib.kt_fold_q8(f, 4000, f, 1, 4096, 4096, None, 0, f, 4096, f, f, None) == INVALID
+    assert lib.kt_smfold_q8(f, 4096, f, 4096, f, 128, 4, 7, 1, 4096, 4096, None, 0, f, 4096, f, f, None) == INVALID
+    assert lib.kt_smfold_q8(f, 4096, f, 4096, f, 128, 4, 0, 1, 4096, 4096, None, 0, f, 4096, f, f, None) == INVALID

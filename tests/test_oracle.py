@@ -386,3 +386,98 @@ def test_router_softmax_topk(orc):
     t[0, [5, 2, 6]] = 1.0
     ids, gw = orc.router_topk(t, 2)
     assert ids.tolist() == [[2, 5]] and np.allclose(gw, 0.5)
+
+
+# ------------------------------------------------------------------------------------------- fused producers
+def hadamard(n):
+    """Sylvester's Hadamard matrix H[i, j] = (-1)^popcount(i & j) (float64)"""
+    i = np.arange(n)
+    bits = np.bitwise_and.outer(i, i)
+    pc = np.zeros_like(bits)
+    while bits.any():
+        pc += bits & 1
+        bits >>= 1
+    return np.where(pc & 1, -1.0, 1.0)
+
+
+@pytest.mark.parametrize("HB", [512, 1024, 4096])
+def test_fwht_blocks_is_the_normalised_hadamard(orc, HB):
+    """the in-place butterflies give H v / sqrt(HB) per block (natural order), and the transform is its own inverse"""
+    C = 2 * HB
+    v = rng(HB).standard_normal(C).astype(np.float32)
+    out = orc.fwht_blocks(v, HB)
+    H = hadamard(HB)
+    want = np.concatenate([H @ v[b:b + HB].astype(np.float64) for b in range(0, C, HB)]) / np.sqrt(HB)
+    assert np.abs(out - want).max() < 2e-5 * np.abs(want).max()
+    back = orc.fwht_blocks(out, HB)
+    assert np.abs(back - v).max() < 1e-5 * np.abs(v).max()
+    # a unit vector at column HB + 3 becomes the block's row 3 of H (+-1 / sqrt(HB)), the first block stays zero
+    e = np.zeros(C, np.float32)
+    e[HB + 3] = 1.0
+    o = orc.fwht_blocks(e, HB)
+    assert not o[:HB].any()
+    assert np.array_equal(o[HB:], (H[3] * np.float32(1.0 / np.sqrt(HB))).astype(np.float32))
+
+
+def test_sumsq_covers_every_column_exactly(orc):
+    """integer columns: the double sum is exact whatever the order, so it must equal sum e^2 (no dropped index)"""
+    for C in (512, 2048, 5120, 8192):
+        x = np.arange(C, dtype=np.float32)
+        assert orc.sumsq(x) == float(sum(int(e) * int(e) for e in range(C)))
+    x = rng(5).standard_normal(5120).astype(np.float32)
+    import math
+    assert abs(orc.sumsq(x) - math.fsum(float(v) * float(v) for v in x)) < 1e-12 * orc.sumsq(x)
+
+
+def test_rmsfold_closed_forms(orc):
+    """xw = x + parts in part order; xn = x / sqrt(mean x^2 + 1e-6) * w (float64); xo = fold(sg * xn); the int8 row
+    is the pinned quantizer of xo"""
+    M, C, HB, np_ = 3, 5120, 1024, 3
+    r = rng(11)
+    x = r.standard_normal((M, C)).astype(np.float32)
+    parts = (r.standard_normal((M, np_, C)) * 1e3).astype(np.float32)
+    parts[:, 1] = -parts[:, 0] + r.standard_normal((M, C)).astype(np.float32) * 1e-3   # order-revealing
+    w = (1.0 + 0.1 * r.standard_normal(C)).astype(np.float32)
+    sg = np.where(r.random(C) < 0.5, -1.0, 1.0).astype(np.float32)
+    d = orc.rmsfold_q8(x, parts.reshape(M, -1), np_, w, sg, HB)
+    rv = parts[:, 0].copy()
+    for p in range(1, np_):
+        rv = (rv + parts[:, p]).astype(np.float32)
+    xf = (x + rv).astype(np.float32)
+    assert np.array_equal(d["xw"], xf)
+    alt = (x + (parts[:, 0] + (parts[:, 1] + parts[:, 2]).astype(np.float32))).astype(np.float32)
+    assert not np.array_equal(alt, xf)                  # the case does tell the two orders apart
+    x64 = xf.astype(np.float64)
+    want = x64 / np.sqrt((x64 * x64).mean(1, keepdims=True) + 1e-6) * w
+    assert np.abs(d["xn"] - want).max() < 2e-6 * np.abs(want).max()
+    for n in range(M):
+        assert np.array_equal(d["xo"][n], orc.fwht_blocks(sg * d["xn"][n], HB))
+    Q, XS, XA = orc.quant_q8(d["xo"])
+    assert np.array_equal(Q, d["Q"]) and np.array_equal(XS, d["XS"]) and np.array_equal(XA, d["XA"])
+    # without parts: the same row from x alone
+    d0 = orc.rmsfold_q8(xf, None, 0, w, sg, HB)
+    assert np.array_equal(d0["xo"], d["xo"]) and d0["xw"] is None
+
+
+def test_fold_and_smfold_closed_forms(orc):
+    M, C, HB = 2, 4096, 4096
+    r = rng(12)
+    x = r.standard_normal((M, C)).astype(np.float32)
+    sg = np.where(r.random(C) < 0.5, -1.0, 1.0).astype(np.float32)
+    H = hadamard(HB) / np.sqrt(HB)
+    d = orc.fold_q8(x, sg, HB)
+    want = (sg * x).astype(np.float64) @ H.T
+    assert np.abs(d["xo"] - want).max() < 2e-5 * np.abs(want).max()
+    # SiLU(a) * b under the grouped-head order: output (k, rep, h) <- source (rep, k, h)
+    hd, nk, rep = 128, 4, 8
+    a = r.standard_normal((M, C)).astype(np.float32) * 3
+    b = r.standard_normal((M, C)).astype(np.float32)
+    src = np.arange(C).reshape(rep, nk, hd).transpose(1, 0, 2).reshape(-1)
+    assert all(orc.lib().or_perm_src(e, hd, nk, rep) == src[e] for e in range(0, C, 7))
+    d = orc.smfold_q8(a, b, sg, HB, (hd, nk, rep))
+    a64, b64 = a.astype(np.float64)[:, src], b.astype(np.float64)[:, src]
+    m = a64 / (1.0 + np.exp(-a64)) * b64
+    want = (sg * m) @ H.T
+    assert np.abs(d["xo"] - want).max() < 2e-5 * np.abs(want).max()
+    Q, XS, XA = orc.quant_q8(d["xo"])
+    assert np.array_equal(Q, d["Q"]) and np.array_equal(XA, d["XA"])
