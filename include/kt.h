@@ -86,7 +86,10 @@ int kt_tern_sum(const float* P, float* y, int R, int M, int sp, void* stream);
    Stages take C % 128 == 0 and C <= 30720, M 1 .. 4 tokens (the same for every stage).
    kt_plan_run: one plan execution (a small reset kernel, then the plan kernel; graph-capturable). Nothing else
    may run on the GPU at the same time (the plan's blocks wait for each other).
-   kt_plan_status: after the run (synchronizes `stream`): 0, or 1 if a stage barrier timed out (results invalid). */
+   One-token plans run on the streamed executor (exec = 1: every block streams its share of all stages' weights
+   through LDS ahead of the stage it computes); others on the register-ring executor (exec = 0).
+   kt_plan_status: after the run (synchronizes `stream`): 0, or nonzero if a stage barrier timed out (results
+   invalid). */
 typedef struct kt_stage {
   const void* W[3];                   /* up to three kt2 matrices; R[i] <= 0 ends the list */
   int R[3];
@@ -100,6 +103,7 @@ typedef struct kt_stage {
 } kt_stage;
 typedef struct kt_plan_info {
   int nstages, grid, waves, mt;
+  int exec;                           /* 0: register-ring executor; 1: streamed executor (one-token plans) */
   size_t lds;
 } kt_plan_info;
 size_t kt_plan_bytes(int nstages);

@@ -4,6 +4,7 @@
    The declarations and the reference interfaces they replace are in include/kt.h. */
 #include "kt_common.h"
 #include <vector>
+#include <algorithm>
 #include "../../include/kt.h"
 #include "kt_fold.h"
 
@@ -18,6 +19,8 @@ __global__ void k_gemv_mma(const KtGemvArgs, const int8_t*, const float*, int32_
 template <bool GRP, bool DBG>
 __global__ void k_q8_mma(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
 template <int MT> __global__ void k_plan(const uint8_t*, unsigned*);
+size_t kt_splan_lds(int smax, int numax, int tmax);
+const void* kt_splan_kernel();
 extern "C" __global__ void k_plan_reset(unsigned*, int);
 extern "C" __global__ void k_tern_pack(const uint8_t*, const uint16_t*, int, int, uint32_t*, uint16_t*);
 extern "C" __global__ void k_q8_pack(const uint8_t*, int, int, uint32_t*, uint16_t*);
@@ -229,16 +232,21 @@ int kt_plan_build(const kt_stage* st, int n, void* plan, kt_plan_info* info, voi
                                 {(uintptr_t)x.XS, (uintptr_t)x.XS + (size_t)M * NU * 4},
                                 {(uintptr_t)x.XA, (uintptr_t)x.XA + (size_t)M * NU * 4}};
     d.coh = 0;
-    for(int p = 0; p < s && !d.coh; ++p)
+    for(int p = 0; p < s; ++p)
       for(int i = 0; i < 3 && st[p].R[i] > 0; ++i){
         const uintptr_t y0 = (uintptr_t)st[p].Y[i], y1 = y0 + (size_t)M * st[p].R[i] * 4;
-        for(int q = 0; q < 3; ++q) if(in[q][0] < y1 && y0 < in[q][1]) d.coh = 1;
+        for(int q = 0; q < 3; ++q) if(in[q][0] < y1 && y0 < in[q][1]){ d.coh = 1; S[p].pub = 1; }
       }
     if(ks > W) W = ks;
   }
+  int qtot = 0, smax = 0, numax = 0;
   for(int s = 0; s < n; ++s){
     S[s].rgpi = W / S[s].KS;
     S[s].nitems = (S[s].ngroups + S[s].rgpi - 1) / S[s].rgpi;
+    S[s].q0 = qtot;
+    qtot += S[s].ngroups;
+    smax = std::max(smax, kt_steps(S[s].NU));
+    numax = std::max(numax, S[s].NU);
   }
   const int mt = M <= 1 ? 1 : M <= 2 ? 2 : 4;
   const size_t lds = (size_t)W * (mt == 1 ? KtFlat<KT_FMT_TERN, 1>::XW : mt == 2 ? KtFlat<KT_FMT_TERN, 2>::XW
@@ -254,11 +262,24 @@ int kt_plan_build(const kt_stage* st, int n, void* plan, kt_plan_info* info, voi
   }
   if(e != hipSuccess) return (int)e;
   if(nb <= 0 || cus <= 0) return KT_INVALID;
-  H->nstages = n; H->G = nb * cus; H->W = W; H->MT = mt;
+  H->nstages = n; H->G = nb * cus; H->W = W; H->MT = mt; H->exec = 0;
+  /* one token: the streamed executor when its LDS fits (one 8-wave block a CU; at least one block a CU, so a
+     block's tasks (row group, K slice) of a stage are at most tmax) */
+  size_t slds = 0;
+  if(M == 1){
+    int tmax = 0, sb = 0;
+    for(int s = 0; s < n; ++s) tmax = std::max(tmax, ((S[s].ngroups + cus - 1) / cus + 1) * S[s].KS);
+    slds = kt_splan_lds(smax, numax, tmax);
+    if(slds <= 160 * 1024 && hipOccupancyMaxActiveBlocksPerMultiprocessor(&sb, kt_splan_kernel(), 576, slds)
+       == hipSuccess && sb > 0){
+      H->exec = 1; H->G = sb * cus; H->smax = smax; H->numax = numax; H->tmax = tmax; H->qtot = qtot;
+    }
+  }
   e = hipMemcpyAsync(plan, buf.data(), buf.size(), hipMemcpyHostToDevice, kt_stream(stream));
   if(e == hipSuccess) e = hipStreamSynchronize(kt_stream(stream));
   if(e != hipSuccess) return (int)e;
-  info->nstages = n; info->grid = H->G; info->waves = W; info->mt = mt; info->lds = lds;
+  info->nstages = n; info->grid = H->G; info->waves = W; info->mt = mt; info->lds = lds; info->exec = H->exec;
+  if(H->exec == 1){ info->waves = 8; info->lds = slds; }             /* 8 compute waves + a control wave */
   return 0;
 }
 
@@ -267,8 +288,14 @@ int kt_plan_run(const void* plan, const kt_plan_info* info, void* stream){
   hipStream_t s = kt_stream(stream);
   unsigned* ctr = (unsigned*)((uint8_t*)plan + kt_plan_ctr_off(info->nstages));
   hipLaunchKernelGGL(k_plan_reset, dim3(1), dim3(256), 0, s, ctr, (int)KT_BAR_WORDS);
-  const dim3 grid(info->grid), block(64 * (info->waves + 1));
   const uint8_t* p = (const uint8_t*)plan;
+  if(info->exec == 1){
+    hipLaunchKernelGGL((void (*)(const uint8_t*, unsigned*))kt_splan_kernel(), dim3(info->grid), dim3(576), info->lds,
+                       s, p, ctr);
+    KT_LAUNCH_CHECK();
+    return 0;
+  }
+  const dim3 grid(info->grid), block(64 * (info->waves + 1));
   if(info->mt == 1) hipLaunchKernelGGL(k_plan<1>, grid, block, info->lds, s, p, ctr);
   else if(info->mt == 2) hipLaunchKernelGGL(k_plan<2>, grid, block, info->lds, s, p, ctr);
   else hipLaunchKernelGGL(k_plan<4>, grid, block, info->lds, s, p, ctr);

@@ -108,10 +108,13 @@ struct KtPStage {
   int nmat, NU, KS, ngroups;          /* matrices, units along C, K slices, row groups of all matrices */
   int rgpi, nitems;                   /* row groups an item, items */
   int ldq, ldxs, M, coh;              /* coh: the inputs overlap an earlier stage's outputs */
+  int q0, pub, pad3[2];               /* streamed executor: row groups of the stages before this one; a later stage
+                                         reads this one's outputs */
 };
 struct KtPlanHdr {
   int nstages, G, W, MT;              /* stages, blocks, data waves a block, tokens a pass */
-  int pad[12];
+  int exec, smax, numax, tmax;        /* executor (0: k_plan, 1: k_splan); streamed: max steps, units, tasks */
+  int qtot, pad[7];                   /* streamed: row groups of all stages */
 };
 #define KT_PLAN_HDR 64
 __host__ __device__ __forceinline__ size_t kt_plan_ctr_off(int nstages){
@@ -137,3 +140,30 @@ struct KtGroupedArgs {
   int ldq, ldd, ldy, pad2;
   float* y;                           /* output rows [entries][ldy] */
 };
+
+/* the value of lane l ^ X (X = 1 .. 32) on the VALU, without the LDS crossbar: DPP quad permutes and mirrors inside a
+   row of 16 lanes (l ^ 4 = (l ^ 7) ^ 3, l ^ 8 = (l ^ 15) ^ 7), gfx950's permlane swaps across rows and halves. Every
+   DPP source lane is inside the row, so bound_ctrl (zero for an invalid source) never applies; it lets the compiler
+   fold the move into the consuming add / max. */
+template <int X>
+__device__ __forceinline__ int kf_xor(int v){
+  if(X == 1) return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);             /* quad_perm [1,0,3,2] */
+  if(X == 2) return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);             /* quad_perm [2,3,0,1] */
+  if(X == 4) return __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true), 0x1B, 0xF, 0xF,
+                                             true);                                 /* half mirror, [3,2,1,0] */
+  if(X == 8) return __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, true), 0x141, 0xF, 0xF,
+                                             true);                                 /* mirror, half mirror */
+  const int l = __lane_id();
+  if(X == 16){
+    const auto s = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (l & 16) ? (int)s[0] : (int)s[1];
+  }
+  const auto s = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (l & 32) ? (int)s[0] : (int)s[1];
+}
+template <int X> __device__ __forceinline__ float kf_xorf(float v){ return __int_as_float(kf_xor<X>(__float_as_int(v))); }
+template <int X> __device__ __forceinline__ double kf_xord(double v){
+  const long long b = __double_as_longlong(v);
+  const int lo = kf_xor<X>((int)b), hi = kf_xor<X>((int)(b >> 32));
+  return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}

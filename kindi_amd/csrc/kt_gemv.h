@@ -13,11 +13,12 @@
 #pragma once
 #include "kt_common.h"
 
-/* the fixed xor butterfly over the 8 k-lanes of a row (lane bits 3..5): every lane ends with the same value */
+/* the fixed xor butterfly over the 8 k-lanes of a row (lane bits 3..5): every lane ends with the same value (each
+   adds the same pair); the exchanges run on the VALU (kf_xor) */
 __device__ __forceinline__ float kt_row_sum(float v){
-  v += __shfl_xor(v, 8);
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
+  v += kf_xorf<8>(v);
+  v += kf_xorf<16>(v);
+  v += kf_xorf<32>(v);
   return v;
 }
 

@@ -23,7 +23,7 @@ class KtStage(ctypes.Structure):
 
 class KtPlanInfo(ctypes.Structure):
     """kt_plan_info (include/kt.h): the launch shape kt_plan_build chose"""
-    _fields_ = [("nstages", I), ("grid", I), ("waves", I), ("mt", I), ("lds", S)]
+    _fields_ = [("nstages", I), ("grid", I), ("waves", I), ("mt", I), ("exec", I), ("lds", S)]
 
 
 # (name, restype, argtypes): the declarations of include/kt.h

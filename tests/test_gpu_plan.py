@@ -71,7 +71,7 @@ def test_plan_matches_launches_27b_layer(linear, synth):
     shapes = synth.CFG["c3"]["mats"]
     stages, ref = _layer_stages(linear, synth, shapes, 1, 1, 700)
     plan = linear.Plan(stages)
-    say("plan 27B layer: grid %d, %d data waves" % (plan.info.grid, plan.info.waves))
+    say("plan 27B layer: grid %d, %d data waves, executor %d" % (plan.info.grid, plan.info.waves, plan.info.exec))
     plan.run()
     torch.cuda.synchronize()
     assert plan.status() == 0
