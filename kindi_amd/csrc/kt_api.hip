@@ -36,6 +36,7 @@ __global__ void k_tern_gemm_rs1(const uint32_t*, const uint16_t*, int, int, cons
 extern "C" __global__ void k_moe_topk(const float*, int, int, int*, float*);
 extern "C" __global__ void k_moe_sort(const int*, int, int, int*, int*, int*, int*, int*, int*, int);
 extern "C" __global__ void k_moe_combine(const float*, const float*, const int*, const float*, int, int, float*);
+extern "C" __global__ void k_moe_route(const float*, int, int, int, int*, float*, int*, int*, int*, int*, int*, int*);
 
 #define KT_INVALID ((int)hipErrorInvalidValue)
 #define KT_RS_ROWS 8192                /* per-row prefill order below this many rows (include/kt.h) */
@@ -410,6 +411,16 @@ int kt_moe_topk(const float* logits, int M, int E, int k, int* ids, float* gw, v
   return 0;
 }
 
+int kt_moe_route(const float* logits, int M, int E, int k, int* ids, float* gw, int* cnt, int* off, int* xrow,
+                 int* where, int* act, int* nact, void* stream){
+  if(!logits || !ids || !gw || !cnt || !off || !xrow || !where || !act || !nact || M < 0 || E <= 0 || E > 1024 ||
+     k <= 0 || k > 16 || k > E) return KT_INVALID;
+  hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(1024), 0, kt_stream(stream), logits, M, E, k, ids, gw, cnt, off, xrow,
+                     where, act, nact);
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
 int kt_moe_sort(const int* ids, int M, int k, int E, int* cnt, int* off, int* xrow, int* where, int* act, int* nact,
                 void* stream){
   if(!ids || !cnt || !off || !xrow || !where || !act || !nact || M < 0 || k <= 0 || E <= 0 || E > 1024) return KT_INVALID;
@@ -467,8 +478,9 @@ int kt_q8_grouped(const void* const* Wexp, int R, int C, int E, const int* cnt, 
 int kt_moe_combine(const float* yd, const float* ysh, const int* where, const float* gw, int M, int k, int cols,
                    float* x, void* stream){
   if(M == 0) return 0;
-  if(!yd || !where || !gw || !x || M < 0 || k <= 0 || cols <= 0) return KT_INVALID;
-  hipLaunchKernelGGL(k_moe_combine, dim3(M), dim3(256), 0, kt_stream(stream), yd, ysh, where, gw, k, cols, x);
+  if(!yd || !where || !gw || !x || M < 0 || M > 65535 || k <= 0 || k > 16 || cols <= 0) return KT_INVALID;
+  hipLaunchKernelGGL(k_moe_combine, dim3((cols + 255) / 256, M), dim3(256), 0, kt_stream(stream), yd, ysh, where, gw,
+                     k, cols, x);
   KT_LAUNCH_CHECK();
   return 0;
 }

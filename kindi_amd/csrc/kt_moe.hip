@@ -9,41 +9,58 @@
                     (stable), so the lists are deterministic.
    (the grouped product itself, per active expert and its token list, is the decode product k_gemv_flat in its
    grouped mode, kt_gemv.h: the dense q8_0 product's lanes, arithmetic and summation tree; output row = entry)
+     k_moe_route    k_moe_topk and k_moe_sort in one launch, for few tokens.
      k_moe_combine  x[t] += sum_j fmaf(gw[t k + j], yd[where[t k + j]], .) (+ ysh[t]).
 */
 #include "kt_common.h"
 
 
-extern "C" __global__ void __launch_bounds__(64) k_moe_topk(const float* __restrict__ logits, int E, int k,
-                                                            int* __restrict__ ids, float* __restrict__ gw){
-  /* one wave per token; E <= 1024, k <= 16 */
-  const int t = blockIdx.x, lane = threadIdx.x;
-  const float* l = logits + (long long)t * E;
-  __shared__ int sel[16];
-  __shared__ float lv[16];
-  for(int j = 0; j < k; ++j){
-    float bv = -INFINITY;
-    int bi = 0x7FFFFFFF;
-    for(int e = lane; e < E; e += 64){
-      bool used = false;
-      for(int i = 0; i < j; ++i) used |= sel[i] == e;
-      const float v = l[e];
-      if(!used && (v > bv || (v == bv && e < bi))){ bv = v; bi = e; }
-    }
+/* the k largest of E <= 1024 logits by one wave, the logits in registers (lane l holds e = l + 64 i): k rounds of a
+   wave arg-max (ties to the lower index, a chosen entry masked out) on the VALU exchanges; lane 0 writes ids and the
+   weights exp(l_j - l_max) / sum of the chosen */
+__device__ __forceinline__ void kt_topk_wave(const float* __restrict__ l, int E, int k, int* __restrict__ ids,
+                                             float* __restrict__ gw, int lane){
+  float v[16];
 #pragma unroll
-    for(int o = 32; o > 0; o >>= 1){
-      const float ov = __shfl_xor(bv, o);
-      const int oi = __shfl_xor(bi, o);
-      if(ov > bv || (ov == bv && oi < bi)){ bv = ov; bi = oi; }
+  for(int i = 0; i < 16; ++i){ const int e = lane + 64 * i; v[i] = e < E ? l[e] : -INFINITY; }
+  unsigned used = 0u;
+  int sel[16];
+  float lv[16];
+#pragma unroll
+  for(int j = 0; j < 16; ++j){
+    sel[j] = 0; lv[j] = 0.0f;
+    if(j < k){
+      float bv = -INFINITY;
+      int bi = 0x7FFFFFFF;
+#pragma unroll
+      for(int i = 0; i < 16; ++i){
+        const int e = lane + 64 * i;
+        if(e < E && !(used >> i & 1u) && (v[i] > bv || (v[i] == bv && e < bi))){ bv = v[i]; bi = e; }
+      }
+#define KT_TOPK_STEP(X) { const float ov = kf_xorf<X>(bv); const int oi = kf_xor<X>(bi); \
+      if(ov > bv || (ov == bv && oi < bi)){ bv = ov; bi = oi; } }
+      KT_TOPK_STEP(1) KT_TOPK_STEP(2) KT_TOPK_STEP(4) KT_TOPK_STEP(8) KT_TOPK_STEP(16) KT_TOPK_STEP(32)
+#undef KT_TOPK_STEP
+      bi = __builtin_amdgcn_readfirstlane(bi);
+      bv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(bv)));
+      if((bi & 63) == lane) used |= 1u << (bi >> 6);
+      sel[j] = bi; lv[j] = bv;
     }
-    if(lane == 0){ sel[j] = bi; lv[j] = bv; }
-    __syncthreads();
   }
   if(lane == 0){
     float p[16], s = 0.0f;
-    for(int j = 0; j < k; ++j){ p[j] = expf(lv[j] - lv[0]); s += p[j]; }
-    for(int j = 0; j < k; ++j){ ids[t * k + j] = sel[j]; gw[t * k + j] = p[j] / s; }
+#pragma unroll
+    for(int j = 0; j < 16; ++j) if(j < k){ p[j] = expf(lv[j] - lv[0]); s += p[j]; }
+#pragma unroll
+    for(int j = 0; j < 16; ++j) if(j < k){ ids[j] = sel[j]; gw[j] = p[j] / s; }
   }
+}
+
+extern "C" __global__ void __launch_bounds__(64) k_moe_topk(const float* __restrict__ logits, int E, int k,
+                                                            int* __restrict__ ids, float* __restrict__ gw){
+  /* one wave per token; E <= 1024, k <= 16 */
+  const int t = blockIdx.x;
+  kt_topk_wave(logits + (long long)t * E, E, k, ids + t * k, gw + t * k, threadIdx.x);
 }
 
 /* an exclusive scan of v over the block's 1024 threads (in-wave shuffle scan, then the 16 wave totals) */
@@ -63,9 +80,9 @@ __device__ __forceinline__ int kt_block_excl_scan(int v, int* wsum){
   return pre + x - v;
 }
 
-extern "C" __global__ void __launch_bounds__(1024) k_moe_sort(const int* __restrict__ ids, int n, int E,
-    int* __restrict__ cnt, int* __restrict__ off, int* __restrict__ xrow, int* __restrict__ where,
-    int* __restrict__ act, int* __restrict__ nact, int k){
+__device__ __forceinline__ void kt_moe_lists(const int* __restrict__ ids, int n, int E, int* __restrict__ cnt,
+    int* __restrict__ off, int* __restrict__ xrow, int* __restrict__ where, int* __restrict__ act,
+    int* __restrict__ nact, int k){
   /* one block of 1024 threads; n = M k entries, E <= 1024. Counting with LDS atomics (order-free); offsets and the
      active list by block scans; placement by one wave per expert (experts w, w + 16, ...): over the entries in
      order, 64 at a time, a ballot of the matches gives each its rank, so an expert's entries keep ascending flat
@@ -110,15 +127,34 @@ extern "C" __global__ void __launch_bounds__(1024) k_moe_sort(const int* __restr
   }
 }
 
+extern "C" __global__ void __launch_bounds__(1024) k_moe_sort(const int* __restrict__ ids, int n, int E,
+    int* __restrict__ cnt, int* __restrict__ off, int* __restrict__ xrow, int* __restrict__ where,
+    int* __restrict__ act, int* __restrict__ nact, int k){
+  kt_moe_lists(ids, n, E, cnt, off, xrow, where, act, nact, k);
+}
+
+/* the router and the lists in one launch (few tokens): the 16 waves take the tokens' top-k (token w, w + 16, ...),
+   then the block sorts them (its own writes of ids, visible after the block barrier) */
+extern "C" __global__ void __launch_bounds__(1024) k_moe_route(const float* __restrict__ logits, int M, int E, int k,
+    int* __restrict__ ids, float* __restrict__ gw, int* __restrict__ cnt, int* __restrict__ off,
+    int* __restrict__ xrow, int* __restrict__ where, int* __restrict__ act, int* __restrict__ nact){
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for(int t = w; t < M; t += 16)
+    kt_topk_wave(logits + (long long)t * E, E, k, ids + t * k, gw + t * k, lane);
+  __syncthreads();
+  kt_moe_lists(ids, M * k, E, cnt, off, xrow, where, act, nact, k);
+}
+
 extern "C" __global__ void __launch_bounds__(256) k_moe_combine(const float* __restrict__ yd, const float* __restrict__ ysh,
     const int* __restrict__ where, const float* __restrict__ gw, int k, int cols, float* __restrict__ x){
-  /* one block per token; its k (entry, weight) pairs read once */
+  /* grid (column blocks of 256, tokens): one column of one token a thread, so its k loads are in flight together;
+     the pairs of the token read once a block */
   __shared__ int wp[16];
   __shared__ float gp[16];
-  const int t = blockIdx.x;
+  const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
   if(threadIdx.x < k){ wp[threadIdx.x] = where[t * k + threadIdx.x]; gp[threadIdx.x] = gw[t * k + threadIdx.x]; }
   __syncthreads();
-  for(int i = threadIdx.x; i < cols; i += blockDim.x){
+  if(i < cols){
     float s = 0.0f;
     for(int j = 0; j < k; ++j) s = fmaf(gp[j], yd[(long long)wp[j] * cols + i], s);
     x[(long long)t * cols + i] += ysh ? s + ysh[(long long)t * cols + i] : s;

@@ -100,6 +100,25 @@ class MoE(object):
         gpudrv.check(gpudrv.load().kt_moe_topk(ptr(logits), M, E, self.k, ptr(ids), ptr(gw), stream()), "kt_moe_topk")
         return ids, gw
 
+    route_max = 16                    # up to this many tokens, router and lists in one launch (kt_moe_route)
+
+    def route_lists(self, logits):
+        """route + lists in one launch: the same ids, weights and lists"""
+        M, E = logits.shape
+        dev = logits.device
+        ids = torch.empty((M, self.k), dtype=torch.int32, device=dev)
+        gw = torch.empty((M, self.k), dtype=torch.float32, device=dev)
+        cnt = torch.empty(self.E, dtype=torch.int32, device=dev)
+        off = torch.empty(self.E, dtype=torch.int32, device=dev)
+        xrow = torch.empty(M * self.k, dtype=torch.int32, device=dev)
+        where = torch.empty(M * self.k, dtype=torch.int32, device=dev)
+        act = torch.empty(self.E, dtype=torch.int32, device=dev)
+        nact = torch.empty(1, dtype=torch.int32, device=dev)
+        rc = gpudrv.load().kt_moe_route(ptr(logits), M, E, self.k, ptr(ids), ptr(gw), ptr(cnt), ptr(off), ptr(xrow),
+                                        ptr(where), ptr(act), ptr(nact), stream())
+        gpudrv.check(rc, "kt_moe_route")
+        return ids, gw, (cnt, off, xrow, where, act, nact)
+
     def lists(self, ids):
         M, k = ids.shape
         dev = ids.device
@@ -126,8 +145,11 @@ class MoE(object):
         F = self.up.R
         b = bufs or self.buffers(M)
         Q, D = q8_quantize(x, 0, b["xq"], b["xd"])
-        ids, gw = self.route(logits)
-        lists = self.lists(ids)
+        if M <= self.route_max:
+            ids, gw, lists = self.route_lists(logits)
+        else:
+            ids, gw = self.route(logits)
+            lists = self.lists(ids)
         self.up.grouped(lists, M, Q, D, b["u"], xrow=True)
         q8_quantize(b["u"], 1, b["uq"], b["ud"])
         self.down.grouped(lists, M, b["uq"], b["ud"], b["yd"], xrow=False)

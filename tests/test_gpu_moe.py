@@ -75,6 +75,31 @@ def test_topk_and_sort(kt):
         assert np.array_equal(got[2], xrow) and np.array_equal(got[3], where)
         active = np.nonzero(cnt)[0]
         assert got[5][0] == len(active) and np.array_equal(got[4][:len(active)], active)
+        if M <= 64:                                                 # the one-launch router + lists
+            ids2, gw2, lists2 = layer.route_lists(dev(lg))
+            assert np.array_equal(host(ids2), rid) and np.array_equal(host(gw2), host(gw)), M
+            for a_, b_ in zip(lists2[:4], lists[:4]):
+                assert np.array_equal(host(a_), host(b_)), M
+            n2 = int(host(lists2[5])[0])                           # act: only its first nact entries are defined
+            assert n2 == len(active) and np.array_equal(host(lists2[4])[:n2], active), M
+
+
+def test_topk_wide(kt):
+    """E = 1000 logits (16 a lane), k = 16, with ties and -inf entries"""
+    lib, moe = kt
+    say("topk wide")
+    E, k, M = 1000, 16, 5
+    lg = rng(9).normal(0, 1, (M, E)).astype(np.float32)
+    lg[1, 500:520] = 3.0
+    lg[2, :] = -np.inf
+    lg[2, [7, 900]] = 1.0
+    ids = torch.empty((M, k), dtype=torch.int32, device="cuda")
+    gw = torch.empty((M, k), dtype=torch.float32, device="cuda")
+    from kindi_amd.linear import ptr, stream
+    assert lib.kt_moe_topk(ptr(dev(lg)), M, E, k, ptr(ids), ptr(gw), stream()) == 0
+    rid, rgw = orc.router_topk(lg, k)
+    assert np.array_equal(host(ids), rid)
+    assert np.allclose(host(gw), rgw, rtol=2e-6, atol=1e-7, equal_nan=True)
 
 
 def oracle_moe(x, lg, up_rows, down_rows, H, F, k):
