@@ -151,10 +151,12 @@ int kt_q8_gemv(const void* W, int R, int C, const int8_t* Q, int ldq, const floa
 int kt_moe_topk(const float* logits, int M, int E, int k, int* ids, float* gw, void* stream);
 int kt_moe_sort(const int* ids, int M, int k, int E, int* cnt, int* off, int* xrow, int* where, int* act, int* nact,
                 void* stream);
-/* kt_moe_route: kt_moe_topk and kt_moe_sort in one launch (one block: suited to few tokens; the same outputs) — the
-   router and list building around lt_router_topk (lightning.cu:414-468) and lt_moe_lists (lightning.cu:1318-1349). */
+/* kt_moe_route: kt_moe_topk and kt_moe_sort in one launch (one wave; M k <= 64 entries; the same outputs) — the
+   router and list building around lt_router_topk (lightning.cu:414-468) and lt_moe_lists (lightning.cu:1318-1349);
+   with x non-NULL, the same launch also writes kt_q8_quant(x, act = 0) into Q / D (H % 32 == 0). */
 int kt_moe_route(const float* logits, int M, int E, int k, int* ids, float* gw, int* cnt, int* off, int* xrow,
-                 int* where, int* act, int* nact, void* stream);
+                 int* where, int* act, int* nact, const float* x, int ldx, int H, int8_t* Q, int ldq, float* D, int ldd,
+                 void* stream);
 int kt_q8_grouped(const void* const* Wexp, int R, int C, int E, const int* cnt, const int* off, const int* act,
                   const int* nact, const int* xrow, int nentries, int M, const int8_t* Q, int ldq, const float* D,
                   int ldd, float* Y, int ldy, int32_t* dbg, void* stream);

@@ -36,7 +36,8 @@ __global__ void k_tern_gemm_rs1(const uint32_t*, const uint16_t*, int, int, cons
 extern "C" __global__ void k_moe_topk(const float*, int, int, int*, float*);
 extern "C" __global__ void k_moe_sort(const int*, int, int, int*, int*, int*, int*, int*, int*, int);
 extern "C" __global__ void k_moe_combine(const float*, const float*, const int*, const float*, int, int, float*);
-extern "C" __global__ void k_moe_route(const float*, int, int, int, int*, float*, int*, int*, int*, int*, int*, int*);
+extern "C" __global__ void k_moe_route(const float*, int, int, int, int*, float*, int*, int*, int*, int*, int*, int*,
+                                       const float*, int, int, int8_t*, int, float*, int);
 
 #define KT_INVALID ((int)hipErrorInvalidValue)
 #define KT_RS_ROWS 8192                /* per-row prefill order below this many rows (include/kt.h) */
@@ -412,11 +413,13 @@ int kt_moe_topk(const float* logits, int M, int E, int k, int* ids, float* gw, v
 }
 
 int kt_moe_route(const float* logits, int M, int E, int k, int* ids, float* gw, int* cnt, int* off, int* xrow,
-                 int* where, int* act, int* nact, void* stream){
+                 int* where, int* act, int* nact, const float* x, int ldx, int H, int8_t* Q, int ldq, float* D, int ldd,
+                 void* stream){
   if(!logits || !ids || !gw || !cnt || !off || !xrow || !where || !act || !nact || M < 0 || E <= 0 || E > 1024 ||
-     k <= 0 || k > 16 || k > E) return KT_INVALID;
-  hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(1024), 0, kt_stream(stream), logits, M, E, k, ids, gw, cnt, off, xrow,
-                     where, act, nact);
+     k <= 0 || k > 16 || k > E || M * k > 64) return KT_INVALID;
+  if(x && (H <= 0 || H % 32 || ldx < H || !Q || ldq < H || !D || ldd < H / 32)) return KT_INVALID;
+  hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(256), 0, kt_stream(stream), logits, M, E, k, ids, gw, cnt, off, xrow,
+                     where, act, nact, x, ldx, H, Q, ldq, D, ldd);
   KT_LAUNCH_CHECK();
   return 0;
 }

@@ -9,7 +9,7 @@
                     (stable), so the lists are deterministic.
    (the grouped product itself, per active expert and its token list, is the decode product k_gemv_flat in its
    grouped mode, kt_gemv.h: the dense q8_0 product's lanes, arithmetic and summation tree; output row = entry)
-     k_moe_route    k_moe_topk and k_moe_sort in one launch, for few tokens.
+     k_moe_route    k_moe_topk and k_moe_sort in one launch by one wave, for up to 64 entries.
      k_moe_combine  x[t] += sum_j fmaf(gw[t k + j], yd[where[t k + j]], .) (+ ysh[t]).
 */
 #include "kt_common.h"
@@ -19,12 +19,11 @@
    wave arg-max (ties to the lower index, a chosen entry masked out) on the VALU exchanges; lane 0 writes ids and the
    weights exp(l_j - l_max) / sum of the chosen */
 __device__ __forceinline__ void kt_topk_wave(const float* __restrict__ l, int E, int k, int* __restrict__ ids,
-                                             float* __restrict__ gw, int lane){
+                                             float* __restrict__ gw, int lane, int (&sel)[16]){
   float v[16];
 #pragma unroll
   for(int i = 0; i < 16; ++i){ const int e = lane + 64 * i; v[i] = e < E ? l[e] : -INFINITY; }
   unsigned used = 0u;
-  int sel[16];
   float lv[16];
 #pragma unroll
   for(int j = 0; j < 16; ++j){
@@ -60,7 +59,8 @@ extern "C" __global__ void __launch_bounds__(64) k_moe_topk(const float* __restr
                                                             int* __restrict__ ids, float* __restrict__ gw){
   /* one wave per token; E <= 1024, k <= 16 */
   const int t = blockIdx.x;
-  kt_topk_wave(logits + (long long)t * E, E, k, ids + t * k, gw + t * k, threadIdx.x);
+  int sel[16];
+  kt_topk_wave(logits + (long long)t * E, E, k, ids + t * k, gw + t * k, threadIdx.x, sel);
 }
 
 /* an exclusive scan of v over the block's 1024 threads (in-wave shuffle scan, then the 16 wave totals) */
@@ -133,16 +133,80 @@ extern "C" __global__ void __launch_bounds__(1024) k_moe_sort(const int* __restr
   kt_moe_lists(ids, n, E, cnt, off, xrow, where, act, nact, k);
 }
 
-/* the router and the lists in one launch (few tokens): the 16 waves take the tokens' top-k (token w, w + 16, ...),
-   then the block sorts them (its own writes of ids, visible after the block barrier) */
-extern "C" __global__ void __launch_bounds__(1024) k_moe_route(const float* __restrict__ logits, int M, int E, int k,
+/* the router and the lists in one launch, by one wave (n = M k <= 64 entries, E <= 1024): the top-k of each token
+   leaves entry p's expert in lane p; lane l owns experts 16 l .. 16 l + 15 (counts from the n entries, read with
+   readlane); offsets and the active list by prefix sums over lanes; an entry's place is its expert's offset plus the
+   entries before it with the same expert (ascending flat index, as kt_moe_sort). The same outputs as
+   k_moe_topk + k_moe_sort. */
+extern "C" __global__ void __launch_bounds__(256) k_moe_route(const float* __restrict__ logits, int M, int E, int k,
     int* __restrict__ ids, float* __restrict__ gw, int* __restrict__ cnt, int* __restrict__ off,
-    int* __restrict__ xrow, int* __restrict__ where, int* __restrict__ act, int* __restrict__ nact){
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  for(int t = w; t < M; t += 16)
-    kt_topk_wave(logits + (long long)t * E, E, k, ids + t * k, gw + t * k, lane);
-  __syncthreads();
-  kt_moe_lists(ids, M * k, E, cnt, off, xrow, where, act, nact, k);
+    int* __restrict__ xrow, int* __restrict__ where, int* __restrict__ act, int* __restrict__ nact,
+    const float* __restrict__ x, int ldx, int H, int8_t* __restrict__ Q, int ldq, float* __restrict__ D, int ldd){
+  __shared__ int o[1024];
+  const int lane = threadIdx.x & 63, n = M * k;
+  if(threadIdx.x >= 64){
+    /* waves 1..3: the tokens' int8 rows, k_quant_q8's numbers (act 0): a 32-lane half per 32-column block */
+    if(!x) return;
+    const int h = (threadIdx.x - 64) >> 5, l = threadIdx.x & 31, nb = H / 32;
+    for(int t = 0; t < M; ++t)
+      for(int b = h; b < nb; b += 6){
+        const float v = x[(long long)t * ldx + b * 32 + l];
+        float a = fabsf(v);
+        a = fmaxf(a, kf_xorf<1>(a)); a = fmaxf(a, kf_xorf<2>(a)); a = fmaxf(a, kf_xorf<4>(a));
+        a = fmaxf(a, kf_xorf<8>(a)); a = fmaxf(a, kf_xorf<16>(a));
+        const float id = a != 0.0f ? 127.0f / a : 0.0f;
+        Q[(long long)t * ldq + b * 32 + l] = (int8_t)__float2int_rn(v * id);
+        if(l == 0) D[(long long)t * ldd + b] = __half2float(__float2half_rn(a / 127.0f));
+      }
+    return;
+  }
+  int ep = -1;                                                     /* entry lane's expert */
+  for(int t = 0; t < M; ++t){
+    int sel[16];
+    kt_topk_wave(logits + (long long)t * E, E, k, ids + t * k, gw + t * k, lane, sel);
+#pragma unroll
+    for(int j = 0; j < 16; ++j) if(j < k && lane == t * k + j) ep = sel[j];
+  }
+  int c[16];
+#pragma unroll
+  for(int i = 0; i < 16; ++i) c[i] = 0;
+  for(int q = 0; q < n; ++q){
+    const int d = __builtin_amdgcn_readlane(ep, q) - 16 * lane;
+#pragma unroll
+    for(int i = 0; i < 16; ++i) c[i] += d == i ? 1 : 0;
+  }
+  int tot = 0, na = 0;
+#pragma unroll
+  for(int i = 0; i < 16; ++i){ tot += c[i]; na += c[i] > 0 ? 1 : 0; }
+  int base = 0, abase = 0, all = 0;
+  for(int l = 0; l < 64; ++l){
+    const int tl = __builtin_amdgcn_readlane(tot, l), al = __builtin_amdgcn_readlane(na, l);
+    base += l < lane ? tl : 0;
+    abase += l < lane ? al : 0;
+    all += al;
+  }
+#pragma unroll
+  for(int i = 0; i < 16; ++i){
+    const int e = 16 * lane + i;
+    if(e < E){
+      cnt[e] = c[i];
+      off[e] = base;
+      o[e] = base;
+      if(c[i] > 0) act[abase++] = e;
+    }
+    base += c[i];
+  }
+  if(lane == 0) *nact = all;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");        /* o[] by this wave only: a wave barrier suffices */
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  if(lane < n){
+    int rank = 0;
+    for(int q = 0; q < n; ++q) rank += (q < lane && __builtin_amdgcn_readlane(ep, q) == ep) ? 1 : 0;
+    const int pos = o[ep] + rank;
+    xrow[pos] = lane / k;
+    where[lane] = pos;
+  }
 }
 
 extern "C" __global__ void __launch_bounds__(256) k_moe_combine(const float* __restrict__ yd, const float* __restrict__ ysh,

@@ -51,7 +51,7 @@ SIGNATURES = [
     ("kt_moe_sort", I, [P, I, I, I, P, P, P, P, P, P, P]),
     ("kt_q8_grouped", I, [P, I, I, I, P, P, P, P, P, I, I, P, I, P, I, P, I, P, P]),
     ("kt_moe_combine", I, [P, P, P, P, I, I, I, P, P]),
-    ("kt_moe_route", I, [P, I, I, I, P, P, P, P, P, P, P, P, P]),
+    ("kt_moe_route", I, [P, I, I, I, P, P, P, P, P, P, P, P, P, I, I, P, I, P, I, P]),
     ("kt_rmsfold_q8", I, [P, I, P, I, I, P, P, I, I, I, P, I, P, I, P, I, P, I, P, P, P]),
     ("kt_fold_q8", I, [P, I, P, I, I, I, P, I, P, I, P, P, P]),
     ("kt_smfold_q8", I, [P, I, P, I, P, I, I, I, I, I, I, P, I, P, I, P, P, P]),

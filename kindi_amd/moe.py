@@ -100,10 +100,9 @@ class MoE(object):
         gpudrv.check(gpudrv.load().kt_moe_topk(ptr(logits), M, E, self.k, ptr(ids), ptr(gw), stream()), "kt_moe_topk")
         return ids, gw
 
-    route_max = 16                    # up to this many tokens, router and lists in one launch (kt_moe_route)
-
-    def route_lists(self, logits):
-        """route + lists in one launch: the same ids, weights and lists"""
+    def route_lists(self, logits, x=None, Q=None, D=None):
+        """route + lists in one launch: the same ids, weights and lists (and, with x, its int8 rows into Q, D as
+        q8_quantize(x) writes them)"""
         M, E = logits.shape
         dev = logits.device
         ids = torch.empty((M, self.k), dtype=torch.int32, device=dev)
@@ -114,8 +113,11 @@ class MoE(object):
         where = torch.empty(M * self.k, dtype=torch.int32, device=dev)
         act = torch.empty(self.E, dtype=torch.int32, device=dev)
         nact = torch.empty(1, dtype=torch.int32, device=dev)
+        H = x.shape[1] if x is not None else 0
         rc = gpudrv.load().kt_moe_route(ptr(logits), M, E, self.k, ptr(ids), ptr(gw), ptr(cnt), ptr(off), ptr(xrow),
-                                        ptr(where), ptr(act), ptr(nact), stream())
+                                        ptr(where), ptr(act), ptr(nact), ptr(x), x.stride(0) if x is not None else 0,
+                                        H, ptr(Q), Q.stride(0) if Q is not None else 0, ptr(D),
+                                        D.stride(0) if D is not None else 0, stream())
         gpudrv.check(rc, "kt_moe_route")
         return ids, gw, (cnt, off, xrow, where, act, nact)
 
@@ -144,10 +146,11 @@ class MoE(object):
         M, H = x.shape
         F = self.up.R
         b = bufs or self.buffers(M)
-        Q, D = q8_quantize(x, 0, b["xq"], b["xd"])
-        if M <= self.route_max:
-            ids, gw, lists = self.route_lists(logits)
+        if M * self.k <= 64:                     # quantize, route and sort in one launch
+            Q, D = b["xq"], b["xd"]
+            ids, gw, lists = self.route_lists(logits, x, Q, D)
         else:
+            Q, D = q8_quantize(x, 0, b["xq"], b["xd"])
             ids, gw = self.route(logits)
             lists = self.lists(ids)
         self.up.grouped(lists, M, Q, D, b["u"], xrow=True)

@@ -60,7 +60,7 @@ def test_topk_and_sort(kt):
     ups = moe.Q8Experts([q8_case(64, 32, e)[0] for e in range(E)], 64, 32)
     downs = moe.Q8Experts([q8_case(32, 64, 500 + e)[0] for e in range(E)], 32, 64)
     layer = moe.MoE(ups, downs, k)
-    for M in (1, 2, 37, 256, 700):
+    for M in (1, 2, 10, 37, 256, 700):
         lg = rng(M).normal(0, 1, (M, E)).astype(np.float32)
         if M == 37:
             lg[3, [10, 11, 12, 13, 14, 15, 16]] = 5.0                # a tie across the k-th place
@@ -75,8 +75,14 @@ def test_topk_and_sort(kt):
         assert np.array_equal(got[2], xrow) and np.array_equal(got[3], where)
         active = np.nonzero(cnt)[0]
         assert got[5][0] == len(active) and np.array_equal(got[4][:len(active)], active)
-        if M <= 64:                                                 # the one-launch router + lists
-            ids2, gw2, lists2 = layer.route_lists(dev(lg))
+        if M * k <= 64:                                             # the one-launch router + lists
+            xr = rng(M + 5).normal(0, 1, (M, 96)).astype(np.float32)
+            xr[0, 32:64] = 0.0                                      # a zero block
+            Qr = torch.empty((M, 96), dtype=torch.int8, device="cuda")
+            Dr = torch.empty((M, 3), dtype=torch.float32, device="cuda")
+            ids2, gw2, lists2 = layer.route_lists(dev(lg), dev(xr), Qr, Dr)
+            Q1, D1 = moe.q8_quantize(dev(xr))
+            assert np.array_equal(host(Qr), host(Q1)) and np.array_equal(host(Dr), host(D1)), M
             assert np.array_equal(host(ids2), rid) and np.array_equal(host(gw2), host(gw)), M
             for a_, b_ in zip(lists2[:4], lists[:4]):
                 assert np.array_equal(host(a_), host(b_)), M
