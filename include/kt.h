@@ -43,6 +43,12 @@ const char* kt_error_string(int rc);
    Replaces layout.repack (layout.py:32-48) and spec.repack / k_tc_pack (spec.py:327-383, tc_hip.cu:31-40). */
 size_t kt_tern_weight_bytes(int R, int C);
 int kt_tern_pack(const uint8_t* bcodes, const uint16_t* dpm, int R, int C, void* W, void* stream);
+/* kt_tern_pack_ptq1: the GGUF tensor itself (type PTQ1_0: per row C / 128 blocks of 28 bytes, qs[24] | qh[2] | fp16
+   d, 5 digits a byte; convert.py:33-46 trits_from_raw) -> W, for rows row0 .. row0 + nrows - 1 (row0 % 8 == 0;
+   nrows % 8 == 0 unless the range ends at R; raw points at row row0's first block), so a tensor can be streamed
+   from a file in row chunks. The same W as kt_tern_pack of convert.py's pack of the tensor. Replaces the offline
+   convert + repack path (convert.py:144-159, layout.py:32-48, spec.repack spec.py:327-383). */
+int kt_tern_pack_ptq1(const uint8_t* raw, int R, int C, int row0, int nrows, void* W, void* stream);
 
 /* ---------------------------------------------------------------- activations
    X fp32 [M][ldx] -> XQ int8 [M][ldq] (natural column order, ldq % 16 == 0), XS f32 / XA i32 [M][C/128].

@@ -24,6 +24,7 @@ const void* kt_splan_kernel();
 extern "C" __global__ void k_plan_reset(unsigned*, int);
 extern "C" __global__ void k_tern_pack(const uint8_t*, const uint16_t*, int, int, uint32_t*, uint16_t*);
 extern "C" __global__ void k_q8_pack(const uint8_t*, int, int, uint32_t*, uint16_t*);
+extern "C" __global__ void k_tern_pack_ptq1(const uint8_t*, int, int, int, int, uint32_t*, uint16_t*);
 extern "C" __global__ void k_quant_tern(const float*, int, int, int, int8_t*, int, float*, int*);
 extern "C" __global__ void k_quant_q8(const float*, int, int, int, int8_t*, int, float*, int);
 extern "C" __global__ void k_tern_sum(const float*, float*, int, int, int);
@@ -149,6 +150,20 @@ int kt_tern_pack(const uint8_t* bcodes, const uint16_t* dpm, int R, int C, void*
   const long long nw = (long long)kt_code_bytes(R, NG) / 4;
   hipLaunchKernelGGL(k_tern_pack, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, kt_stream(stream),
                      bcodes, dpm, R, C, codes, scales);
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
+int kt_tern_pack_ptq1(const uint8_t* raw, int R, int C, int row0, int nrows, void* W, void* stream){
+  if(nrows == 0) return 0;
+  if(!raw || !W || R <= 0 || C <= 0 || C % 128 || !kt_al(W, 16) || row0 < 0 || row0 % KT_RG || nrows < 0
+     || row0 + nrows > R || (row0 + nrows < R && nrows % KT_RG)) return KT_INVALID;
+  const int NG = C / 128, nrg = (row0 + nrows == R ? kt_r8(R) : (row0 + nrows) / KT_RG) - row0 / KT_RG;
+  uint32_t* codes = (uint32_t*)W;
+  uint16_t* scales = (uint16_t*)((uint8_t*)W + kt_code_bytes(R, NG));
+  const long long nw = (long long)nrg * NG * 64;
+  hipLaunchKernelGGL(k_tern_pack_ptq1, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, kt_stream(stream),
+                     raw, R, C, row0, nrg, codes, scales);
   KT_LAUNCH_CHECK();
   return 0;
 }

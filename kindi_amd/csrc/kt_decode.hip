@@ -1,5 +1,6 @@
 /* kt_decode.hip - gfx950 kernels of the decode side of the quantized linear layer:
      k_tern_pack   reference pack (convert.py:144-159 bcodes [C/4][R], dpm [C/128][R]) -> kt2 device layout
+     k_tern_pack_ptq1  GGUF PTQ1_0 rows (28-byte blocks, convert.py:33-46) -> kt2, a range of row groups a launch
      k_q8_pack     GGUF Q8_0 rows (34-byte blocks) -> kq8 device layout
      k_quant_tern  fp32 rows -> int8 per 128-column group (or per row), XS, XA   (k_tc_q8, tc_hip.cu:43-74)
      k_quant_q8    fp32 rows -> int8 per 32-column block, fp16-rounded scale   (quant_q8, dsv41_cpu.c:251-280)
@@ -48,6 +49,50 @@ extern "C" __global__ void k_tern_pack(const uint8_t* __restrict__ bc, const uin
   if(i < ns){
     const int r = (int)(i & 7), u = (int)((i >> 3) % NG), rg = (int)((i >> 3) / NG), row = rg * KT_RG + r;
     scales[i] = row < R ? dpm[(long long)u * R + row] : (uint16_t)0;
+  }
+}
+
+/* digit e (0..127) of a GGUF PTQ1_0 block (convert.py:33-46): qs bytes 0..15 hold elements n 16 + j, 16..23 hold
+   80 + n 8 + j, qh bytes 24..25 hold 120 + n 2 + j; digit n of byte v = ((v 3^n) mod 256) 3 / 256 */
+__device__ __forceinline__ uint32_t kt_ptq1_digit(const uint8_t* __restrict__ blk, int e){
+  int byte, n;
+  if(e < 80){ byte = e & 15; n = e >> 4; }
+  else if(e < 120){ byte = 16 + ((e - 80) & 7); n = (e - 80) >> 3; }
+  else { byte = 24 + ((e - 120) & 1); n = (e - 120) >> 1; }
+  const uint32_t p3 = n == 0 ? 1u : n == 1 ? 3u : n == 2 ? 9u : n == 3 ? 27u : 81u;
+  return (((uint32_t)blk[byte] * p3) & 255u) * 3u >> 8;
+}
+
+extern "C" __global__ void k_tern_pack_ptq1(const uint8_t* __restrict__ raw, int R, int C, int row0, int nrg,
+                                            uint32_t* __restrict__ codes, uint16_t* __restrict__ scales){
+  /* one thread per output word of row groups row0 / 8 .. + nrg; raw = the GGUF rows from row0 on (C / 128 blocks of
+     28 bytes a row) */
+  const int NG = C >> 7, rg0 = row0 >> 3;
+  const long long nw = (long long)nrg * NG * 64;
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if(i < nw){
+    int rg, u, h, r;
+    kt_word_pos(i, NG, rg, u, h, r);
+    const int j = (int)(i & 3), row = (rg0 + rg) * KT_RG + r;
+    uint32_t w = 0x55555555u;                                  /* padding rows: digit 1 (weight 0) everywhere */
+    if(row < R){
+      w = 0u;
+      const uint8_t* blk = raw + ((long long)(row - row0) * NG + u) * 28;
+      const int e0 = h * 64 + j * 16;
+#pragma unroll
+      for(int m = 0; m < 16; ++m) w |= kt_ptq1_digit(blk, e0 + m) << (8 * (m & 3) + 2 * (m >> 2));
+    }
+    codes[(long long)rg0 * NG * 64 + i] = w;
+  }
+  const long long ns = (long long)nrg * NG * 8;
+  if(i < ns){
+    const int r = (int)(i & 7), u = (int)((i >> 3) % NG), rg = (int)((i >> 3) / NG), row = (rg0 + rg) * KT_RG + r;
+    uint16_t v = 0;
+    if(row < R){
+      const uint8_t* blk = raw + ((long long)(row - row0) * NG + u) * 28;
+      v = (uint16_t)(blk[26] | (blk[27] << 8));
+    }
+    scales[(long long)rg0 * NG * 8 + i] = v;
   }
 }
 

@@ -67,6 +67,58 @@ class TernaryMatrix(object):
     def nbytes(self):
         return self.W.numel()
 
+    @classmethod
+    def _empty(cls, R, C, device, W):
+        lib = gpudrv.load()
+        self = cls.__new__(cls)
+        self.R, self.C = int(R), int(C)
+        nbytes = lib.kt_tern_weight_bytes(self.R, self.C)
+        if nbytes == 0:
+            raise ValueError("ternary tensor %d x %d does not fit the kt2 layout (C %% 128 != 0)" % (R, C))
+        self.W = torch.empty(nbytes, dtype=torch.uint8, device=device) if W is None else W[:nbytes]
+        if self.W.numel() < nbytes or self.W.data_ptr() % 16:
+            raise ValueError("weight buffer too small or not 16-byte aligned")
+        return self
+
+    @classmethod
+    def from_ptq1(cls, raw, R, C, device="cuda", W=None):
+        """the GGUF PTQ1_0 tensor data itself (R rows of C / 128 blocks of 28 bytes; convert.py:33-46), decoded on
+        the device straight into the kt2 layout (the same W as the reference pack of it would give)"""
+        self = cls._empty(R, C, device, W)
+        rd = _dev_u8(raw, device).reshape(-1)
+        if rd.numel() != self.R * (self.C // 128) * 28:
+            raise ValueError("PTQ1_0 data does not match %d x %d" % (R, C))
+        gpudrv.check(gpudrv.load().kt_tern_pack_ptq1(ptr(rd), self.R, self.C, 0, self.R, ptr(self.W), stream()),
+                     "kt_tern_pack_ptq1")
+        return self
+
+
+def load_ptq1(path, offset, R, C, device="cuda", W=None, chunk_rows=8192):
+    """stream one PTQ1_0 tensor from a GGUF file (its data at byte `offset`) to the device in row chunks: two pinned
+    host buffers and two device buffers alternate, so reading chunk i + 1 from the file overlaps its copy and the
+    decode of chunk i (the role of tp._stream_to_card, tp.py:236-254, for the packed layout)"""
+    m = TernaryMatrix._empty(R, C, device, W)
+    bpr = (C // 128) * 28
+    chunk_rows = max(8, chunk_rows // 8 * 8)
+    src = np.memmap(path, dtype=np.uint8, mode="r", offset=offset, shape=(R * bpr,))
+    n = min(chunk_rows, R)
+    host = [torch.empty(n * bpr, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
+    dev = [torch.empty(n * bpr, dtype=torch.uint8, device=device) for _ in range(2)]
+    done = [None, None]
+    lib = gpudrv.load()
+    for k, r0 in enumerate(range(0, R, chunk_rows)):
+        b = k & 1
+        rows = min(chunk_rows, R - r0)
+        if done[b] is not None:
+            done[b].synchronize()                   # the buffers' previous chunk has been decoded
+        host[b][:rows * bpr].numpy()[:] = src[r0 * bpr:(r0 + rows) * bpr]
+        dev[b][:rows * bpr].copy_(host[b][:rows * bpr], non_blocking=True)
+        gpudrv.check(lib.kt_tern_pack_ptq1(ptr(dev[b]), R, C, r0, rows, ptr(m.W), stream()), "kt_tern_pack_ptq1")
+        done[b] = torch.cuda.Event()
+        done[b].record()
+    torch.cuda.current_stream().synchronize()
+    return m
+
 
 Act = namedtuple("Act", "XQ XS XA M C per_row")
 

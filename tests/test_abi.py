@@ -27,7 +27,7 @@ def lib():
 
 def test_exports_every_declared_symbol(lib):
     names = declared()
-    assert len(names) == 27
+    assert len(names) == 28
     for n in names:
         assert hasattr(lib, n), n
     from kindi_amd import gpudrv
@@ -126,3 +126,12 @@ def test_fold_validation(lib):
     assert lib.kt_fold_q8(f, 4000, f, 1, 4096, 4096, None, 0, f, 4096, f, f, None) == INVALID
     assert lib.kt_smfold_q8(f, 4096, f, 4096, f, 128, 4, 7, 1, 4096, 4096, None, 0, f, 4096, f, f, None) == INVALID
     assert lib.kt_smfold_q8(f, 4096, f, 4096, f, 128, 4, 0, 1, 4096, 4096, None, 0, f, 4096, f, f, None) == INVALID
+
+
+def test_ptq1_validation(lib):
+    f = ctypes.c_void_p(0x1000)
+    assert lib.kt_tern_pack_ptq1(f, 100, 200, 0, 100, f, None) == INVALID     # C % 128
+    assert lib.kt_tern_pack_ptq1(f, 100, 256, 4, 96, f, None) == INVALID      # row0 % 8
+    assert lib.kt_tern_pack_ptq1(f, 100, 256, 0, 20, f, None) == INVALID      # a middle chunk of 20 rows
+    assert lib.kt_tern_pack_ptq1(f, 100, 256, 96, 8, f, None) == INVALID      # past R
+    assert lib.kt_tern_pack_ptq1(f, 100, 256, 0, 0, f, None) == 0             # nothing to do

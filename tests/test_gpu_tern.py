@@ -267,3 +267,25 @@ def test_repeated_launches_same_bits(kt):
         if k % 10 == 9 or k > 290:
             bad += int(not np.array_equal(host(outs[i]), refs[i]))
     assert bad == 0
+
+
+@pytest.mark.parametrize("R,C", [(8, 128), (100, 256), (6144, 2048), (1024, 17408)])
+def test_pack_from_ptq1(kt, R, C, tmp_path):
+    """the GGUF PTQ1_0 tensor decoded on the device gives the same kt2 bytes as the reference pack of the same
+    digits (through kt_tern_pack), whole and streamed from a file in row chunks (ragged last chunk)"""
+    lib, linear = kt
+    say("ptq1", R, C)
+    dig, bc, dpm = tern_case(R, C, R + C)
+    NG = C // 128
+    raw = orc.ptq1_from_digits(dig.reshape(R * NG, 128), np.ascontiguousarray(dpm.T).reshape(R * NG))
+    assert np.array_equal(orc.trits_from_ptq1(raw).reshape(R, C), dig)
+    want = host(linear.TernaryMatrix(bc, dpm, R, C).W)
+    got = linear.TernaryMatrix.from_ptq1(raw, R, C)
+    assert np.array_equal(host(got.W), want)
+    f = tmp_path / "t.gguf"
+    pad = 96
+    with open(f, "wb") as fh:
+        fh.write(b"\0" * pad)
+        fh.write(raw.tobytes())
+    m = linear.load_ptq1(str(f), pad, R, C, chunk_rows=40)
+    assert np.array_equal(host(m.W), want)
