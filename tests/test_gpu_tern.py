@@ -289,3 +289,50 @@ def test_pack_from_ptq1(kt, R, C, tmp_path):
         fh.write(raw.tobytes())
     m = linear.load_ptq1(str(f), pad, R, C, chunk_rows=40)
     assert np.array_equal(host(m.W), want)
+
+
+def _gguf_bytes(tensors, kv):
+    """a small GGUF v3 file: kv {key: (type, value)}, tensors [(name, dims, type, data bytes)]"""
+    import struct
+    s = lambda x: struct.pack("<Q", len(x.encode())) + x.encode()
+    out = b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(kv))
+    for k, (ty, v) in kv.items():
+        out += s(k) + struct.pack("<I", ty)
+        if ty == 8:
+            out += s(v)
+        elif ty == 9:
+            out += struct.pack("<IQ", 4, len(v)) + b"".join(struct.pack("<I", x) for x in v)
+        else:
+            out += struct.pack("<I", v)
+    off, datas = 0, []
+    for name, dims, ty, data in tensors:
+        out += s(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+        out += struct.pack("<IQ", ty, off)
+        datas.append((off, data))
+        off = (off + len(data) + 31) // 32 * 32
+    out += b"\0" * ((len(out) + 31) // 32 * 32 - len(out))
+    body = bytearray(off)
+    for o, d in datas:
+        body[o:o + len(d)] = d
+    return out + bytes(body)
+
+
+def test_gguf_ptq1_by_name(kt, tmp_path):
+    lib, linear = kt
+    from kindi_amd import gguf
+    say("gguf")
+    tens, wants = [], {}
+    for i, (R, C) in enumerate([(24, 256), (16, 128)]):
+        dig, bc, dpm = tern_case(R, C, 50 + i)
+        NG = C // 128
+        raw = orc.ptq1_from_digits(dig.reshape(R * NG, 128), np.ascontiguousarray(dpm.T).reshape(R * NG))
+        tens.append(("blk.%d.ffn_up.weight" % i, [C, R], gguf.PTQ1_0, raw.tobytes()))
+        wants[tens[-1][0]] = host(linear.TernaryMatrix(bc, dpm, R, C).W)
+    f = tmp_path / "m.gguf"
+    f.write_bytes(_gguf_bytes(tens, {"general.architecture": (8, "test"), "general.alignment": (4, 32),
+                                     "x.list": (9, [1, 2, 3])}))
+    g = gguf.GGUF(str(f))
+    assert g.kv["general.architecture"] == "test" and g.kv["x.list"] == [1, 2, 3]
+    for name, want in wants.items():
+        m = gguf.load_ternary(str(f), name, chunk_rows=8, g=g)
+        assert np.array_equal(host(m.W), want), name
