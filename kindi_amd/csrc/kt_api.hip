@@ -75,7 +75,7 @@ static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, int32_
   int tiles = 0;
   for(int i = 0; i < a.nmat; ++i){ a.mat[i].pad = tiles; tiles += (kt_r8(a.mat[i].R) + 3) / 4; }
   const dim3 grid(tiles, (a.M + 15) / 16), block(64 * ks);
-  const size_t lds = (size_t)ks * 16 * 32 * 4;
+  const size_t lds = (size_t)ks * 16 * 32 * 4 + (size_t)ks * 256 * 4;        /* slice sums, XS */
   if(dbg) hipLaunchKernelGGL((k_gemv_mma<16, true>), grid, block, lds, s, a, xq, xs, dbg, ks);
   else hipLaunchKernelGGL((k_gemv_mma<16, false>), grid, block, lds, s, a, xq, xs, dbg, ks);
   KT_LAUNCH_CHECK();

@@ -54,6 +54,19 @@ __global__ void __launch_bounds__(64 * KT_KSMAX) k_gemv_mma(const KtGemvArgs a, 
   const uint4* __restrict__ wb = (const uint4*)m.codes;
   const uint16_t* __restrict__ sb = m.scales;
 
+  /* the slice's XS [16 units][16 tokens] into this wave's LDS region first (unconditional clamped loads, one wave
+     barrier): the epilogue then reads them from LDS, and every global load below is unconditional, so the compiler's
+     wait counts stay exact and the activation loads of later units run ahead */
+  float* xsl = (float*)(kt_lds + (size_t)KS * NT * 32 * 4) + (size_t)ks * 256;
+#pragma unroll
+  for(int q = 0; q < 4; ++q){
+    const int idx = lane + 64 * q, n = idx >> 4, tl = idx & 15;
+    const int u = (s_lo + (n >> 3)) * KT_KL + (n & 7);
+    const int t = t0 + tl < a.M ? t0 + tl : t0;
+    xsl[idx] = xs[(long long)t * a.ldxs + (u < NU ? u : 0)];
+  }
+  kt_wave_sync();
+
   float part[NE];                                                  /* the combined chains of this slice */
   float t01[NE], t23[NE], t45[NE], pend[NE];
 #pragma unroll
@@ -108,8 +121,7 @@ __global__ void __launch_bounds__(64 * KT_KSMAX) k_gemv_mma(const KtGemvArgs a, 
 #pragma unroll
         for(int e = 0; e < NE; ++e){
           const int t = t0 + km_tok(e, lane);
-          const int tc = t < a.M ? t : t0;
-          const float sx = xs[(long long)tc * a.ldxs + u];
+          const float sx = xsl[(j * 8 + c) * 16 + km_tok(e, lane)];
           chain[e] = fmaf((float)acc[e], sx * d, chain[e]);
           if(DBG && t < a.M && rok) dbg[((long long)t * m.R + row) * NU + u] = acc[e];
         }
