@@ -14,7 +14,7 @@ __global__ void k_gemv_flat(const KtGemvArgs, const KtGroupedArgs, const int8_t*
 template <int FMT, int MT, bool DBG, bool GRP>
 __global__ void k_gemv_flat1(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, const int*, int32_t*,
                              int);
-template <int NT, bool DBG>
+template <int NT, bool DBG, int LB>
 __global__ void k_gemv_mma(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
 template <bool GRP, bool DBG>
 __global__ void k_q8_mma(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
@@ -76,8 +76,18 @@ static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, int32_
   for(int i = 0; i < a.nmat; ++i){ a.mat[i].pad = tiles; tiles += (kt_r8(a.mat[i].R) + 3) / 4; }
   const dim3 grid(tiles, (a.M + 15) / 16), block(64 * ks);
   const size_t lds = (size_t)ks * 16 * 32 * 4 + (size_t)ks * 256 * 4;        /* slice sums, XS */
-  if(dbg) hipLaunchKernelGGL((k_gemv_mma<16, true>), grid, block, lds, s, a, xq, xs, dbg, ks);
-  else hipLaunchKernelGGL((k_gemv_mma<16, false>), grid, block, lds, s, a, xq, xs, dbg, ks);
+  /* fewer waves a block leave each more registers, so the activation loads run further ahead (4 units up to 4
+     slices, C <= 8192; 2 up to 10 slices) */
+  if(ks <= 4){
+    if(dbg) hipLaunchKernelGGL((k_gemv_mma<16, true, 256>), grid, block, lds, s, a, xq, xs, dbg, ks);
+    else hipLaunchKernelGGL((k_gemv_mma<16, false, 256>), grid, block, lds, s, a, xq, xs, dbg, ks);
+  } else if(ks <= 10){
+    if(dbg) hipLaunchKernelGGL((k_gemv_mma<16, true, 640>), grid, block, lds, s, a, xq, xs, dbg, ks);
+    else hipLaunchKernelGGL((k_gemv_mma<16, false, 640>), grid, block, lds, s, a, xq, xs, dbg, ks);
+  } else {
+    if(dbg) hipLaunchKernelGGL((k_gemv_mma<16, true, 64 * KT_KSMAX>), grid, block, lds, s, a, xq, xs, dbg, ks);
+    else hipLaunchKernelGGL((k_gemv_mma<16, false, 64 * KT_KSMAX>), grid, block, lds, s, a, xq, xs, dbg, ks);
+  }
   KT_LAUNCH_CHECK();
   return 0;
 }

@@ -30,11 +30,12 @@ __device__ __forceinline__ int km_trits(uint32_t dig){ return (int)__builtin_amd
 /* the token of D register e of lane l */
 __device__ __forceinline__ int km_tok(int e, int lane){ return (e & 3) + 8 * (e >> 2) + 4 * (lane >> 5); }
 
-template <int NT, bool DBG>   /* NT: the token rows of a pass (16: D registers e < 8) */
-__global__ void __launch_bounds__(64 * KT_KSMAX) k_gemv_mma(const KtGemvArgs a, const int8_t* __restrict__ xq,
+template <int NT, bool DBG, int LB>   /* NT: the token rows of a pass (16: D registers e < 8); LB: threads a block */
+__global__ void __launch_bounds__(LB) k_gemv_mma(const KtGemvArgs a, const int8_t* __restrict__ xq,
                                                             const float* __restrict__ xs,
                                                             int32_t* __restrict__ dbg, int KS){
   constexpr int NE = NT / 2;                                     /* D registers that hold used tokens */
+  constexpr int KM_PF = LB <= 256 ? 4 : LB <= 640 ? 2 : 0;        /* activation units loaded ahead (register room) */
   extern __shared__ __attribute__((aligned(16))) uint8_t kt_lds[];
   float* red = (float*)kt_lds;                                   /* [KS][NT][32] slice sums */
   const int NU = a.NU, S = kt_steps(NU);
@@ -85,6 +86,18 @@ __global__ void __launch_bounds__(64 * KT_KSMAX) k_gemv_mma(const KtGemvArgs a, 
       wq[j][c] = kt_ldnt(wb + (ok ? kt_widx(NU, rg, s, h, c, r) : 0));
       hq[j][c] = sb[ok ? kt_sidx(NU, rg, u, r) : 0];
     }
+  /* A: this lane's token, unit n's columns 64 h .. 64 h + 63, issued KM_PF units ahead of their products */
+  const int8_t* xrow = xq + (long long)(tok_ok ? tok : t0) * a.ldq + 64 * h;
+  uint4 xa[KM_PF > 0 ? KM_PF : 1][4];
+  auto ld_act = [&](int n, uint4* dst){
+    const int c = n >> 1, j = n & 1, u = (s_lo + j) * KT_KL + c;
+    const int uu = (j < ns && u < NU) ? u : 0;
+    const uint4* xp = (const uint4*)(xrow + (long long)uu * 128);
+#pragma unroll
+    for(int i = 0; i < 4; ++i) dst[i] = xp[i];
+  };
+#pragma unroll
+  for(int n = 0; n < KM_PF; ++n) ld_act(n, xa[n]);
 #pragma unroll
   for(int c = 0; c < KT_KL; ++c){
     float chain[NE];
@@ -92,14 +105,15 @@ __global__ void __launch_bounds__(64 * KT_KSMAX) k_gemv_mma(const KtGemvArgs a, 
     for(int e = 0; e < NE; ++e) chain[e] = 0.0f;
 #pragma unroll
     for(int j = 0; j < 2; ++j){
-      const int s = s_lo + j, u = s * KT_KL + c;
+      const int n = 2 * c + j, s = s_lo + j, u = s * KT_KL + c;
       const bool uok = j < ns && u < NU;                        /* wave-uniform */
-      const int uu = uok ? u : 0;
-      /* A: this lane's token, the unit's columns 64 h .. 64 h + 63 */
       uint4 xa4[4];
-      const uint4* xp = (const uint4*)(xq + (long long)(tok_ok ? tok : t0) * a.ldq + (long long)uu * 128 + 64 * h);
+      if constexpr(KM_PF == 0) ld_act(n, xa4);
+      else {
 #pragma unroll
-      for(int i = 0; i < 4; ++i) xa4[i] = xp[i];
+        for(int i = 0; i < 4; ++i) xa4[i] = xa[n % KM_PF][i];
+        if(n + KM_PF < 2 * KT_KL) ld_act(n + KM_PF, xa[n % KM_PF]);
+      }
       if(uok){
         const uint32_t ww[4] = {wq[j][c].x, wq[j][c].y, wq[j][c].z, wq[j][c].w};
         const float d = rok ? kt_h2f(hq[j][c]) : 0.0f;
@@ -152,8 +166,12 @@ __global__ void __launch_bounds__(64 * KT_KSMAX) k_gemv_mma(const KtGemvArgs a, 
   }
 }
 
-template __global__ void k_gemv_mma<16, false>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
-template __global__ void k_gemv_mma<16, true>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
+template __global__ void k_gemv_mma<16, false, 64 * KT_KSMAX>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
+template __global__ void k_gemv_mma<16, true, 64 * KT_KSMAX>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
+template __global__ void k_gemv_mma<16, false, 640>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
+template __global__ void k_gemv_mma<16, true, 640>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
+template __global__ void k_gemv_mma<16, false, 256>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
+template __global__ void k_gemv_mma<16, true, 256>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
 
 /* ------------------------------------------------------------------ q8_0 on the matrix cores
    The q8_0 product (kq8 weights against int8 rows with per-32 scales, lt_mv_q8 lightning.cu:258-284, k_q8
