@@ -65,7 +65,7 @@ static int kt_kslices(int NU){
 #define KT_MMA_MAX 32
 #define KT_Q8_MMA_KS 8                 /* q8_0 matrix-core product: K slices a block (kt_mma.hip KM_Q8_KS) */
 static bool kt_use_mma(const KtGemvArgs& a){
-  if(a.M < KT_MMA_MIN || a.M > KT_MMA_MAX) return false;
+  if(a.M < KT_MMA_MIN || a.M > KT_MMA_MAX || (long long)a.M * a.ldq >= (1ll << 30)) return false;
   long long w = 0;
   for(int i = 0; i < a.nmat; ++i) w += (long long)a.mat[i].R * a.NU * 128;
   return a.M >= KT_MMA_ANY || w >= (1ll << 24);

@@ -9,7 +9,7 @@
    MFMA i (h = l / 32), so the 4 MFMAs cover the unit's 128 columns once each and give its exact int32 value
    v(t, r) (any pairing of columns gives the same integer). A lane's kt2 load is exactly its row's 64 columns of
    the unit (kt_widx with half h), unpacked to signed trits (shift, mask, v_perm byte lookup); its activations are
-   the same 64 columns of its token, read from L2 (tokens past M are zero and not loaded).
+   the same 64 columns of its token, read from L2 (tokens past the pass or M are zero and not loaded).
 
    The fp32 epilogue takes k_gemv_flat's order: for each k-lane c (0..7) of the step layout, the chain over the
    slice's units 8 s + c in increasing s, fmaf((float)v, XS[t][u] * d[r][u], .); then ((c0 + c1) + (c2 + c3)) +
@@ -55,18 +55,19 @@ __global__ void __launch_bounds__(LB) k_gemv_mma(const KtGemvArgs a, const int8_
   const uint4* __restrict__ wb = (const uint4*)m.codes;
   const uint16_t* __restrict__ sb = m.scales;
 
-  /* the slice's XS [16 units][16 tokens] into this wave's LDS region first (unconditional clamped loads, one wave
-     barrier): the epilogue then reads them from LDS, and every global load below is unconditional, so the compiler's
+  /* the slice's XS [16 units][16 tokens] (clamped, unconditional loads) first: they go to this wave's LDS region
+     after the weight and the first activation loads are issued, so that wait leaves those in flight (loads retire
+     in order); the epilogue reads them from LDS, and every global load below is unconditional, so the compiler's
      wait counts stay exact and the activation loads of later units run ahead */
   float* xsl = (float*)(kt_lds + (size_t)KS * NT * 32 * 4) + (size_t)ks * 256;
+  float xsv[4];
 #pragma unroll
   for(int q = 0; q < 4; ++q){
     const int idx = lane + 64 * q, n = idx >> 4, tl = idx & 15;
     const int u = (s_lo + (n >> 3)) * KT_KL + (n & 7);
     const int t = t0 + tl < a.M ? t0 + tl : t0;
-    xsl[idx] = xs[(long long)t * a.ldxs + (u < NU ? u : 0)];
+    xsv[q] = xs[(long long)t * a.ldxs + (u < NU ? u : 0)];
   }
-  kt_wave_sync();
 
   float part[NE];                                                  /* the combined chains of this slice */
   float t01[NE], t23[NE], t45[NE], pend[NE];
@@ -86,18 +87,23 @@ __global__ void __launch_bounds__(LB) k_gemv_mma(const KtGemvArgs a, const int8_
       wq[j][c] = kt_ldnt(wb + (ok ? kt_widx(NU, rg, s, h, c, r) : 0));
       hq[j][c] = sb[ok ? kt_sidx(NU, rg, u, r) : 0];
     }
-  /* A: this lane's token, unit n's columns 64 h .. 64 h + 63, issued KM_PF units ahead of their products */
-  const int8_t* xrow = xq + (long long)(tok_ok ? tok : t0) * a.ldq + 64 * h;
+  /* a buffer resource over the M token rows: lanes past the pass's tokens read from offset 2^30, beyond the range
+     (the launcher keeps M ldq below it), which returns zeros without a memory access */
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, a.M * a.ldq, 0x00020000);
+  const uint32_t xoff = tok_ok ? (uint32_t)(tok * a.ldq + 64 * h) : (1u << 30);
   uint4 xa[KM_PF > 0 ? KM_PF : 1][4];
   auto ld_act = [&](int n, uint4* dst){
     const int c = n >> 1, j = n & 1, u = (s_lo + j) * KT_KL + c;
     const int uu = (j < ns && u < NU) ? u : 0;
-    const uint4* xp = (const uint4*)(xrow + (long long)uu * 128);
 #pragma unroll
-    for(int i = 0; i < 4; ++i) dst[i] = xp[i];
+    for(int i = 0; i < 4; ++i)
+      dst[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + uu * 128 + 16 * i, 0, 0));
   };
 #pragma unroll
   for(int n = 0; n < KM_PF; ++n) ld_act(n, xa[n]);
+#pragma unroll
+  for(int q = 0; q < 4; ++q) xsl[lane + 64 * q] = xsv[q];
+  kt_wave_sync();
 #pragma unroll
   for(int c = 0; c < KT_KL; ++c){
     float chain[NE];
@@ -127,8 +133,7 @@ __global__ void __launch_bounds__(LB) k_gemv_mma(const KtGemvArgs a, const int8_
           B[1] = km_trits((ww[i] >> 2) & 0x03030303u);
           B[2] = km_trits((ww[i] >> 4) & 0x03030303u);
           B[3] = km_trits((ww[i] >> 6) & 0x03030303u);
-          A[0] = tok_ok ? (int)xa4[i].x : 0; A[1] = tok_ok ? (int)xa4[i].y : 0;
-          A[2] = tok_ok ? (int)xa4[i].z : 0; A[3] = tok_ok ? (int)xa4[i].w : 0;
+          A[0] = (int)xa4[i].x; A[1] = (int)xa4[i].y; A[2] = (int)xa4[i].z; A[3] = (int)xa4[i].w;
           acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, acc, 0, 0, 0);
         }
         /* epilogue: the k-lane chain, fmaf((float)v, XS * d, .) */
