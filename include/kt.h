@@ -119,11 +119,12 @@ int kt_plan_status(const void* plan, const kt_plan_info* info, int* status, void
 
 /* ---------------------------------------------------------------- prefill product (any M, matrix cores)
    Y and/or Y16 [M][ldy] (fp32 / fp16 bits); dbg as kt_tern_gemv. XA is accepted for the reference's argument list
-   and not read (the matrix cores take signed trits). Y = sum_g fmaf(v, XS[t][g] d[r][g], .) in group order (the
-   reference's expression), except when per_row = 1 (XS from kt_quant_q8 per_row: one scale a token) and R < 8192:
-   then Y = XS[t][0] * sum_g fmaf(v, d[r][g], .) in group order (a kernel on smaller blocks for matrices with few
-   rows; the choice depends on R only, never on M). Replaces k_tc_mm2 /
-   k_tc_mm{4,8,16} (tc_hip.cu:243-269, chunk.py:273-296) and k_mm_g5q (chunk.cu:858-918, chunk.py:245-271). */
+   and not read (the matrix cores take signed trits). per_row = 0: Y = sum_g fmaf(v, XS[t][g] d[r][g], .) in group
+   order (the reference's expression). per_row = 1 (XS from kt_quant_q8 per_row: one scale a token): Y = XS[t][0] *
+   sum_g fmaf(v, d[r][g], .) in group order (two VALU operations an element and group instead of three; the same
+   bits whichever of the two block shapes R selects, within the 1e-3 tolerance of the reference's expression).
+   M ldq, M C / 32 and the packed codes stay below 2^31 bytes. Replaces k_tc_mm2 / k_tc_mm{4,8,16}
+   (tc_hip.cu:243-269, chunk.py:273-296) and k_mm_g5q (chunk.cu:858-918, chunk.py:245-271). */
 int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA,
                  int per_row, int M, float* Y, uint16_t* Y16, int ldy, int32_t* dbg, void* stream);
 

@@ -28,7 +28,7 @@ extern "C" __global__ void k_tern_pack_ptq1(const uint8_t*, int, int, int, int, 
 extern "C" __global__ void k_quant_tern(const float*, int, int, int, int8_t*, int, float*, int*);
 extern "C" __global__ void k_quant_q8(const float*, int, int, int, int8_t*, int, float*, int);
 extern "C" __global__ void k_tern_sum(const float*, float*, int, int, int);
-template <bool DBG>
+template <bool DBG, bool RS>
 __global__ void k_tern_gemm(const uint32_t*, const uint16_t*, int, int, const int8_t*, int, const float*, int, float*,
                             uint16_t*, int, int32_t*);
 template <int WT, int WR, int PD, bool DBG>
@@ -41,7 +41,7 @@ extern "C" __global__ void k_moe_route(const float*, int, int, int, int*, float*
                                        const float*, int, int, int8_t*, int, float*, int);
 
 #define KT_INVALID ((int)hipErrorInvalidValue)
-#define KT_RS_ROWS 8192                /* per-row prefill order below this many rows (include/kt.h) */
+#define KT_RS_ROWS 8192                /* per-row prefill on small blocks below this many rows */
 #define KT_LAUNCH_CHECK() do { const hipError_t _e = hipGetLastError(); if(_e != hipSuccess) return (int)_e; } while(0)
 
 static inline hipStream_t kt_stream(void* s){ return (hipStream_t)s; }
@@ -341,8 +341,9 @@ int kt_plan_status(const void* plan, const kt_plan_info* info, int* status, void
 }
 
 /* ------------------------------------------------------------------ prefill product */
-/* per-row scales: 256 tokens x 128 rows (8 waves of 2 x 2 tiles) when that gives every CU a block, else 128 x 128
-   (16 waves of one tile); both run the same per-element chain, so the bits do not depend on the choice */
+/* per_row = 0: the reference's per-group expression on 128 x 128 blocks. per_row = 1: the per-row order, on small
+   blocks (128 tokens x 64 rows) below KT_RS_ROWS rows so that every CU gets work, else on 128 x 128 blocks; both run
+   the same per-element chain, so the bits do not depend on the choice */
 int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA,
                  int per_row, int M, float* Y, uint16_t* Y16, int ldy, int32_t* dbg, void* stream){
   (void)XA;                                                  /* signed trits on the matrix cores: no digit offset */
@@ -354,8 +355,7 @@ int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const f
   const uint16_t* scales = (const uint16_t*)((const uint8_t*)W + kt_code_bytes(R, NG));
   hipStream_t s = kt_stream(stream);
   if(per_row && R < KT_RS_ROWS){
-    /* per-row order on small blocks (one 32 x 32 tile a wave, 8 waves: 128 tokens x 64 rows); the choice depends on
-       the shape of W only, so a token's result does not depend on M */
+    /* one 32 x 32 tile a wave, 8 waves: 128 tokens x 64 rows */
     const dim3 grid((R + 63) / 64, (M + 127) / 128);
     if(dbg) hipLaunchKernelGGL((k_tern_gemm_rs1<4, 2, 3, true>), grid, dim3(512), 0, s, codes, scales, R, NG, XQ, ldq,
                                XS, M, Y, Y16, ldy, dbg);
@@ -364,11 +364,15 @@ int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const f
     KT_LAUNCH_CHECK();
     return 0;
   }
+  /* the 128 x 128 kernel reads through buffer resources with 32-bit offsets */
+  if((long long)M * ldq >= (1ll << 31) || (long long)M * NG * 4 >= (1ll << 31) || kt_code_bytes(R, NG) >= (1ull << 31))
+    return KT_INVALID;
   const dim3 grid((R + 127) / 128, (M + 127) / 128);
-  if(dbg) hipLaunchKernelGGL(k_tern_gemm<true>, grid, dim3(256), 0, s, codes, scales, R, NG, XQ, ldq, XS, M,
-                     Y, Y16, ldy, dbg);
-  else hipLaunchKernelGGL(k_tern_gemm<false>, grid, dim3(256), 0, s, codes, scales, R, NG, XQ, ldq, XS, M,
-                     Y, Y16, ldy, dbg);
+#define KT_TG(DBG, RS) hipLaunchKernelGGL((k_tern_gemm<DBG, RS>), grid, dim3(256), 0, s, codes, scales, R, NG, XQ, ldq, \
+                                          XS, M, Y, Y16, ldy, dbg)
+  if(per_row){ if(dbg) KT_TG(true, true); else KT_TG(false, true); }
+  else { if(dbg) KT_TG(true, false); else KT_TG(false, false); }
+#undef KT_TG
   KT_LAUNCH_CHECK();
   return 0;
 }

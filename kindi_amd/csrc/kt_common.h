@@ -57,6 +57,20 @@ __host__ __device__ __forceinline__ long long kt_widx(int NU, int rg, int s, int
 /* index of the fp16 scale of (rg, unit u, row r) */
 __host__ __device__ __forceinline__ long long kt_sidx(int NU, int rg, int u, int r){ return ((long long)rg * NU + u) * 8 + r; }
 
+/* XCD-aware tile order. Workgroups are dispatched to the 8 XCDs round-robin by linear id, and each XCD has its own
+   L2. kt_xcd_tile maps the linear id L of a gx x gy grid to a tile (x, y) so that XCD k (the ids L = k mod 8) takes
+   a contiguous band of about gx / 8 columns x, walked y-major: the blocks resident on one XCD share their x band's
+   data and a few y rows. A bijection of [0, gx gy) for any gx, gy. */
+__host__ __device__ __forceinline__ void kt_xcd_tile(int L, int gx, int gy, int& x, int& y){
+  const int N = gx * gy, k = L & 7, i = L >> 3;
+  const int q = N >> 3, rem = N & 7;
+  const int T = k * q + (k < rem ? k : rem) + i;                  /* ids of XCDs before k, then i */
+  const int cw = (gx + 7) >> 3, band = T / (cw * gy), w = gx - band * cw < cw ? gx - band * cw : cw;
+  const int in = T - band * cw * gy;
+  y = in / w;
+  x = band * cw + in % w;
+}
+
 __device__ __forceinline__ float kt_h2f(uint16_t h){ return __half2float(__ushort_as_half(h)); }
 
 typedef unsigned int kt_u32x4 __attribute__((ext_vector_type(4)));

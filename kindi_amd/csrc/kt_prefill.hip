@@ -7,11 +7,13 @@
    as 2 x 2 MFMA tiles of 32 x 32. Per group: the block loads the 128 rows' packed trits (4 KB: one 16-byte load
    per thread, 32 lines of 128 bytes of the kt2 layout), unpacks them to signed int8 once (shift, mask, v_perm byte
    lookup) into LDS, stages the 128 tokens' int8 activations in LDS, and each wave runs 4 k-steps of 2 x 2 MFMAs.
-   Two LDS stages: the loads of group g + 1 are issued before group g's products and unpacked into the other stage
-   after its epilogue, so one barrier a group separates the stages and the memory latency overlaps the products. The
-   MFMA A operand is the activations (rows = tokens), B the weights (columns = weight rows), so a lane's 16
-   accumulators share one weight row: its group scale is one register. After the group the int32 accumulators are
-   scaled into fp32 accumulators in the reference expression and cleared.
+   Two LDS stages and two register sets: the global loads of group g + 2 (through buffer resources: 32-bit offsets,
+   out-of-range reads are zeros without a branch) are issued before group g's products, and group g + 1 is unpacked
+   into the other stage after its epilogue, so one barrier a group separates the stages and every load has two
+   groups of products to arrive. The MFMA A operand is the activations (rows = tokens), B the weights (columns =
+   weight rows), so a lane's 16 accumulators share one weight row: its group scale is one register. After the group
+   the int32 accumulators are scaled into fp32 accumulators (the reference expression, or with per-row scales
+   fmaf(v, d, .) and XS[t] at the end) and cleared. Blocks take their tiles in the XCD order of kt_xcd_tile.
 
    MFMA 32x32x32 i8 register layouts on gfx950 (measured): A lane l holds row l % 32, k = 16 (l / 32) .. +15;
    B lane l holds column l % 32, the same k; D lane l register i holds column l % 32, row (i % 4) + 8 (i / 4) +
@@ -28,7 +30,7 @@ typedef int kt_v16i __attribute__((ext_vector_type(16)));
 /* 4 digits (0/1/2, one per byte) -> 4 signed trits (-1/0/+1): byte lookup in 0x000100FF */
 __device__ __forceinline__ uint32_t kt_trits(uint32_t dig){ return __builtin_amdgcn_perm(0x000100FFu, 0x000100FFu, dig); }
 
-template <bool DBG>
+template <bool DBG, bool RS>   /* RS: per-row activation scales, Y[t][r] = XS[t][0] sum_g fmaf(v, d[r][g], .) */
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k_tern_gemm(const uint32_t* __restrict__ codes,
     const uint16_t* __restrict__ scales, int R, int NG, const int8_t* __restrict__ XQ, int ldq,
     const float* __restrict__ XS, int M, float* __restrict__ Y, uint16_t* __restrict__ Y16, int ldy,
@@ -36,45 +38,64 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k
   /* two LDS stages: group g's operands are read while group g + 1's are written; one barrier a group */
   __shared__ __attribute__((aligned(16))) uint8_t Xl[2][PF_BT * PF_LD];
   __shared__ __attribute__((aligned(16))) uint8_t Wl[2][PF_BR * PF_LD];
-  __shared__ float xs_l[2][PF_BT];
+  __shared__ float xs_l[2][2 * PF_BT];                          /* [PF_BT, 2 PF_BT): written, never read */
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wt = wv >> 1, wr = wv & 1;
-  const int r0 = blockIdx.x * PF_BR, n0 = blockIdx.y * PF_BT;
+  int bx, by;
+  kt_xcd_tile(blockIdx.x + blockIdx.y * gridDim.x, gridDim.x, gridDim.y, bx, by);
+  const int r0 = bx * PF_BR, n0 = by * PF_BT;
 
   const int R8 = kt_r8(R);
+  /* every global read goes through a buffer resource (a scalar base and a 32-bit offset a lane): an offset past the
+     range reads zeros without a memory access or a branch. Zeros only reach accumulators of rows past R or tokens past
+     M, which are never stored (the launcher keeps each buffer below 2^31 bytes, so 2^31 is past every range) */
+  const uint32_t OOB = 1u << 31;
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)codes, (short)0, R8 * NG * 256, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, R8 * NG * 16, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)XQ, (short)0, M * ldq, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)XS, (short)0, M * NG * 4, 0x00020000);
   /* this thread's weight chunk: row group r0/8 + (tid >> 4), half (tid >> 3) & 1, row tid & 7 (16 bytes = 64
      columns of one row); a unit's 128 rows are 32 chunks of 128 contiguous bytes */
   const int lrg = tid >> 4, lh = (tid >> 3) & 1, lr = tid & 7;
   const int grg = (r0 >> 3) + lrg;
-  const bool wvalid = grg < R8;
-  const uint4* __restrict__ wsrc = (const uint4*)codes;
   const int woff = (lrg * 8 + lr) * PF_LD + lh * 64;
+  /* byte offset of the chunk of group g: wbase + lh nc(g) 128 + 2048 (g / 8) + 128 (g % 8), nc(g) the units of g's
+     step (kt_widx) */
+  const uint32_t wbase = grg < R8 ? (uint32_t)(grg * NG * 16 + lr) * 16 : OOB;
 
-  /* this thread's activation chunk: token tid/2, 64 bytes at (tid&1)*64 */
+  /* this thread's activation chunk: token tid/2, 64 bytes at (tid&1)*64 (past M: out of range) */
   const int xt = tid >> 1, xh = tid & 1;
-  const bool xvalid = n0 + xt < M;
-  const int8_t* __restrict__ xsrc = XQ + (long long)(n0 + (xvalid ? xt : 0)) * ldq + xh * 64;
+  const uint32_t xbase = (uint32_t)(n0 + xt) * (uint32_t)ldq + xh * 64;
   const int xoff = xt * PF_LD + xh * 64;
+  const uint32_t sbase = tid < PF_BT ? (uint32_t)(n0 + tid) * NG * 4 : OOB;
 
   /* scales of this lane's two weight rows (columns of the 2 B tiles) */
   const int cr0 = r0 + wr * 64 + (lane & 31), cr1 = cr0 + 32;
-  const int crg0 = cr0 >> 3, crg1 = cr1 >> 3;
-  const bool c0v = (cr0 >> 3) < R8, c1v = (cr1 >> 3) < R8;
+  /* byte offsets of their scales of group 0 (group g: + 16 g) */
+  const uint32_t hbase0 = (cr0 >> 3) < R8 ? (uint32_t)(((cr0 >> 3) * NG * 8 + (cr0 & 7)) * 2) : OOB;
+  const uint32_t hbase1 = (cr1 >> 3) < R8 ? (uint32_t)(((cr1 >> 3) * NG * 8 + (cr1 & 7)) * 2) : OOB;
 
-  /* the global loads of one group (registers), then their unpack into LDS stage b */
-  struct Grp { uint4 wc; uint4 xv[4]; uint16_t h0, h1; float xs; };
-  auto load = [&](int g, Grp& q){
-    q.wc = wvalid ? kt_ldnt(wsrc + kt_widx(NG, grg, g >> 3, lh, g & 7, lr))
-                  : make_uint4(0x55555555u, 0x55555555u, 0x55555555u, 0x55555555u);
-#pragma unroll
-    for(int k = 0; k < 4; ++k) q.xv[k] = xvalid ? ((const uint4*)(xsrc + g * 128))[k] : make_uint4(0u, 0u, 0u, 0u);
-    q.h0 = c0v ? scales[kt_sidx(NG, crg0, g, cr0 & 7)] : (uint16_t)0;
-    q.h1 = c1v ? scales[kt_sidx(NG, crg1, g, cr1 & 7)] : (uint16_t)0;
-    q.xs = (tid < PF_BT && n0 + tid < M) ? XS[(long long)(n0 + tid) * NG + g] : 0.0f;
-  };
-  auto store = [&](const Grp& q, int b){
+  /* the global loads of group g into registers (clamped: past the last group it is read again, so every group issues
+     the same loads and the waits stay exact), and the unpack of a set into LDS stage b. Macros with named registers,
+     not a struct by reference: the register sets must stay in registers */
+#define KT_PF_LOADW(g, WC, H0, H1) do { \
+    const int gg_ = (g) < NG ? (g) : NG - 1; \
+    const int nc_ = NG - (gg_ & ~7) < 8 ? NG - (gg_ & ~7) : 8; \
+    WC = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wbase + (lh ? nc_ * 128 : 0), \
+         (gg_ >> 3) * 2048 + (gg_ & 7) * 128, 2)); \
+    H0 = __builtin_amdgcn_raw_buffer_load_b16(rh, hbase0, gg_ * 16, 0); \
+    H1 = __builtin_amdgcn_raw_buffer_load_b16(rh, hbase1, gg_ * 16, 0); \
+  } while(0)
+#define KT_PF_LOADX(g, X0, X1, X2, X3, XSV) do { \
+    const int gg_ = (g) < NG ? (g) : NG - 1; \
+    X0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, xbase, gg_ * 128, 0)); \
+    X1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, xbase + 16, gg_ * 128, 0)); \
+    X2 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, xbase + 32, gg_ * 128, 0)); \
+    X3 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, xbase + 48, gg_ * 128, 0)); \
+    if(!RS) XSV = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, sbase, gg_ * 4, 0)); } while(0)
+  auto store = [&](const uint4 wc, const uint4 x0, const uint4 x1, const uint4 x2, const uint4 x3, float xsv, int b){
     /* unpack: word j of the chunk = columns 16j .. +15 of the half; slot s = columns 16j + 4s .. +3 */
-    const uint32_t ww[4] = {q.wc.x, q.wc.y, q.wc.z, q.wc.w};
+    const uint32_t ww[4] = {wc.x, wc.y, wc.z, wc.w};
 #pragma unroll
     for(int j = 0; j < 4; ++j){
       uint4 o;
@@ -84,9 +105,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k
       o.w = kt_trits((ww[j] >> 6) & 0x03030303u);
       *(uint4*)(Wl[b] + woff + 16 * j) = o;
     }
-#pragma unroll
-    for(int k = 0; k < 4; ++k) *(uint4*)(Xl[b] + xoff + 16 * k) = q.xv[k];
-    if(tid < PF_BT) xs_l[b][tid] = q.xs;
+    *(uint4*)(Xl[b] + xoff) = x0;
+    *(uint4*)(Xl[b] + xoff + 16) = x1;
+    *(uint4*)(Xl[b] + xoff + 32) = x2;
+    *(uint4*)(Xl[b] + xoff + 48) = x3;
+    if(!RS) xs_l[b][tid] = xsv;
   };
 
   float acc[2][2][16];
@@ -97,14 +120,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k
 #pragma unroll
       for(int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  Grp cur, nxt;
-  load(0, cur);
-  store(cur, 0);
-  float d0 = kt_h2f(cur.h0), d1 = kt_h2f(cur.h1);
-  __syncthreads();
-  for(int g = 0; g < NG; ++g){
+  /* group g's products and epilogue from LDS stage g % 2 with row scales d0, d1 */
+  auto prod = [&](int g, float d0, float d1){
     const int b = g & 1;
-    if(g + 1 < NG) load(g + 1, nxt);                          /* in flight during this group's products */
     kt_v16i c[2][2];
 #pragma unroll
     for(int i = 0; i < 2; ++i)
@@ -125,15 +143,20 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k
 #pragma unroll
         for(int j = 0; j < 2; ++j) c[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[i], B[j], c[i][j], 0, 0, 0);
     }
-    /* group epilogue: acc += (float)v * (XS[t][g] * d[r][g]) */
+    /* group epilogue: acc += (float)v * (XS[t][g] * d[r][g]), or acc += (float)v * d[r][g] (RS) */
 #pragma unroll
     for(int i = 0; i < 2; ++i)
 #pragma unroll
       for(int e = 0; e < 16; ++e){
         const int tl = wt * 64 + i * 32 + (e & 3) + 8 * (e >> 2) + 4 * (lane >> 5);
-        const float xs = xs_l[b][tl];
-        acc[i][0][e] = fmaf((float)c[i][0][e], xs * d0, acc[i][0][e]);
-        acc[i][1][e] = fmaf((float)c[i][1][e], xs * d1, acc[i][1][e]);
+        if(RS){
+          acc[i][0][e] = fmaf((float)c[i][0][e], d0, acc[i][0][e]);
+          acc[i][1][e] = fmaf((float)c[i][1][e], d1, acc[i][1][e]);
+        } else {
+          const float xs = xs_l[b][tl];
+          acc[i][0][e] = fmaf((float)c[i][0][e], xs * d0, acc[i][0][e]);
+          acc[i][1][e] = fmaf((float)c[i][1][e], xs * d1, acc[i][1][e]);
+        }
         if(DBG){
           const int t = n0 + tl;
           if(t < M){
@@ -142,13 +165,38 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k
           }
         }
       }
-    if(g + 1 < NG){
-      store(nxt, b ^ 1);                                        /* stage b ^ 1 was last read in group g - 1 */
-      d0 = kt_h2f(nxt.h0);
-      d1 = kt_h2f(nxt.h1);
-    }
-    __syncthreads();
+  };
+
+  /* every global load two groups ahead, in two register sets: at the start of group g the set holding g + 1 is
+     landing and g + 2 is issued into the other; after group g's products, g + 1 is unpacked into the other LDS
+     stage */
+  uint4 wa, wb, xa0, xa1, xa2, xa3, xb0, xb1, xb2, xb3;
+  uint16_t ha0, ha1, hb0, hb1;
+  float xsa = 0.0f, xsb = 0.0f, d0, d1;
+  KT_PF_LOADW(0, wa, ha0, ha1);
+  KT_PF_LOADX(0, xa0, xa1, xa2, xa3, xsa);
+  KT_PF_LOADW(1, wb, hb0, hb1);
+  KT_PF_LOADX(1, xb0, xb1, xb2, xb3, xsb);
+  store(wa, xa0, xa1, xa2, xa3, xsa, 0);
+  d0 = kt_h2f(ha0); d1 = kt_h2f(ha1);
+  __syncthreads();
+  /* step: group g; set S holds g + 1, set T takes g + 2 */
+#define KT_PF_STEP(g, WS, HS0, HS1, XS0, XS1, XS2, XS3, XSS, WT_, HT0, HT1, XT0, XT1, XT2, XT3, XST) do { \
+    KT_PF_LOADW((g) + 2, WT_, HT0, HT1); \
+    KT_PF_LOADX((g) + 2, XT0, XT1, XT2, XT3, XST); \
+    prod((g), d0, d1); \
+    store(WS, XS0, XS1, XS2, XS3, XSS, ((g) & 1) ^ 1); \
+    d0 = kt_h2f(HS0); d1 = kt_h2f(HS1); \
+    __syncthreads(); } while(0)
+  int g = 0;
+  for(; g + 2 <= NG; g += 2){
+    KT_PF_STEP(g, wb, hb0, hb1, xb0, xb1, xb2, xb3, xsb, wa, ha0, ha1, xa0, xa1, xa2, xa3, xsa);
+    KT_PF_STEP(g + 1, wa, ha0, ha1, xa0, xa1, xa2, xa3, xsa, wb, hb0, hb1, xb0, xb1, xb2, xb3, xsb);
   }
+  if(g < NG) prod(g, d0, d1);
+#undef KT_PF_STEP
+#undef KT_PF_LOADW
+#undef KT_PF_LOADX
   /* store: lanes of one register write 32 consecutive rows of one token */
 #pragma unroll
   for(int i = 0; i < 2; ++i)
@@ -156,22 +204,23 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k
     for(int e = 0; e < 16; ++e){
       const int t = n0 + wt * 64 + i * 32 + (e & 3) + 8 * (e >> 2) + 4 * (lane >> 5);
       if(t < M){
+        const float xr = RS ? XS[(long long)t * NG] : 1.0f;
+        const float y0 = RS ? acc[i][0][e] * xr : acc[i][0][e], y1 = RS ? acc[i][1][e] * xr : acc[i][1][e];
         if(cr0 < R){
-          if(Y) Y[(long long)t * ldy + cr0] = acc[i][0][e];
-          if(Y16) Y16[(long long)t * ldy + cr0] = __half_as_ushort(__float2half_rn(acc[i][0][e]));
+          if(Y) Y[(long long)t * ldy + cr0] = y0;
+          if(Y16) Y16[(long long)t * ldy + cr0] = __half_as_ushort(__float2half_rn(y0));
         }
         if(cr1 < R){
-          if(Y) Y[(long long)t * ldy + cr1] = acc[i][1][e];
-          if(Y16) Y16[(long long)t * ldy + cr1] = __half_as_ushort(__float2half_rn(acc[i][1][e]));
+          if(Y) Y[(long long)t * ldy + cr1] = y1;
+          if(Y16) Y16[(long long)t * ldy + cr1] = __half_as_ushort(__float2half_rn(y1));
         }
       }
     }
 }
 
-template __global__ void k_tern_gemm<false>(const uint32_t*, const uint16_t*, int, int, const int8_t*, int, const float*,
-                                            int, float*, uint16_t*, int, int32_t*);
-template __global__ void k_tern_gemm<true>(const uint32_t*, const uint16_t*, int, int, const int8_t*, int, const float*,
-                                           int, float*, uint16_t*, int, int32_t*);
+#define KT_TG(DBG, RS) template __global__ void k_tern_gemm<DBG, RS>(const uint32_t*, const uint16_t*, int, int, \
+    const int8_t*, int, const float*, int, float*, uint16_t*, int, int32_t*);
+KT_TG(false, false) KT_TG(true, false) KT_TG(false, true) KT_TG(true, true)
 
 /* ------------------------------------------------------------------ per-row activation scales
    The prefill product when the activations are quantized per token (kt_quant_q8 per_row: one XS a token, the
@@ -195,7 +244,9 @@ __global__ void __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_
   __shared__ __attribute__((aligned(16))) uint8_t Wl[2][BR * PF_LD];
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, wt = wv / WR, wr = wv % WR;
-  const int r0 = blockIdx.x * BR, n0 = blockIdx.y * BT;
+  int bx, by;
+  kt_xcd_tile(blockIdx.x + blockIdx.y * gridDim.x, gridDim.x, gridDim.y, bx, by);
+  const int r0 = bx * BR, n0 = by * BT;
   const int R8 = kt_r8(R);
 
   /* activations: token tid / 4 of the block, 32 bytes at (tid % 4) 32 of each group (clamped to a real row) */

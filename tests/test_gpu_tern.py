@@ -138,11 +138,11 @@ def test_gemm_small(kt, R, C, M):
 
 
 @pytest.mark.parametrize("R,C,M", [(128, 256, 128), (100, 384, 5), (256, 512, 300), (384, 1024, 200),
-                                   (8192, 128, 1024), (8100, 256, 1000)])
+                                   (8192, 128, 1024), (8100, 256, 1000), (8200, 256, 130)])
 def test_gemm_per_row(kt, R, C, M):
-    """per-row activation scales (below 8192 rows the small-block kernel in the per-row order, above it the 128 x 128
-    kernel in the reference's order; ragged rows and tokens): int32 group values exact, fp32 bit-exact in the
-    documented order, fp16 its rounding, and within the tolerance of the reference's sequential order"""
+    """per-row activation scales (the per-row order on both block shapes: small blocks below 8192 rows, 128 x 128
+    from 8192; ragged rows and tokens): int32 group values exact, fp32 bit-exact in the documented order, fp16 its
+    rounding, and within the tolerance of the reference's sequential order"""
     lib, linear = kt
     say("gemm per-row", R, C, M)
     W, dig, bc, dpm = upload(linear, R, C, R * 7 + M)
@@ -157,7 +157,7 @@ def test_gemm_per_row(kt, R, C, M):
     acc = orc.tern_acc(bc, R, C, Q)
     assert np.array_equal(host(dbg), acc), "int32 group values"
     seq = orc.tern_out(acc, XS, dpm, R, C)
-    want = orc.tern_out_rs(acc, XS, dpm, R, C) if R < 8192 else seq      # the per-row order below 8192 rows
+    want = orc.tern_out_rs(acc, XS, dpm, R, C)                             # the per-row order at every R
     y = host(Y)
     assert np.array_equal(y, want), "fp32 in the documented order"
     assert np.array_equal(host(Y16), want.astype(np.float16))
@@ -188,7 +188,7 @@ def test_gemm_config2_sampled(kt, R, C, M):
     assert np.array_equal(host(act.XQ), Q)
     acc = orc.tern_acc(np.ascontiguousarray(bc), len(rows), C, Q)
     seq = orc.tern_out(acc, XS, np.ascontiguousarray(dpm), len(rows), C)
-    want = orc.tern_out_rs(acc, XS, np.ascontiguousarray(dpm), len(rows), C) if R < 8192 else seq
+    want = orc.tern_out_rs(acc, XS, np.ascontiguousarray(dpm), len(rows), C)
     y = host(Y)
     assert np.array_equal(y[:, rows], want), "documented order"
     assert max_rel(y[:, rows], seq) < TOL
