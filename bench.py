@@ -213,6 +213,17 @@ def config2(torch, linear, synth, timer, steps):
             tops = 2.0 * M * R * C / ms / 1e9
             res["%s M=%d" % (n, M)] = {"shape": [R, C], "us": round(ms * 1e3, 1), "TOPS": round(tops, 1),
                                        "frac_int8_peak": round(tops / INT8_PEAK, 4)}
+            # the vendor's plain int8 GEMM (hipBLASLt through torch._int_mm: int32 out, no scales, no trit unpack)
+            # on the same shapes and box, as the practical ceiling of an int8 product here
+            try:
+                qa = act.XQ[:, :C].contiguous()
+                qb = torch.randint(-1, 2, (C, R), dtype=torch.int8, device="cuda")
+                vms = timer.run(lambda: torch._int_mm(qa, qb), max(steps // 2, 3), 2)
+                vt = 2.0 * M * R * C / vms / 1e9
+                res["%s M=%d" % (n, M)].update({"vendor_int8_TOPS": round(vt, 1), "vs_vendor": round(tops / vt, 3)})
+                del qb
+            except Exception as e:                                   # not every build routes int8 mm
+                res["%s M=%d" % (n, M)]["vendor_int8"] = repr(e)[:80]
     return res
 
 

@@ -419,10 +419,10 @@ int kt_q8_gemv(const void* W, int R, int C, const int8_t* Q, int ldq, const floa
   a.ldq = ldq; a.ldxs = ldd;
   a.M = M;
   const int ks = kt_kslices(NB);
-  if(M >= KT_MMA_MIN && ks <= KT_Q8_MMA_KS){
+  if(M >= KT_MMA_MIN && ks <= KT_Q8_MMA_KS && (long long)M * ldq < (1ll << 31)){
     /* the matrix-core product (the same numbers and tree): tiles of 32 rows, all tokens a block */
     const dim3 grid((kt_r8(R) + 3) / 4), block(64 * ks);
-    const size_t lds = (size_t)ks * 16 * 32 * 4;
+    const size_t lds = (size_t)ks * 16 * 32 * 4 + (size_t)ks * 256 * 4;          /* slice sums, D */
     const KtGroupedArgs ga = {};
     if(dbg) hipLaunchKernelGGL((k_q8_mma<false, true>), grid, block, lds, kt_stream(stream), a, ga, Q, D, dbg, ks);
     else hipLaunchKernelGGL((k_q8_mma<false, false>), grid, block, lds, kt_stream(stream), a, ga, Q, D, dbg, ks);
@@ -473,16 +473,17 @@ int kt_q8_grouped(const void* const* Wexp, int R, int C, int E, const int* cnt, 
   a.wexp = (const uint8_t* const*)Wexp;
   a.R = R; a.C = C; a.NU = C / 32;
   a.cnt = cnt; a.off = off; a.act = act; a.nact = nact; a.xrow = xrow;
-  a.ldq = ldq; a.ldd = ldd; a.ldy = ldy;
+  a.ldq = ldq; a.ldd = ldd; a.ldy = ldy; a.nrows = xrow ? M : nentries;
   a.y = Y;
   const int ks = kt_kslices(a.NU);
   const int ny = E < nentries ? E : nentries;
   hipStream_t s = kt_stream(stream);
-  if(nentries >= 4 * ny && ks <= KT_Q8_MMA_KS){
+  /* the matrix-core kernel reads the input rows through a buffer resource with 32-bit offsets */
+  if(nentries >= 4 * ny && ks <= KT_Q8_MMA_KS && (long long)a.nrows * ldq < (1ll << 31)){
     /* 4 or more entries an active expert on average: the matrix-core product per (32-row tile, active expert), the
        expert's whole list in passes of 16 (the same numbers and tree) */
     const dim3 grid((kt_r8(R) + 3) / 4, ny), block(64 * ks);
-    const size_t lds = (size_t)ks * 16 * 32 * 4;
+    const size_t lds = (size_t)ks * 16 * 32 * 4 + (size_t)ks * 256 * 4;          /* slice sums, D */
     const KtGemvArgs da = {};
     if(dbg) hipLaunchKernelGGL((k_q8_mma<true, true>), grid, block, lds, s, da, a, Q, D, dbg, ks);
     else hipLaunchKernelGGL((k_q8_mma<true, false>), grid, block, lds, s, da, a, Q, D, dbg, ks);

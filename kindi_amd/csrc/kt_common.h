@@ -151,7 +151,7 @@ struct KtGroupedArgs {
   const int* cnt; const int* off;     /* per expert: list length and start */
   const int* act; const int* nact;    /* active experts (ascending) and their count */
   const int* xrow;                    /* nullable: input row of list entry p (else p itself) */
-  int ldq, ldd, ldy, pad2;
+  int ldq, ldd, ldy, nrows;           /* nrows: input rows (M with xrow, else the entries) */
   float* y;                           /* output rows [entries][ldy] */
 };
 

@@ -224,6 +224,35 @@ __global__ void __launch_bounds__(64 * KM_Q8_KS) k_q8_mma(const KtGemvArgs a, co
   const int rg = tile * 4 + (lr >> 3), r = lr & 7, row = rg * KT_RG + r;
   const bool rok = row < R;
   const int s_lo = ks * S / KS, ns = (ks + 1) * S / KS - s_lo;   /* this slice's steps (1 or 2) */
+  const int nrows = GRP ? ga.nrows : cntM;
+
+  /* a pass's loads, all unconditional (clamped) and issued together: the D scales of the slice's 16 units x 16
+     tokens (to this wave's LDS region before the products, so the epilogue reads them there), and this lane's
+     activations of the 16 units through a buffer resource over the input rows (lanes past the pass's tokens read at
+     2^31, past the range, which gives zeros without a memory access; the launcher keeps the rows below 2^31 bytes) */
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, nrows * ldq, 0x00020000);
+  float* xsl = (float*)(kt_lds + (size_t)KS * NT * 32 * 4) + (size_t)ks * 256;
+  float xsv[4];
+  uint4 xa[2 * KT_KL];
+  auto ld_pass = [&](int t0){
+    const int nt = min(NT, cntM - t0);
+#pragma unroll
+    for(int q = 0; q < 4; ++q){
+      const int idx = lane + 64 * q, n = idx >> 4, tl = idx & 15;
+      const int u = (s_lo + (n >> 3)) * KT_KL + (n & 7);
+      const int pt = p0 + t0 + (tl < nt ? tl : 0), nr = xrow ? xrow[pt] : pt;
+      xsv[q] = xd[(long long)nr * ldd + (u < NU ? u : 0)];
+    }
+    const int pe = p0 + t0 + (lr < nt ? lr : 0), na = xrow ? xrow[pe] : pe;
+    const uint32_t xo = lr < nt ? (uint32_t)(na * ldq + 16 * h) : (1u << 31);
+#pragma unroll
+    for(int n = 0; n < 2 * KT_KL; ++n){
+      const int c = n >> 1, j = n & 1, u = (s_lo + j) * KT_KL + c;
+      const int uu = (j < ns && u < NU) ? u : 0;
+      xa[n] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo + uu * 32, 0, 0));
+    }
+  };
+  ld_pass(0);
 
   /* the slice's 16 units in k-lane-major order, loaded once (unconditional: a unit past the slice or the matrix
      reads offset 0) */
@@ -240,16 +269,9 @@ __global__ void __launch_bounds__(64 * KM_Q8_KS) k_q8_mma(const KtGemvArgs a, co
     }
 
   for(int t0 = 0; t0 < cntM; t0 += NT){                          /* uniform: the block's list in passes */
-    const int nt = min(NT, cntM - t0);
-    const bool tok_ok = lr < nt;
-    const int pe = p0 + t0 + (tok_ok ? lr : 0);
-    const int n_a = xrow ? xrow[pe] : pe;                        /* this lane's A row */
-    int n_e[NE];                                                 /* the input rows of this lane's D registers */
 #pragma unroll
-    for(int e = 0; e < NE; ++e){
-      const int t = km_tok(e, lane), pt = p0 + t0 + (t < nt ? t : 0);
-      n_e[e] = xrow ? xrow[pt] : pt;
-    }
+    for(int q = 0; q < 4; ++q) xsl[lane + 64 * q] = xsv[q];
+    kt_wave_sync();
     float part[NE], t01[NE], t23[NE], t45[NE], pend[NE];
 #pragma unroll
     for(int e = 0; e < NE; ++e){ part[e] = 0.0f; t01[e] = 0.0f; t23[e] = 0.0f; t45[e] = 0.0f; pend[e] = 0.0f; }
@@ -262,18 +284,15 @@ __global__ void __launch_bounds__(64 * KM_Q8_KS) k_q8_mma(const KtGemvArgs a, co
       for(int j = 0; j < 2; ++j){
         const int s = s_lo + j, u = s * KT_KL + c;
         const bool uok = j < ns && u < NU;                      /* wave-uniform */
-        const int uu = uok ? u : 0;
-        const uint4 xa = *(const uint4*)(xq + (long long)n_a * ldq + (long long)uu * 32 + 16 * h);
+        const uint4 x = xa[2 * c + j];
         if(uok){
           const float d = rok ? kt_h2f(hq[j][c]) : 0.0f;
-          kt_v4i A, B;
-          A[0] = tok_ok ? (int)xa.x : 0; A[1] = tok_ok ? (int)xa.y : 0;
-          A[2] = tok_ok ? (int)xa.z : 0; A[3] = tok_ok ? (int)xa.w : 0;
-          B[0] = (int)wq[j][c].x; B[1] = (int)wq[j][c].y; B[2] = (int)wq[j][c].z; B[3] = (int)wq[j][c].w;
+          const kt_v4i A = {(int)x.x, (int)x.y, (int)x.z, (int)x.w};
+          const kt_v4i B = {(int)wq[j][c].x, (int)wq[j][c].y, (int)wq[j][c].z, (int)wq[j][c].w};
           const kt_v16i acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, (kt_v16i){}, 0, 0, 0);
 #pragma unroll
           for(int e = 0; e < NE; ++e){
-            const float sx = xd[(long long)n_e[e] * ldd + u];
+            const float sx = xsl[(j * 8 + c) * 16 + km_tok(e, lane)];
             chain[e] = fmaf((float)acc[e], d * sx, chain[e]);
             if(DBG){
               const int t = t0 + km_tok(e, lane);
@@ -291,6 +310,7 @@ __global__ void __launch_bounds__(64 * KM_Q8_KS) k_q8_mma(const KtGemvArgs a, co
         else part[e] = t23[e] + (t45[e] + (pend[e] + chain[e]));
       }
     }
+    if(t0 + NT < cntM) ld_pass(t0 + NT);                          /* uniform: the next pass's loads in flight */
 #pragma unroll
     for(int e = 0; e < NE; ++e) red[((size_t)ks * NT + km_tok(e, lane)) * 32 + lr] = part[e];
     __syncthreads();
