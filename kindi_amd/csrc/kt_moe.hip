@@ -15,52 +15,76 @@
 #include "kt_common.h"
 
 
-/* the k largest of E <= 1024 logits by one wave, the logits in registers (lane l holds e = l + 64 i): k rounds of a
-   wave arg-max (ties to the lower index, a chosen entry masked out) on the VALU exchanges; lane 0 writes ids and the
-   weights exp(l_j - l_max) / sum of the chosen */
-__device__ __forceinline__ void kt_topk_wave(const float* __restrict__ l, int E, int k, int* __restrict__ ids,
-                                             float* __restrict__ gw, int lane, int (&sel)[16]){
-  float v[16];
+/* the k largest of E <= 1024 logits by one wave, the logits in registers (lane l holds e = l + 64 i, loaded together,
+   clamped): k rounds of a wave arg-max (ties to the lower index, a chosen entry masked out) on the VALU exchanges,
+   branch-free (selects, not branches: the loads are one round trip and the rounds one straight chain). Pick j lands
+   in lane j, which writes ids[j] and the weight exp(l_j - l_max) / sum of the chosen (the sum in j order, as a
+   sequential loop over the picks). Returns lane j's pick (lanes >= k: the last one). */
+template <int NI>   /* logits a lane: E <= 64 NI */
+__device__ __forceinline__ int kt_topk_wave_n(const float* __restrict__ l, int E, int k, int* __restrict__ ids,
+                                              float* __restrict__ gw, int lane){
+  float v[NI];
 #pragma unroll
-  for(int i = 0; i < 16; ++i){ const int e = lane + 64 * i; v[i] = e < E ? l[e] : -INFINITY; }
+  for(int i = 0; i < NI; ++i){
+    const int e = lane + 64 * i;
+    const float x = l[e < E ? e : E - 1];
+    v[i] = e < E ? x : -INFINITY;
+  }
   unsigned used = 0u;
-  float lv[16];
+  int mine = 0;
+  float myv = 0.0f;
+  for(int j = 0; j < k; ++j){                                      /* uniform */
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
 #pragma unroll
-  for(int j = 0; j < 16; ++j){
-    sel[j] = 0; lv[j] = 0.0f;
-    if(j < k){
-      float bv = -INFINITY;
-      int bi = 0x7FFFFFFF;
-#pragma unroll
-      for(int i = 0; i < 16; ++i){
-        const int e = lane + 64 * i;
-        if(e < E && !(used >> i & 1u) && (v[i] > bv || (v[i] == bv && e < bi))){ bv = v[i]; bi = e; }
-      }
-#define KT_TOPK_STEP(X) { const float ov = kf_xorf<X>(bv); const int oi = kf_xor<X>(bi); \
-      if(ov > bv || (ov == bv && oi < bi)){ bv = ov; bi = oi; } }
-      KT_TOPK_STEP(1) KT_TOPK_STEP(2) KT_TOPK_STEP(4) KT_TOPK_STEP(8) KT_TOPK_STEP(16) KT_TOPK_STEP(32)
-#undef KT_TOPK_STEP
-      bi = __builtin_amdgcn_readfirstlane(bi);
-      bv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(bv)));
-      if((bi & 63) == lane) used |= 1u << (bi >> 6);
-      sel[j] = bi; lv[j] = bv;
+    for(int i = 0; i < NI; ++i){
+      const int e = lane + 64 * i;
+      const bool ok = e < E && !(used >> i & 1u) && (v[i] > bv || (v[i] == bv && e < bi));
+      bv = ok ? v[i] : bv;
+      bi = ok ? e : bi;
     }
+#define KT_TOPK_STEP(X) { const float ov = kf_xorf<X>(bv); const int oi = kf_xor<X>(bi); \
+    const bool tk = ov > bv || (ov == bv && oi < bi); bv = tk ? ov : bv; bi = tk ? oi : bi; }
+    KT_TOPK_STEP(1) KT_TOPK_STEP(2) KT_TOPK_STEP(4) KT_TOPK_STEP(8) KT_TOPK_STEP(16) KT_TOPK_STEP(32)
+#undef KT_TOPK_STEP
+    bi = __builtin_amdgcn_readfirstlane(bi);
+    bv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(bv)));
+    used |= (bi & 63) == lane ? 1u << (bi >> 6) : 0u;
+    mine = lane == j ? bi : mine;
+    myv = lane == j ? bv : myv;
   }
-  if(lane == 0){
-    float p[16], s = 0.0f;
+  const float lmax = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(myv)));
+  const float p = expf(myv - lmax);
+  float sum = 0.0f;
+  for(int j = 0; j < k; ++j) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), j));
+  if(lane < k){ ids[lane] = mine; gw[lane] = p / sum; }
+  return mine;
+}
+/* the scan length by E (uniform): a lane scans only the logits it holds */
+__device__ __forceinline__ int kt_topk_wave(const float* __restrict__ l, int E, int k, int* __restrict__ ids,
+                                            float* __restrict__ gw, int lane){
+  if(E <= 128) return kt_topk_wave_n<2>(l, E, k, ids, gw, lane);
+  if(E <= 256) return kt_topk_wave_n<4>(l, E, k, ids, gw, lane);
+  return kt_topk_wave_n<16>(l, E, k, ids, gw, lane);
+}
+
+/* exclusive prefix sum over the wave's 64 lanes (6 lane shifts through ds_bpermute); *total = the sum */
+__device__ __forceinline__ int kt_wave_excl_scan(int v, int lane, int* total){
+  int inc = v;
 #pragma unroll
-    for(int j = 0; j < 16; ++j) if(j < k){ p[j] = expf(lv[j] - lv[0]); s += p[j]; }
-#pragma unroll
-    for(int j = 0; j < 16; ++j) if(j < k){ ids[j] = sel[j]; gw[j] = p[j] / s; }
+  for(int d = 1; d < 64; d <<= 1){
+    const int y = __builtin_amdgcn_ds_bpermute(((lane - d) & 63) << 2, inc);
+    inc += lane >= d ? y : 0;
   }
+  *total = __builtin_amdgcn_readlane(inc, 63);
+  return inc - v;
 }
 
 extern "C" __global__ void __launch_bounds__(64) k_moe_topk(const float* __restrict__ logits, int E, int k,
                                                             int* __restrict__ ids, float* __restrict__ gw){
   /* one wave per token; E <= 1024, k <= 16 */
   const int t = blockIdx.x;
-  int sel[16];
-  kt_topk_wave(logits + (long long)t * E, E, k, ids + t * k, gw + t * k, threadIdx.x, sel);
+  kt_topk_wave(logits + (long long)t * E, E, k, ids + t * k, gw + t * k, threadIdx.x);
 }
 
 /* an exclusive scan of v over the block's 1024 threads (in-wave shuffle scan, then the 16 wave totals) */
@@ -147,25 +171,39 @@ extern "C" __global__ void __launch_bounds__(256) k_moe_route(const float* __res
   if(threadIdx.x >= 64){
     /* waves 1..3: the tokens' int8 rows, k_quant_q8's numbers (act 0): a 32-lane half per 32-column block */
     if(!x) return;
+    /* blocks h, h + 6, ... of every token, KT_RQ at a time: their loads issued together (clamped to a real block),
+       then the reductions and stores, so a half-wave waits for memory once per KT_RQ blocks, not once per block */
     const int h = (threadIdx.x - 64) >> 5, l = threadIdx.x & 31, nb = H / 32;
+    constexpr int KT_RQ = 8;
     for(int t = 0; t < M; ++t)
-      for(int b = h; b < nb; b += 6){
-        const float v = x[(long long)t * ldx + b * 32 + l];
-        float a = fabsf(v);
-        a = fmaxf(a, kf_xorf<1>(a)); a = fmaxf(a, kf_xorf<2>(a)); a = fmaxf(a, kf_xorf<4>(a));
-        a = fmaxf(a, kf_xorf<8>(a)); a = fmaxf(a, kf_xorf<16>(a));
-        const float id = a != 0.0f ? 127.0f / a : 0.0f;
-        Q[(long long)t * ldq + b * 32 + l] = (int8_t)__float2int_rn(v * id);
-        if(l == 0) D[(long long)t * ldd + b] = __half2float(__float2half_rn(a / 127.0f));
+      for(int b0 = h; b0 < nb; b0 += 6 * KT_RQ){
+        float v[KT_RQ];
+#pragma unroll
+        for(int q = 0; q < KT_RQ; ++q){
+          const int b = b0 + 6 * q;
+          v[q] = x[(long long)t * ldx + (b < nb ? b : h) * 32 + l];
+        }
+#pragma unroll
+        for(int q = 0; q < KT_RQ; ++q){
+          const int b = b0 + 6 * q;
+          float a = fabsf(v[q]);
+          a = fmaxf(a, kf_xorf<1>(a)); a = fmaxf(a, kf_xorf<2>(a)); a = fmaxf(a, kf_xorf<4>(a));
+          a = fmaxf(a, kf_xorf<8>(a)); a = fmaxf(a, kf_xorf<16>(a));
+          const float id = a != 0.0f ? 127.0f / a : 0.0f;
+          if(b < nb){
+            Q[(long long)t * ldq + b * 32 + l] = (int8_t)__float2int_rn(v[q] * id);
+            if(l == 0) D[(long long)t * ldd + b] = __half2float(__float2half_rn(a / 127.0f));
+          }
+        }
       }
     return;
   }
   int ep = -1;                                                     /* entry lane's expert */
   for(int t = 0; t < M; ++t){
-    int sel[16];
-    kt_topk_wave(logits + (long long)t * E, E, k, ids + t * k, gw + t * k, lane, sel);
-#pragma unroll
-    for(int j = 0; j < 16; ++j) if(j < k && lane == t * k + j) ep = sel[j];
+    /* entry lanes t k .. t k + k - 1 take the picks from lanes 0 .. k - 1 */
+    const int mine = kt_topk_wave(logits + (long long)t * E, E, k, ids + t * k, gw + t * k, lane);
+    const int got = __builtin_amdgcn_ds_bpermute(((lane - t * k) & 63) << 2, mine);
+    ep = lane >= t * k && lane < t * k + k ? got : ep;
   }
   int c[16];
 #pragma unroll
@@ -178,13 +216,8 @@ extern "C" __global__ void __launch_bounds__(256) k_moe_route(const float* __res
   int tot = 0, na = 0;
 #pragma unroll
   for(int i = 0; i < 16; ++i){ tot += c[i]; na += c[i] > 0 ? 1 : 0; }
-  int base = 0, abase = 0, all = 0;
-  for(int l = 0; l < 64; ++l){
-    const int tl = __builtin_amdgcn_readlane(tot, l), al = __builtin_amdgcn_readlane(na, l);
-    base += l < lane ? tl : 0;
-    abase += l < lane ? al : 0;
-    all += al;
-  }
+  int tall, all;
+  int base = kt_wave_excl_scan(tot, lane, &tall), abase = kt_wave_excl_scan(na, lane, &all);
 #pragma unroll
   for(int i = 0; i < 16; ++i){
     const int e = 16 * lane + i;
