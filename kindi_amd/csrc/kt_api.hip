@@ -456,8 +456,8 @@ int kt_moe_route(const float* logits, int M, int E, int k, int* ids, float* gw, 
 int kt_moe_sort(const int* ids, int M, int k, int E, int* cnt, int* off, int* xrow, int* where, int* act, int* nact,
                 void* stream){
   if(!ids || !cnt || !off || !xrow || !where || !act || !nact || M < 0 || k <= 0 || E <= 0 || E > 1024) return KT_INVALID;
-  hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(1024), 0, kt_stream(stream), ids, M * k, E, cnt, off, xrow, where, act,
-                     nact, k);
+  hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(1024), (size_t)16 * E * 4, kt_stream(stream), ids, M * k, E, cnt, off,
+                     xrow, where, act, nact, k);
   KT_LAUNCH_CHECK();
   return 0;
 }

@@ -106,13 +106,14 @@ __device__ __forceinline__ int kt_block_excl_scan(int v, int* wsum){
 
 __device__ __forceinline__ void kt_moe_lists(const int* __restrict__ ids, int n, int E, int* __restrict__ cnt,
     int* __restrict__ off, int* __restrict__ xrow, int* __restrict__ where, int* __restrict__ act,
-    int* __restrict__ nact, int k){
-  /* one block of 1024 threads; n = M k entries, E <= 1024. Counting with LDS atomics (order-free); offsets and the
-     active list by block scans; placement by one wave per expert (experts w, w + 16, ...): over the entries in
-     order, 64 at a time, a ballot of the matches gives each its rank, so an expert's entries keep ascending flat
-     index (stable) */
+    int* __restrict__ nact, int k, int* __restrict__ wc){
+  /* one block of 1024 threads; n = M k entries, E <= 1024; wc: 16 E ints of LDS. Counting with LDS atomics
+     (order-free); offsets and the active list by block scans; placement in chunks of 1024 entries, one a thread: the
+     lanes of a wave holding the same expert found by ten ballots over the expert's bits (the lane's rank among them
+     in lane order), each wave's count per expert in wc, an exclusive scan of those over the 16 waves per expert; an
+     entry's place = its expert's offset + the earlier waves' count + its rank, so an expert's entries keep
+     ascending flat index (stable) */
   __shared__ int c[1024], o[1024], wsum[16];
-  __shared__ int chunk[2048];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   c[tid] = 0;
   __syncthreads();
@@ -128,33 +129,42 @@ __device__ __forceinline__ void kt_moe_lists(const int* __restrict__ ids, int n,
     if(ce > 0) act[ae] = tid;
     if(tid == E - 1) *nact = ae + (ce > 0 ? 1 : 0);
   }
-  __syncthreads();
-  for(int i0 = 0; i0 < n; i0 += 2048){
-    const int m = min(2048, n - i0);
-    for(int i = tid; i < m; i += 1024) chunk[i] = ids[i0 + i];
+  for(int i0 = 0; i0 < n; i0 += 1024){
+    for(int q = tid; q < 16 * E; q += 1024) wc[q] = 0;
     __syncthreads();
-    for(int e = w; e < E; e += 16){
-      int pos = o[e];
-      for(int j = 0; j < m; j += 64){
-        const bool hit = j + lane < m && chunk[j + lane] == e;
-        const unsigned long long b = __ballot(hit);
-        if(hit){
-          const int p = pos + __popcll(b & ((1ull << lane) - 1ull));
-          xrow[p] = (i0 + j + lane) / k;
-          where[i0 + j + lane] = p;
-        }
-        pos += __popcll(b);
-      }
-      if(lane == 0) o[e] = pos;                                 /* the next chunk continues here */
+    const int i = i0 + tid;
+    const bool valid = i < n;
+    const int e = valid ? ids[i] : 0;
+    unsigned long long eq = __ballot(valid);
+#pragma unroll
+    for(int b = 0; b < 10; ++b){
+      const bool bit = (e >> b) & 1;
+      const unsigned long long bal = __ballot(bit);
+      eq &= bit ? bal : ~bal;
+    }
+    const int rk = __popcll(eq & ((1ull << lane) - 1ull));
+    if(valid && rk == 0) wc[w * E + e] = __popcll(eq);
+    __syncthreads();
+    if(tid < E){
+      int run = o[tid];
+      for(int ww = 0; ww < 16; ++ww){ const int t = wc[ww * E + tid]; wc[ww * E + tid] = run; run += t; }
+      o[tid] = run;                                              /* the next chunk continues here */
     }
     __syncthreads();
+    if(valid){
+      const int p = wc[w * E + e] + rk;
+      xrow[p] = i / k;
+      where[i] = p;
+    }
+    __syncthreads();                                             /* wc is cleared for the next chunk */
   }
 }
 
 extern "C" __global__ void __launch_bounds__(1024) k_moe_sort(const int* __restrict__ ids, int n, int E,
     int* __restrict__ cnt, int* __restrict__ off, int* __restrict__ xrow, int* __restrict__ where,
     int* __restrict__ act, int* __restrict__ nact, int k){
-  kt_moe_lists(ids, n, E, cnt, off, xrow, where, act, nact, k);
+  extern __shared__ int kt_moe_wc[];                              /* 16 E */
+  kt_moe_lists(ids, n, E, cnt, off, xrow, where, act, nact, k, kt_moe_wc);
 }
 
 /* the router and the lists in one launch, by one wave (n = M k <= 64 entries, E <= 1024): the top-k of each token

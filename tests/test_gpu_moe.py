@@ -53,6 +53,28 @@ def test_q8_gemv(kt, R, C, M):
     assert max_rel(y, orc.q8_out(acc, rows, R, C, d)) < TOL
 
 
+@pytest.mark.parametrize("E,M", [(60, 1), (60, 300), (1024, 200), (1000, 700)])
+def test_sort_wide(kt, E, M):
+    """kt_moe_sort at other expert counts (not a power of two, the 1024 maximum), one expert taking half the
+    entries, several 1024-entry chunks: the lists equal the oracle's (stable order)"""
+    lib, moe = kt
+    say("sort wide", E, M)
+    from kindi_amd.linear import ptr, stream
+    k = 6
+    ids = rng(E + M).integers(0, E, (M, k)).astype(np.int32)
+    ids[: (M + 1) // 2, 0] = E - 1
+    d = dev(ids)
+    cnt, off, xrow, where, act = [torch.empty(n, dtype=torch.int32, device="cuda") for n in (E, E, M * k, M * k, E)]
+    nact = torch.empty(1, dtype=torch.int32, device="cuda")
+    assert lib.kt_moe_sort(ptr(d), M, k, E, ptr(cnt), ptr(off), ptr(xrow), ptr(where), ptr(act), ptr(nact),
+                           stream()) == 0
+    rc, ro, rx, rw = orc.moe_sort(ids, E)
+    assert np.array_equal(host(cnt), rc) and np.array_equal(host(off), ro)
+    assert np.array_equal(host(xrow), rx) and np.array_equal(host(where), rw)
+    active = np.nonzero(rc)[0]
+    assert host(nact)[0] == len(active) and np.array_equal(host(act)[:len(active)], active)
+
+
 def test_topk_and_sort(kt):
     lib, moe = kt
     say("topk + sort")
