@@ -58,10 +58,16 @@ static int kt_kslices(int NU){
 }
 
 /* up to 32 ternary tokens: the matrix-core product (the same numbers and tree, so the same bits), tiles of 32 rows
-   of one matrix, passes of 16 tokens. It pays from 12 tokens on launches of 2^24 weights or more and from 24 tokens
-   on any (measured on MI355X: 27B-class layers from 12 tokens, 2B-class layers from about 24) */
-#define KT_MMA_MIN 12
-#define KT_MMA_ANY 24
+   of one matrix, passes of 16 tokens. It pays from 6 tokens on launches of 2^24 weights or more and from 8 tokens
+   on any (measured on MI355X: a 27B-class step at 8 tokens 6.36 -> 3.96 ms, at 4 tokens 3.85 -> 3.80 ms; a 2B-class
+   layer even at 8 tokens, 18.8 -> 20.5 us at 4) */
+#ifndef KT_MMA_MIN
+#define KT_MMA_MIN 6
+#endif
+#ifndef KT_MMA_ANY
+#define KT_MMA_ANY 8
+#endif
+#define KT_Q8_MMA_MIN 12               /* q8_0 dense: the matrix-core product from 12 tokens */
 #define KT_MMA_MAX 32
 #define KT_Q8_MMA_KS 8                 /* q8_0 matrix-core product: K slices a block (kt_mma.hip KM_Q8_KS) */
 static bool kt_use_mma(const KtGemvArgs& a){
@@ -419,7 +425,7 @@ int kt_q8_gemv(const void* W, int R, int C, const int8_t* Q, int ldq, const floa
   a.ldq = ldq; a.ldxs = ldd;
   a.M = M;
   const int ks = kt_kslices(NB);
-  if(M >= KT_MMA_MIN && ks <= KT_Q8_MMA_KS && (long long)M * ldq < (1ll << 31)){
+  if(M >= KT_Q8_MMA_MIN && ks <= KT_Q8_MMA_KS && (long long)M * ldq < (1ll << 31)){
     /* the matrix-core product (the same numbers and tree): tiles of 32 rows, all tokens a block */
     const dim3 grid((kt_r8(R) + 3) / 4), block(64 * ks);
     const size_t lds = (size_t)ks * 16 * 32 * 4 + (size_t)ks * 256 * 4;          /* slice sums, D */

@@ -1,4 +1,4 @@
-/* kt_mma.hip - the decode product on the matrix cores for up to 32 tokens (passes of 16; the launcher takes it from 12) (k_tc_mv*, tc_hip.cu:180-240, at
+/* kt_mma.hip - the decode product on the matrix cores for up to 32 tokens (passes of 16; the launcher takes it from 6 or 8 tokens) (k_tc_mv*, tc_hip.cu:180-240, at
    the verify widths spec.py:45 takes them): ternary weights (kt2) against int8 token rows, the same numbers and the
    same summation tree as k_gemv_flat, so a token's bits do not depend on which of the two kernels ran it.
 

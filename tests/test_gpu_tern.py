@@ -75,7 +75,7 @@ def test_gemv_m1(kt, R, C):
 @pytest.mark.parametrize("R,C", [(640, 1024), (2048, 6144), (4096, 4096)])
 def test_gemv_token_invariance(kt, R, C):
     """a token's output does not depend on how many tokens share the pass (tc_hip.cu:14-15), for M = 1 .. 32: the
-    bandwidth kernel and the matrix-core kernel (from 12 tokens at 2^24 weights, from 24 on any) give the same bits"""
+    bandwidth kernel and the matrix-core kernel (from 6 tokens at 2^24 weights, from 8 on any) give the same bits"""
     lib, linear = kt
     say("gemv T-invariance", R, C)
     W, dig, bc, dpm = upload(linear, R, C, 5 + R)
