@@ -234,16 +234,27 @@ __global__ void __launch_bounds__(64 * KM_Q8_KS) k_q8_mma(const KtGemvArgs a, co
   float* xsl = (float*)(kt_lds + (size_t)KS * NT * 32 * 4) + (size_t)ks * 256;
   float xsv[4];
   uint4 xa[2 * KT_KL];
+  /* the pass's input rows (the list indirection) first, the loads that need them after */
+  int nrq[4], na = 0;
+  auto ld_rows = [&](int t0){
+    const int nt = min(NT, cntM - t0);
+#pragma unroll
+    for(int q = 0; q < 4; ++q){
+      const int tl = (lane + 64 * q) & 15;
+      const int pt = p0 + t0 + (tl < nt ? tl : 0);
+      nrq[q] = xrow ? xrow[pt] : pt;
+    }
+    const int pe = p0 + t0 + (lr < nt ? lr : 0);
+    na = xrow ? xrow[pe] : pe;
+  };
   auto ld_pass = [&](int t0){
     const int nt = min(NT, cntM - t0);
 #pragma unroll
     for(int q = 0; q < 4; ++q){
-      const int idx = lane + 64 * q, n = idx >> 4, tl = idx & 15;
+      const int idx = lane + 64 * q, n = idx >> 4;
       const int u = (s_lo + (n >> 3)) * KT_KL + (n & 7);
-      const int pt = p0 + t0 + (tl < nt ? tl : 0), nr = xrow ? xrow[pt] : pt;
-      xsv[q] = xd[(long long)nr * ldd + (u < NU ? u : 0)];
+      xsv[q] = xd[(long long)nrq[q] * ldd + (u < NU ? u : 0)];
     }
-    const int pe = p0 + t0 + (lr < nt ? lr : 0), na = xrow ? xrow[pe] : pe;
     const uint32_t xo = lr < nt ? (uint32_t)(na * ldq + 16 * h) : (1u << 31);
 #pragma unroll
     for(int n = 0; n < 2 * KT_KL; ++n){
@@ -252,7 +263,10 @@ __global__ void __launch_bounds__(64 * KM_Q8_KS) k_q8_mma(const KtGemvArgs a, co
       xa[n] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo + uu * 32, 0, 0));
     }
   };
-  ld_pass(0);
+  /* the input rows of pass 0, then the weights (independent of them), then the pass's D and activations, so the
+     weight stream overlaps the list indirection */
+  ld_rows(0);
+  __builtin_amdgcn_sched_barrier(0);
 
   /* the slice's 16 units in k-lane-major order, loaded once (unconditional: a unit past the slice or the matrix
      reads offset 0) */
@@ -267,6 +281,8 @@ __global__ void __launch_bounds__(64 * KM_Q8_KS) k_q8_mma(const KtGemvArgs a, co
       wq[j][c] = kt_ldnt(wb + (ok ? kt_widx(NU, rg, s, h, c, r) : 0));
       hq[j][c] = sb[ok ? kt_sidx(NU, rg, u, r) : 0];
     }
+  __builtin_amdgcn_sched_barrier(0);
+  ld_pass(0);
 
   for(int t0 = 0; t0 < cntM; t0 += NT){                          /* uniform: the block's list in passes */
 #pragma unroll
@@ -310,7 +326,7 @@ __global__ void __launch_bounds__(64 * KM_Q8_KS) k_q8_mma(const KtGemvArgs a, co
         else part[e] = t23[e] + (t45[e] + (pend[e] + chain[e]));
       }
     }
-    if(t0 + NT < cntM) ld_pass(t0 + NT);                          /* uniform: the next pass's loads in flight */
+    if(t0 + NT < cntM){ ld_rows(t0 + NT); ld_pass(t0 + NT); }                          /* uniform: the next pass's loads in flight */
 #pragma unroll
     for(int e = 0; e < NE; ++e) red[((size_t)ks * NT + km_tok(e, lane)) * 32 + lr] = part[e];
     __syncthreads();
