@@ -103,8 +103,10 @@ __device__ __forceinline__ void kt_gemv_flat_body(const KtGemvArgs& a, const KtG
   int R, ldy, rg, M, p0, ldq, ldxs;
   const int* xrow = nullptr;
   if(GRP){
-    if((int)blockIdx.y >= *ga.nact) return;
-    const int e = ga.act[blockIdx.y];
+    /* the active count and this block's expert loaded together (act holds E entries: an index past the count reads
+       an unused entry, not used) */
+    const int nact = *ga.nact, e = ga.act[blockIdx.y];
+    if((int)blockIdx.y >= nact) return;
     const uint8_t* base = ga.wexp[e];
     wb = (const uint4*)base;
     sb = (const uint16_t*)(base + (long long)kt_r8(ga.R) * NU * 256);

@@ -205,8 +205,10 @@ __global__ void __launch_bounds__(64 * KM_Q8_KS) k_q8_mma(const KtGemvArgs a, co
   int R, ldy, NU, ldq, ldd, cntM, p0;
   const int* xrow = nullptr;
   if(GRP){
-    if((int)blockIdx.y >= *ga.nact) return;
-    const int e = ga.act[blockIdx.y];
+    /* the active count and this block's expert loaded together (act holds E entries: an index past the count reads
+       an unused entry, not used) */
+    const int nact = *ga.nact, e = ga.act[blockIdx.y];
+    if((int)blockIdx.y >= nact) return;
     const uint8_t* base = ga.wexp[e];
     NU = ga.NU; R = ga.R;
     wb = (const uint4*)base;
