@@ -343,8 +343,16 @@ def cpu_baseline(synth, budget_s=12.0, nlayers=4):
         reps += 1
     el = time.perf_counter() - t0
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count()))
+    model = ""
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
     return {"value": round(nbytes * reps / el / 1e9, 2), "unit": "GB/s", "cores": threads,
-            "kind": "reference" if ref else "port",
+            "cpu": model, "host_cpus": os.cpu_count(), "kind": "reference" if ref else "port",
             "sample": "%d layer passes of the 27B-class decode (q,k,v,o,gate,up,down; %.1f MB of ternary weights per "
                       "layer, %d distinct layers rotating) in %.1f s: fp32 pair-table GEMV (kcpu.c gemv), %d OpenMP "
                       "threads" % (reps, nbytes / 1e6, nlayers, el, threads)}
