@@ -65,6 +65,11 @@ def test_validation_rejects_bad_shapes(lib):
     # null output
     assert lib.kt_tern_gemm(fake, 64, 256, fake, 256, fake, fake, 0, 4, None, None, 64, None, None) == INVALID
     assert lib.kt_tern_gemm(fake, 64, 256, fake, 256, fake, fake, 2, 4, fake, None, 256, None, None) == INVALID
+    # the 128 x 128 kernel's 32-bit buffer offsets: M ldq at 2^31 bytes and more is refused (per-group scales, and
+    # per-row scales from 8192 rows, take that kernel)
+    assert lib.kt_tern_gemm(fake, 64, 256, fake, 1 << 16, fake, fake, 0, 1 << 15, fake, None, 256, None, None) == INVALID
+    assert lib.kt_tern_gemm(fake, 8192, 256, fake, 1 << 16, fake, fake, 1, 1 << 15, fake, None, 8192, None,
+                            None) == INVALID
     # q8: C % 32
     assert lib.kt_q8_gemv(fake, 64, 48, fake, 48, fake, 1, 1, fake, 64, None, None) == INVALID
     # moe: k > 16, E > 1024
