@@ -134,7 +134,8 @@ int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const f
    (dsv41_gpu.cu:66-88) and the Q8_0 repack of lightning.py.
    kt_q8_quant: X fp32 -> Q int8 [M][ldq] + D f32 [M][ldd] per 32 columns, llama.cpp's CPU rounding
    (d = fp16(amax/127), q = rne(x * 127 / amax); quant_q8 dsv41_cpu.c:251-280, moe_cpu.c:84-112); act = 1 applies
-   relu^2 first (lt_quant2, lightning.cu:470).
+   relu^2 first (lt_quant2, lightning.cu:470). X 16-byte aligned with ldx % 4 == 0, Q 4-byte aligned with
+   ldq % 4 == 0.
    kt_q8_gemv: Y = W x for M tokens: per block v = sum w q exact, acc = fmaf((float)v, dw * dx, acc) (lt_mv_q8
    lightning.cu:258-284, k_q8 dsv41_gpu.cu:131-296), summed in kt_tern_gemv's order over 32-column units
    (KS = kt_decode_kslices(C, 1)); dbg int32 [M][R][C/32]. */

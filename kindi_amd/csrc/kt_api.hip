@@ -403,9 +403,10 @@ int kt_q8_pack(const uint8_t* rows, int R, int C, void* W, void* stream){
 
 int kt_q8_quant(const float* X, int ldx, int M, int C, int act, int8_t* Q, int ldq, float* D, int ldd, void* stream){
   if(M == 0) return 0;
-  if(!X || !Q || !D || M < 0 || C <= 0 || C % 32 || ldx < C || ldq < C || ldd < C / 32) return KT_INVALID;
+  if(!X || !Q || !D || M < 0 || C <= 0 || C % 32 || ldx < C || ldq < C || ldd < C / 32 || !kt_al(X, 16) || ldx % 4
+     || !kt_al(Q, 4) || ldq % 4) return KT_INVALID;
   const int NB = C / 32;
-  hipLaunchKernelGGL(k_quant_q8, dim3((NB + 7) / 8, M), dim3(256), 0, kt_stream(stream), X, ldx, C, act ? 1 : 0, Q,
+  hipLaunchKernelGGL(k_quant_q8, dim3((NB + 31) / 32, M), dim3(256), 0, kt_stream(stream), X, ldx, C, act ? 1 : 0, Q,
                      ldq, D, ldd);
   KT_LAUNCH_CHECK();
   return 0;

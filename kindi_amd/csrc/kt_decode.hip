@@ -176,16 +176,30 @@ extern "C" __global__ void __launch_bounds__(256) k_quant_tern(const float* __re
    intermediate, lightning.cu lt_quant2). */
 extern "C" __global__ void __launch_bounds__(256) k_quant_q8(const float* __restrict__ X, int ldx, int C, int act,
                                                              int8_t* __restrict__ Q, int ldq, float* __restrict__ D, int ldd){
-  const int n = blockIdx.y, b = blockIdx.x * 8 + (threadIdx.x >> 5), l = threadIdx.x & 31;
-  if(b * 32 >= C) return;                                    /* whole 32-lane halves leave together */
-  float v = X[(long long)n * ldx + b * 32 + l];
-  if(act){ v = fmaxf(v, 0.0f); v = v * v; }
-  float a = fabsf(v);
+  /* a thread takes 4 consecutive columns (one 16-byte load, one 4-byte store), 8 lanes a 32-column block, 32 blocks a
+     256-thread block; the block's absmax by 3 VALU lane exchanges (max is exact in any order) */
+  const int n = blockIdx.y, b = blockIdx.x * 32 + (threadIdx.x >> 3), l = threadIdx.x & 7;
+  const bool ok = b * 32 < C;                                 /* whole 8-lane groups leave together */
+  const int bb = ok ? b : 0;
+  const float4 x = *(const float4*)(X + (long long)n * ldx + bb * 32 + 4 * l);
+  float v[4] = {x.x, x.y, x.z, x.w};
+  float a = 0.0f;
 #pragma unroll
-  for(int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 32));
+  for(int i = 0; i < 4; ++i){
+    if(act){ v[i] = fmaxf(v[i], 0.0f); v[i] = v[i] * v[i]; }
+    a = fmaxf(a, fabsf(v[i]));
+  }
+  a = fmaxf(a, kf_xorf<1>(a));
+  a = fmaxf(a, kf_xorf<2>(a));
+  a = fmaxf(a, kf_xorf<4>(a));
   const float id = a != 0.0f ? 127.0f / a : 0.0f;
-  Q[(long long)n * ldq + b * 32 + l] = (int8_t)__float2int_rn(v * id);
-  if(l == 0) D[(long long)n * ldd + b] = __half2float(__float2half_rn(a / 127.0f));
+  uint32_t q = 0;
+#pragma unroll
+  for(int i = 0; i < 4; ++i) q |= (uint32_t)(uint8_t)(int8_t)__float2int_rn(v[i] * id) << (8 * i);
+  if(ok){
+    *(uint32_t*)(Q + (long long)n * ldq + b * 32 + 4 * l) = q;
+    if(l == 0) D[(long long)n * ldd + b] = __half2float(__float2half_rn(a / 127.0f));
+  }
 }
 
 /* ------------------------------------------------------------------ the split parts of a k_tc_mv launch */
