@@ -72,6 +72,8 @@ def test_validation_rejects_bad_shapes(lib):
                             None) == INVALID
     # q8: C % 32
     assert lib.kt_q8_gemv(fake, 64, 48, fake, 48, fake, 1, 1, fake, 64, None, None) == INVALID
+    assert lib.kt_q8_quant(fake, 66, 2, 64, 0, fake, 64, fake, 2, None) == INVALID      # ldx % 4 (vector loads)
+    assert lib.kt_q8_quant(fake, 64, 2, 64, 0, fake, 66, fake, 2, None) == INVALID      # ldq % 4 (word stores)
     # moe: k > 16, E > 1024
     assert lib.kt_moe_topk(fake, 1, 128, 17, fake, fake, None) == INVALID
     assert lib.kt_moe_sort(fake, 1, 6, 2048, fake, fake, fake, fake, fake, fake, None) == INVALID
