@@ -359,6 +359,9 @@ int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const f
   const int NG = C / 128;
   const uint32_t* codes = (const uint32_t*)W;
   const uint16_t* scales = (const uint16_t*)((const uint8_t*)W + kt_code_bytes(R, NG));
+  /* both kernels read through buffer resources with 32-bit offsets */
+  if((long long)M * ldq >= (1ll << 31) || (long long)M * NG * 4 >= (1ll << 31) || kt_code_bytes(R, NG) >= (1ull << 31))
+    return KT_INVALID;
   hipStream_t s = kt_stream(stream);
   if(per_row && R < KT_RS_ROWS){
     /* one 32 x 32 tile a wave, 8 waves: 128 tokens x 64 rows */
@@ -370,9 +373,6 @@ int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const f
     KT_LAUNCH_CHECK();
     return 0;
   }
-  /* the 128 x 128 kernel reads through buffer resources with 32-bit offsets */
-  if((long long)M * ldq >= (1ll << 31) || (long long)M * NG * 4 >= (1ll << 31) || kt_code_bytes(R, NG) >= (1ull << 31))
-    return KT_INVALID;
   const dim3 grid((R + 127) / 128, (M + 127) / 128);
 #define KT_TG(DBG, RS) hipLaunchKernelGGL((k_tern_gemm<DBG, RS>), grid, dim3(256), 0, s, codes, scales, R, NG, XQ, ldq, \
                                           XS, M, Y, Y16, ldy, dbg)

@@ -249,35 +249,43 @@ __global__ void __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_
   const int r0 = bx * BR, n0 = by * BT;
   const int R8 = kt_r8(R);
 
-  /* activations: token tid / 4 of the block, 32 bytes at (tid % 4) 32 of each group (clamped to a real row) */
+  /* every global read through a buffer resource: an offset past the range (2^31; the launcher keeps the buffers
+     below it) reads zeros without a memory access or a branch, and zeros only reach rows past R or tokens past M,
+     which are never stored */
+  const uint32_t OOB = 1u << 31;
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)codes, (short)0, R8 * NG * 256, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, R8 * NG * 16, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)XQ, (short)0, M * ldq, 0x00020000);
+  /* activations: token tid / 4 of the block, 32 bytes at (tid % 4) 32 of each group */
   const int xt = tid >> 2, xq = tid & 3;
-  const int8_t* xsrc = XQ + (long long)(n0 + xt < M ? n0 + xt : M - 1) * ldq + xq * 32;
+  const uint32_t xbase = (uint32_t)(n0 + xt) * (uint32_t)ldq + xq * 32;
   const int xdst = xt * PF_LD + xq * 32;
   /* packed trits: word tid of the group's NW (chunk tid / 4 = (row group, half, row), word tid % 4) */
   const bool wown = tid < NW;
   const int ch = (tid >> 2) & (2 * BR - 1), wj = tid & 3;
   const int lrg = ch >> 4, lh = (ch >> 3) & 1, lr = ch & 7;
   const int grg = (r0 >> 3) + lrg;
-  const bool wvalid = grg < R8;
+  const uint32_t wbase = grg < R8 ? (uint32_t)(grg * NG * 16 + lr) * 16 + wj * 4 : OOB;
   const int wdst = (lrg * 8 + lr) * PF_LD + lh * 64 + 16 * wj;
   /* this lane's tile: tokens 32 wt + .., weight row cr (its scale row clamped to a real one) */
   const int cr = r0 + 32 * wr + (lane & 31);
-  const int srow = cr < R8 * KT_RG ? cr : 0;
+  const uint32_t hbase = cr < R8 * KT_RG ? (uint32_t)(((cr >> 3) * NG * 8 + (cr & 7)) * 2) : OOB;
 
   /* the global loads of group g (clamped: past the last group it is read again) into registers X0 X1 W H; the
      LDS stores of such a set into stage b. Macros with named registers, not a struct: the three sets must stay in
      registers (a struct by reference let the compiler merge the three steps behind a pointer select) */
 #define KT_RS1_LOAD(g, X0, X1, W, H) do { \
     const int gg_ = (g) < NG ? (g) : NG - 1; \
-    const uint4* xp_ = (const uint4*)(xsrc + gg_ * 128); \
-    X0 = xp_[0]; X1 = xp_[1]; \
-    W = codes[wvalid ? kt_widx(NG, grg, gg_ >> 3, lh, gg_ & 7, lr) * 4 + wj : 0]; \
-    H = scales[kt_sidx(NG, srow >> 3, gg_, srow & 7)]; } while(0)
+    const int nc_ = NG - (gg_ & ~7) < 8 ? NG - (gg_ & ~7) : 8; \
+    X0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, xbase, gg_ * 128, 0)); \
+    X1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, xbase + 16, gg_ * 128, 0)); \
+    W = __builtin_amdgcn_raw_buffer_load_b32(rw, wbase + (lh ? nc_ * 128 : 0), (gg_ >> 3) * 2048 + (gg_ & 7) * 128, 2); \
+    H = __builtin_amdgcn_raw_buffer_load_b16(rh, hbase, gg_ * 16, 0); } while(0)
   auto store = [&](const uint4 x0, const uint4 x1, const uint32_t wraw, int b){
     *(uint4*)(Xl[b] + xdst) = x0;
     *(uint4*)(Xl[b] + xdst + 16) = x1;
     if(wown){
-      const uint32_t w = wvalid ? wraw : 0x55555555u;           /* rows past the matrix: digit 1, trit 0 */
+      const uint32_t w = wraw;                                  /* rows past the matrix: zeros, never stored */
       uint4 o;
       o.x = kt_trits(w & 0x03030303u);
       o.y = kt_trits((w >> 2) & 0x03030303u);
