@@ -221,9 +221,9 @@ int kt_tern_gemv3(const void* W0, int R0, float* Y0, const void* W1, int R1, flo
 
 int kt_tern_sum(const float* P, float* y, int R, int M, int sp, void* stream){
   if(M == 0) return 0;
-  if(!P || !y || R <= 0 || M < 0 || sp <= 0) return KT_INVALID;
-  const long long n = (long long)R * M;
-  hipLaunchKernelGGL(k_tern_sum, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, kt_stream(stream), P, y, R, M, sp);
+  if(!P || !y || R <= 0 || M < 0 || M > 65535 || sp <= 0) return KT_INVALID;
+  hipLaunchKernelGGL(k_tern_sum, dim3((unsigned)((R + 255) / 256), (unsigned)M), dim3(256), 0, kt_stream(stream), P, y,
+                     R, M, sp);
   KT_LAUNCH_CHECK();
   return 0;
 }
@@ -452,7 +452,7 @@ int kt_moe_route(const float* logits, int M, int E, int k, int* ids, float* gw, 
                  int* where, int* act, int* nact, const float* x, int ldx, int H, int8_t* Q, int ldq, float* D, int ldd,
                  void* stream){
   if(!logits || !ids || !gw || !cnt || !off || !xrow || !where || !act || !nact || M < 0 || E <= 0 || E > 1024 ||
-     k <= 0 || k > 16 || k > E || M * k > 64) return KT_INVALID;
+     k <= 0 || k > 16 || k > E || M > 64 || (long long)M * k > 64) return KT_INVALID;
   if(x && (H <= 0 || H % 32 || ldx < H || !Q || ldq < H || !D || ldd < H / 32)) return KT_INVALID;
   hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(256), 0, kt_stream(stream), logits, M, E, k, ids, gw, cnt, off, xrow,
                      where, act, nact, x, ldx, H, Q, ldq, D, ldd);
@@ -462,7 +462,8 @@ int kt_moe_route(const float* logits, int M, int E, int k, int* ids, float* gw, 
 
 int kt_moe_sort(const int* ids, int M, int k, int E, int* cnt, int* off, int* xrow, int* where, int* act, int* nact,
                 void* stream){
-  if(!ids || !cnt || !off || !xrow || !where || !act || !nact || M < 0 || k <= 0 || E <= 0 || E > 1024) return KT_INVALID;
+  if(!ids || !cnt || !off || !xrow || !where || !act || !nact || M < 0 || k <= 0 || k > 16 || E <= 0 || E > 1024
+     || (long long)M * k > (1ll << 30)) return KT_INVALID;
   hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(1024), (size_t)16 * E * 4, kt_stream(stream), ids, M * k, E, cnt, off,
                      xrow, where, act, nact, k);
   KT_LAUNCH_CHECK();

@@ -203,13 +203,23 @@ extern "C" __global__ void __launch_bounds__(256) k_quant_q8(const float* __rest
 }
 
 /* ------------------------------------------------------------------ the split parts of a k_tc_mv launch */
-/* k_tc_sum (tc_hip.cu:271-279): y[n R + r] = sum_p P[(n sp + p) R + r], parts in order */
-extern "C" __global__ void k_tern_sum(const float* __restrict__ P, float* __restrict__ y, int R, int ntok, int sp){
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if(i >= (long long)R * ntok) return;
-  const long long n = i / R, r = i - n * R;
-  const float* q = P + n * sp * R + r;
-  float s = q[0];
-  for(int p = 1; p < sp; ++p) s += q[(long long)p * R];
-  y[i] = s;
+/* the part sums of a split product (k_tc_sum, tc_hip.cu:271-279): y[n R + r] = P_0 + P_1 + ... + P_{sp-1} in part
+   order, P_p = P[(n sp + p) R + r]. Grid (row blocks, tokens): thread r of token blockIdx.y; the parts are read 8 at a
+   time with every load of a batch issued before the first add, then added left to right. */
+extern "C" __global__ void __launch_bounds__(256) k_tern_sum(const float* __restrict__ P, float* __restrict__ y, int R,
+                                                             int ntok, int sp){
+  (void)ntok;
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  if(r >= R) return;
+  const long long n = blockIdx.y;
+  const float* col = P + n * sp * R + r;
+  float acc = col[0];
+  for(int p0 = 1; p0 < sp; p0 += 8){
+    float v[8];
+#pragma unroll
+    for(int k = 0; k < 8; ++k) v[k] = p0 + k < sp ? col[(long long)(p0 + k) * R] : 0.0f;
+#pragma unroll
+    for(int k = 0; k < 8; ++k) if(p0 + k < sp) acc += v[k];
+  }
+  y[n * R + r] = acc;
 }

@@ -16,8 +16,9 @@ __device__ __forceinline__ const KtPStage& kt_stage_at(const uint8_t* plan, int 
    each until every counter has reached its count for barrier k ((k + 1) x its blocks: counts only grow, and no
    block arrives at barrier k + 1 before all have arrived at k). No cache-wide maintenance: what crosses stages is
    made coherent where it is written and read instead (agent-scope stores of the output rows; agent-scope loads of
-   a stage's inputs when they overlap an earlier stage's outputs), and the workgroup-scope fences wait for this
-   wave's own stores before it arrives. */
+   a stage's inputs when they overlap an earlier stage's outputs). The fences here are workgroup scope and do not
+   wait for the wave's outstanding stores: a caller whose stores must be visible to the other blocks waits for them
+   (s_waitcnt vmcnt(0)) before it arrives. */
 __device__ __forceinline__ void kt_plan_barrier(unsigned* ctr, unsigned k, unsigned G, int lane){
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   unsigned* status = ctr + KT_BAR_STATUS * 32;

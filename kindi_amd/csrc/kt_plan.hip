@@ -58,7 +58,10 @@ __global__ void __launch_bounds__(1024) k_plan(const uint8_t* __restrict__ plan,
     /* ---------------------------------------------------------------- control wave */
     int par = 0;
     for(int s = 0; s < nS; ++s){
-      if(s > 0) kt_plan_barrier(ctr, (unsigned)(s - 1), (unsigned)G, lane);
+      /* the block's rows of stage s - 1 are complete in memory before it arrives: the agent-scope stores are
+         relaxed and a workgroup-scope fence does not wait for them (the control wave issues no other memory
+         operations, so this waits for nothing else) */
+      if(s > 0){ __builtin_amdgcn_s_waitcnt(0); kt_plan_barrier(ctr, (unsigned)(s - 1), (unsigned)G, lane); }
       kt_block_sync();                                           /* B1: stage s may start */
       const KtPStage& S = kt_stage_at(plan, s);
       for(int i = b; i < S.nitems; i += G){

@@ -77,6 +77,15 @@ def test_validation_rejects_bad_shapes(lib):
     # moe: k > 16, E > 1024
     assert lib.kt_moe_topk(fake, 1, 128, 17, fake, fake, None) == INVALID
     assert lib.kt_moe_sort(fake, 1, 6, 2048, fake, fake, fake, fake, fake, fake, None) == INVALID
+    assert lib.kt_moe_sort(fake, 1, 17, 128, fake, fake, fake, fake, fake, fake, None) == INVALID      # k > 16
+    assert lib.kt_moe_sort(fake, 1 << 27, 16, 128, fake, fake, fake, fake, fake, fake, None) == INVALID  # M k > 2^30
+    # the one-wave route: M k <= 64, checked without int overflow (M k = 2^32 + 6 wraps to 6 in 32 bits)
+    route = [fake, 1, 128, 6] + [fake] * 8 + [None, 0, 0, None, 0, None, 0, None]
+    assert lib.kt_moe_route(*(route[:1] + [11] + route[2:])) == INVALID                  # 66 entries
+    assert lib.kt_moe_route(*(route[:1] + [(1 << 31) // 3 + 1] + route[2:])) == INVALID
+    assert lib.kt_moe_route(*(route[:1] + [715827883] + route[2:])) == INVALID          # 6 M wraps to 2 in int32
+    # tern_sum: a token count past the grid's y range
+    assert lib.kt_tern_sum(fake, fake, 64, 70000, 2, None) == INVALID
     # M = 0: a no-op
     assert lib.kt_tern_gemv(fake, 64, 256, fake, 256, fake, fake, 0, fake, 64, None, None) == 0
     # dbg with several matrices in one launch

@@ -80,13 +80,15 @@ def test_plan_matches_launches_27b_layer(linear, synth):
             assert np.array_equal(host(o).view(np.uint32), host(r).view(np.uint32)), k
 
 
-def test_plan_stage_reads_earlier_output(linear, synth):
-    """stage k + 1's group scales XS are stage k's output rows: the plan must give what launches in order give"""
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_plan_stage_reads_earlier_output(linear, synth, M):
+    """stage k + 1's group scales XS are stage k's output rows: the plan must give what launches in order give (one
+    token: the streamed executor; two and four: the register-ring executor)"""
     C = 2048
     NG = C // 128
     mats = [_mats(linear, synth, [("m%d" % i, NG, C)], 900 + i)["m%d" % i] for i in range(4)]
     big = _mats(linear, synth, [("big", 8192, C)], 990)["big"]      # keeps the other blocks busy between
-    x = synth.activations(1, C, 77, device="cuda")
+    x = synth.activations(M, C, 77, device="cuda")
     a0 = linear.quantize(x)
 
     def chain(XS0, outs):
@@ -97,19 +99,20 @@ def test_plan_stage_reads_earlier_output(linear, synth):
 
     # in order, one launch each
     L = linear.Linear({"m%d" % i: m for i, m in enumerate(mats)})
-    ref = [torch.empty((1, NG), device="cuda") for _ in range(4)]
+    ref = [torch.empty((M, NG), device="cuda") for _ in range(4)]
     acts = chain(a0.XS, ref)
     for i in range(4):
         L.gemv_q(["m%d" % i], acts[i], [ref[i]])
     # the plan: the same chain, a large unrelated product between each pair
-    outs = [torch.full((1, NG), float("nan"), device="cuda") for _ in range(4)]
-    ybig = [torch.empty((1, 8192), device="cuda") for _ in range(4)]
+    outs = [torch.full((M, NG), float("nan"), device="cuda") for _ in range(4)]
+    ybig = [torch.empty((M, 8192), device="cuda") for _ in range(4)]
     acts = chain(a0.XS, outs)
     stages = []
     for i in range(4):
         stages.append(([mats[i]], acts[i], [outs[i]]))
         stages.append(([big], a0, [ybig[i]]))
     plan = linear.Plan(stages)
+    say("plan chain M=%d: executor %d" % (M, plan.info.exec))
     for rep in range(3):
         for o in outs:
             o.fill_(float("nan"))

@@ -95,6 +95,110 @@ def test_gemv_token_invariance(kt, R, C):
         assert np.array_equal(host(Y), tree[:M]), M
 
 
+@pytest.mark.parametrize("R,C", [(5120, 5120), (1024, 5120), (17408, 5120), (5120, 17408), (256, 24576)])
+def test_gemv_27b_tokens(kt, R, C):
+    """the config 3 shapes at M = 1, 6, 8, 16, 32, against the oracle: every launch kind that serves them (the
+    v_dot4 kernels below 6 / 8 tokens, the matrix-core kernel with its three launch bounds: up to 4 K slices (C <=
+    8192), up to 10 (the 27B down projection, C = 17408: 9 slices) and above (C = 24576: 12 slices)). int32 group
+    values and fp32 outputs bit-exact against the oracle's decode tree, with and without the dbg output"""
+    lib, linear = kt
+    say("gemv 27B tokens", R, C)
+    W, dig, bc, dpm = upload(linear, R, C, 3 * R + C)
+    L = linear.Linear({"w": W})
+    X = rng(R + 11).normal(0, 1, (32, C)).astype(np.float32)
+    Xd = dev(X)
+    Q, XS, XA = orc.quant_q8(X)
+    acc = orc.tern_acc(bc, R, C, Q)
+    dq = dpm.view(np.float16).astype(np.float32)
+    tree = orc.out_lanes(acc, XS, dq, 8, 0, lib.kt_decode_kslices(C, 0))
+    assert max_rel(tree, orc.tern_out(acc, XS, dpm, R, C)) < TOL
+    for M in (1, 6, 8, 16, 32):
+        say("  M", M)
+        act = linear.quantize(Xd[:M])
+        Y = torch.empty((M, R), dtype=torch.float32, device="cuda")
+        dbg = torch.empty((M, R, C // 128), dtype=torch.int32, device="cuda")
+        L.gemv_q(["w"], act, [Y], dbg=dbg)
+        assert np.array_equal(host(dbg), acc[:M]), M
+        assert np.array_equal(host(Y), tree[:M]), M
+        Y2 = torch.full((M, R), float("nan"), dtype=torch.float32, device="cuda")
+        L.gemv_q(["w"], act, [Y2])
+        assert np.array_equal(host(Y2), tree[:M]), M
+
+
+@pytest.mark.parametrize("M", [4, 16])
+def test_gemv3_gate_up_27b(kt, M):
+    """gate and up [17408 x 5120] in one launch at 4 and 16 tokens: each matrix's rows equal its own launch's bits
+    (the multi-matrix tile offsets of both kernels), and 64 sampled rows of each equal the oracle's tree"""
+    lib, linear = kt
+    say("gemv3 gate/up", M)
+    R, C = 17408, 5120
+    mats = {n: upload(linear, R, C, s) for n, s in (("gate", 71), ("up", 72))}
+    L = linear.Linear({n: m[0] for n, m in mats.items()})
+    X = rng(M).normal(0, 1, (M, C)).astype(np.float32)
+    act = linear.quantize(dev(X))
+    outs = [torch.empty((M, R), dtype=torch.float32, device="cuda") for _ in range(2)]
+    L.gemv_q(["gate", "up"], act, outs)
+    Q, XS, XA = orc.quant_q8(X)
+    rows = np.sort(rng(5).choice(R, 64, replace=False))
+    for n, o in zip(("gate", "up"), outs):
+        one = torch.empty((M, R), dtype=torch.float32, device="cuda")
+        L.gemv_q([n], act, [one])
+        assert torch.equal(one, o), n
+        W, dig, bc, dpm = mats[n]
+        acc = orc.tern_acc(np.ascontiguousarray(bc[:, rows]), 64, C, Q)
+        dq = np.ascontiguousarray(dpm[:, rows]).view(np.float16).astype(np.float32)
+        assert np.array_equal(host(o)[:, rows], orc.out_lanes(acc, XS, dq, 8, 0, lib.kt_decode_kslices(C, 0))), n
+
+
+@pytest.mark.parametrize("R,M,sp", [(100, 1, 1), (5120, 1, 3), (5120, 5, 9), (333, 4, 17), (6144, 2, 16)])
+def test_tern_sum(kt, R, M, sp):
+    """kt_tern_sum (k_tc_sum, tc_hip.cu:271-279): the parts added in part order, bit-exact against the oracle; a
+    case where another order gives other bits is included (large and small parts of both signs)"""
+    lib, linear = kt
+    say("tern_sum", R, M, sp)
+    r = rng(R + sp)
+    P = (r.normal(0, 1, (M, sp, R)) * np.exp(r.normal(0, 6, (M, sp, R)))).astype(np.float32)
+    want = orc.tern_sum(P.reshape(-1), R, M, sp)
+    Pd = dev(P)
+    y = torch.full((M, R), float("nan"), dtype=torch.float32, device="cuda")
+    from kindi_amd import gpudrv
+    gpudrv.check(lib.kt_tern_sum(Pd.data_ptr(), y.data_ptr(), R, M, sp, None), "kt_tern_sum")
+    assert np.array_equal(host(y), want)
+    if sp >= 3:
+        rev = P[:, ::-1, :].astype(np.float32)
+        other = np.zeros((M, R), np.float32)
+        for p in range(sp):
+            other = (other + rev[:, p, :]).astype(np.float32)
+        assert not np.array_equal(other, want)          # the order is observable on these inputs
+
+
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("R,C", [(6144, 2048), (2048, 2048), (512, 2048), (2048, 6144)])
+def test_gemv_vs_kcpu(kt, R, C, per_row):
+    """the kcpu.c half of the parity bar (kcpu.c:72-135): the CPU engine's fp32 pair-table GEMV (the oracle's
+    restatement, pinned bit-exact to kcpu.c's own gemv; the reference build itself where it travelled) run on the
+    dequantized activations x^ = q XS equals the GPU product of the quantized row within 1e-3 relative (configs 0
+    and 1: per-row and per-group scales)"""
+    lib, linear = kt
+    say("gemv vs kcpu", R, C, per_row)
+    W, dig, bc, dpm = upload(linear, R, C, R + 3 * C)
+    L = linear.Linear({"w": W})
+    X = rng(C + R).normal(0, 1, (1, C)).astype(np.float32)
+    act = linear.quantize(dev(X), per_row=per_row)
+    Y = torch.empty((1, R), dtype=torch.float32, device="cuda")
+    L.gemv_q(["w"], act, [Y])
+    Q, XS, XA = orc.quant_q8(X, per_row)
+    xhat = (Q[0].astype(np.float32).reshape(-1, 128) * XS[0][:, None]).reshape(-1).astype(np.float32)
+    Pc = orc.paircodes_fast(bc, R, C)
+    S = orc.pair_scales(dpm, R, C)
+    y_cpu = orc.pair_gemv(Pc, S, R, C, xhat)
+    y = host(Y)[0]
+    assert max_rel(y, y_cpu) < TOL
+    assert max_rel(y, y_cpu) < 1e-5                     # in practice: only fp32 summation-order differences
+    if orc.ref_kcpu() is not None:
+        assert np.array_equal(orc.ref_gemv(Pc, S, R, C, xhat), y_cpu)
+
+
 def test_gemv3_qkv(kt):
     """q / k / v of the 2B layer in one launch (k_tc_mv3, spec.py:659-673), M = 4"""
     lib, linear = kt
@@ -167,9 +271,9 @@ def test_gemm_per_row(kt, R, C, M):
     assert np.array_equal(host(Y2), y)
 
 
-@pytest.mark.parametrize("R,C,M", [(12288, 4096, 512), (4096, 12288, 512)])
+@pytest.mark.parametrize("R,C,M", [(12288, 4096, 512), (4096, 12288, 512), (12288, 4096, 2048), (4096, 12288, 2048)])
 def test_gemm_config2_sampled(kt, R, C, M):
-    """config 2 shapes at M = 512: int32 group values and outputs of 96 sampled rows against the oracle, all rows
+    """config 2 shapes at M = 512 and 2048: int32 group values and outputs of 96 sampled rows against the oracle, all rows
     against the decode kernel's fp32 output for 16 tokens (the same int32 values, another summation tree)"""
     lib, linear = kt
     say("gemm config2", R, C, M)
@@ -179,14 +283,20 @@ def test_gemm_config2_sampled(kt, R, C, M):
     L = linear.Linear({"w": W})
     Xd = syn.activations(M, C, 22, device="cuda")
     act = linear.quantize(Xd, per_row=True)
-    Y = L.gemm("w", act)
     rows = np.sort(rng(1).choice(R, 96, replace=False))
+    dbg = torch.empty((M, R, C // 128), dtype=torch.int32, device="cuda")
+    Y = torch.empty((M, R), dtype=torch.float32, device="cuda")
+    L.gemm("w", act, Y=Y, dbg=dbg)
+    Y2 = L.gemm("w", act)                                                   # the instantiation without dbg
+    assert torch.equal(Y, Y2)
     bc = host(bc_t)[:, rows]
     dpm = host(dpm_t).view(np.uint16)[:, rows]
     X = host(Xd)
     Q, XS, XA = orc.quant_q8(X, per_row=True)
     assert np.array_equal(host(act.XQ), Q)
     acc = orc.tern_acc(np.ascontiguousarray(bc), len(rows), C, Q)
+    assert np.array_equal(host(dbg[:, torch.from_numpy(rows).cuda()]), acc), "int32 group values"
+    del dbg
     seq = orc.tern_out(acc, XS, np.ascontiguousarray(dpm), len(rows), C)
     want = orc.tern_out_rs(acc, XS, np.ascontiguousarray(dpm), len(rows), C)
     y = host(Y)
