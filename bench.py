@@ -244,9 +244,26 @@ def config4(torch, moe, synth, timer, steps, use_graph):
         touched = int((st["lists"][0] > 0).sum().item())
         per_expert = 2 * up.bytes_per_expert
         b = touched * per_expert + M * H * (4 + 1 + 4 / 32) + M * k * (F * (4 + 1 + 4 / 32) + H * 4) + M * H * 4
-        ms = timer.run(graphed(torch, lambda: layer.forward(x, lg, bufs), use_graph), steps, 2)
+        reps = 20 if M == 1 else 1           # back-to-back layers in one graph, as config 1
+
+        def rep(fn):
+            def f():
+                for _ in range(reps):
+                    fn()
+            return f
+        if M * k <= 64:
+            # kt_moe_decode (one token: two launches); the six separate launches beside it
+            work = layer.workspace(M)
+            ms = timer.run(graphed(torch, rep(lambda: layer.decode(x, lg, work)), use_graph), steps, 2) / reps
+            ms_sep = timer.run(graphed(torch, rep(lambda: layer.forward(x, lg, bufs)), use_graph), steps, 2) / reps
+            extra = {"launches": 2 if M == 1 else 4, "us_separate_launches": round(ms_sep * 1e3, 1)}
+        else:
+            ms = timer.run(graphed(torch, rep(lambda: layer.forward(x, lg, bufs)), use_graph), steps, 2) / reps
+            extra = {"launches": 6}
+        extra["note"] = "%d back-to-back layers per timed graph" % reps
         res["M=%d" % M] = {"experts_touched": touched, "us": round(ms * 1e3, 1), "GB/s": round(b / ms / 1e6, 1),
                            "bytes": int(b), "frac_hbm": round(b / ms / 1e6 / HBM_PEAK, 4)}
+        res["M=%d" % M].update(extra)
     return res
 
 

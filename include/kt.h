@@ -171,6 +171,23 @@ int kt_q8_grouped(const void* const* Wexp, int R, int C, int E, const int* cnt, 
 int kt_moe_combine(const float* yd, const float* ysh, const int* where, const float* gw, int M, int k, int cols,
                    float* x, void* stream);
 
+/* kt_moe_decode: a q8_0 MoE feed-forward at few tokens (M k <= 64), x [M][ldx] updated in place:
+     x[t] += sum_j gw[t][j] down_{e_j}(relu^2(up_{e_j}(x[t])))  (+ ysh[t], stride ldx, nullable)
+   with e_j, gw the softmax top-k of logits [M][E] (kt_moe_topk). One token (k <= 8, F <= 4096): two launches; the up
+   product routes for itself (every block computes the top-k) and quantizes x in its staging; the down product takes a
+   row group of every pick at once, makes relu^2 and the quantization of the intermediate in its staging and adds the
+   picks into x in selection order. Otherwise four: kt_moe_route's lists, the grouped up and down products with the
+   quantization in their staging, kt_moe_combine. Every intermediate has the bits of the separate launches
+   (kt_moe_route + kt_q8_quant + kt_q8_grouped + kt_q8_quant(act 1) + kt_q8_grouped + kt_moe_combine), so x does too.
+   Wup / Wdown: device tables of E kq8 buffers ([F x H] and [H x F]); H, F multiples of 32; ldx % 4 == 0, x 16-byte
+   aligned. work: a caller buffer of kt_moe_decode_workspace(M, k, E, H, F) bytes (0 = shape not taken), 256-byte
+   aligned; its contents need no initialisation, and two calls that overlap in time must not share it. Replaces the
+   decode half of Kindi's Lightning MoE layer: lt_router_topk (lightning.cu:414-468), lt_moe_lists (1318-1349),
+   lt_quant (70-88), lt_mv_q2 (154-195), lt_quant2 (470), lt_mv_q2_down (197-256) and lt_moe_combine (1352-1361). */
+size_t kt_moe_decode_workspace(int M, int k, int E, int H, int F);
+int kt_moe_decode(const void* const* Wup, const void* const* Wdown, int E, int H, int F, int k, const float* logits,
+                  int M, float* x, int ldx, const float* ysh, void* work, size_t work_bytes, void* stream);
+
 /* ---------------------------------------------------------------- fused input producers
    One launch makes a product's int8 input from the fp32 stream, with the reference's numbers bit for bit:
    kt_rmsfold_q8 replaces k_rmsfold_qT (tcf.cu:370-390; k_rmsfold kindi.cu:350-394): per token row n,

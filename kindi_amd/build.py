@@ -10,7 +10,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libkt_gfx950.so")
 SOURCES = ["kt_decode.hip", "kt_gemv.hip", "kt_mma.hip", "kt_plan.hip", "kt_splan.hip", "kt_prefill.hip",
-           "kt_moe.hip", "kt_fold.hip", "kt_api.hip"]
+           "kt_moe.hip", "kt_moe1.hip", "kt_fold.hip", "kt_api.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
          # packed fp32 (v_pk_*_f32) stays off: hand-written kernels here use scalar fp32 only

@@ -36,9 +36,15 @@ __global__ void k_tern_gemm_rs1(const uint32_t*, const uint16_t*, int, int, cons
                                 float*, uint16_t*, int, int32_t*);
 extern "C" __global__ void k_moe_topk(const float*, int, int, int*, float*);
 extern "C" __global__ void k_moe_sort(const int*, int, int, int*, int*, int*, int*, int*, int*, int);
-extern "C" __global__ void k_moe_combine(const float*, const float*, const int*, const float*, int, int, float*);
+extern "C" __global__ void k_moe_combine(const float*, const float*, const int*, const float*, int, int, float*, int);
 extern "C" __global__ void k_moe_route(const float*, int, int, int, int*, float*, int*, int*, int*, int*, int*, int*,
                                        const float*, int, int, int8_t*, int, float*, int);
+__global__ void k_moe1_up(const float*, int, int, const uint8_t* const*, const uint8_t* const*, int, int, const float*,
+                          float*, int*, float*, const uint8_t**, int);
+__global__ void k_moe1_down(const uint8_t* const*, const float*, int, int, int, const float*, float*, float*,
+                            const float*, int);
+size_t kt_moe1_up_lds(int KS);
+size_t kt_moe1_down_lds(int k, int KS);
 
 #define KT_INVALID ((int)hipErrorInvalidValue)
 #define KT_RS_ROWS 8192                /* per-row prefill on small blocks below this many rows */
@@ -142,6 +148,97 @@ static int kt_tern_gemv_n(int nmat, const void* const* W, const int* Rs, float* 
   a.ldxs = NG;
   a.M = M;
   return kt_launch_gemv<KT_FMT_TERN>(a, groups, XQ, XS, (const int*)XA, dbg, kt_stream(stream));
+}
+
+/* the MoE decode chain (kt_moe_decode): the workspace's sections, 256-byte aligned */
+struct KtMoeWork {
+  size_t ids, gw, cnt, off, xrow, where, act, nact, pd, u, yd, total;
+};
+static bool kt_moe_work(int M, int k, int E, int H, int F, KtMoeWork& w){
+  if(M <= 0 || k <= 0 || k > 16 || M > 64 || (long long)M * k > 64 || E <= 0 || E > 1024 || k > E || H <= 0 || F <= 0
+     || H % 32 || F % 32 || H > (1 << 20) || F > (1 << 20)) return false;
+  const size_t n = (size_t)M * k;
+  size_t o = 0;
+  auto put = [&](size_t bytes){ const size_t at = o; o += (bytes + 255) / 256 * 256; return at; };
+  w.ids = put(n * 4); w.gw = put(n * 4); w.cnt = put((size_t)E * 4); w.off = put((size_t)E * 4);
+  w.xrow = put(n * 4); w.where = put(n * 4); w.act = put((size_t)E * 4); w.nact = put(4); w.pd = put(n * 8);
+  w.u = put(n * F * 4); w.yd = put(n * H * 4);
+  w.total = o;
+  return true;
+}
+
+/* one grouped q8_0 product on the v_dot4 kernel, activations quantized in the staging from fp32 rows (FMT Q8X, Q8R) */
+template <int FMT>
+static int kt_grouped_xf(const KtGroupedArgs& a, int E, int nentries, int M, hipStream_t s){
+  const int ks = kt_kslices(a.NU);
+  const int ny = E < nentries ? E : nentries;
+  const int mt = M <= 1 ? 1 : 2;
+  const dim3 grid(kt_r8(a.R), ny), block(64 * ks);
+  const KtGemvArgs da = {};
+  const size_t lds1 = KtFlat<FMT, 1>::lds(ks), lds2 = KtFlat<FMT, 2>::lds(ks);
+  if(mt == 1)
+    hipLaunchKernelGGL((k_gemv_flat1<FMT, 1, false, true>), grid, block, lds1, s, da, a,
+                       (const int8_t*)nullptr, (const float*)nullptr, (const int*)nullptr, (int32_t*)nullptr, ks);
+  else
+    hipLaunchKernelGGL((k_gemv_flat<FMT, 2, false, true>), grid, block, lds2, s, da, a,
+                       (const int8_t*)nullptr, (const float*)nullptr, (const int*)nullptr, (int32_t*)nullptr, ks);
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
+static int kt_moe_decode_run(const void* const* Wup, const void* const* Wdown, int E, int H, int F, int k,
+                             const float* logits, int M, float* x, int ldx, const float* ysh, uint8_t* work,
+                             size_t work_bytes, hipStream_t s){
+  KtMoeWork w;
+  if(!kt_moe_work(M, k, E, H, F, w) || !Wup || !Wdown || !logits || !x || !work || ldx < H || ldx % 4
+     || !kt_al(x, 16) || !kt_al(work, 256) || work_bytes < w.total) return KT_INVALID;
+  int* ids = (int*)(work + w.ids); float* gw = (float*)(work + w.gw);
+  int* cnt = (int*)(work + w.cnt); int* off = (int*)(work + w.off); int* xrow = (int*)(work + w.xrow);
+  int* where = (int*)(work + w.where); int* act = (int*)(work + w.act); int* nact = (int*)(work + w.nact);
+  float* u = (float*)(work + w.u); float* yd = (float*)(work + w.yd);
+  const int ksu = kt_kslices(H / 32), ksd = kt_kslices(F / 32);
+  if(M == 1 && k <= 8 && ksu <= 16 && ksd * ((k + 1) / 2) <= 16 && kt_steps(F / 32) <= 2 * ksd
+     && kt_steps(H / 32) <= 2 * ksu){
+    /* one token: the up launch routes for itself; the down launch takes all k picks of a row group and combines */
+    const uint8_t* const* wu = (const uint8_t* const*)Wup;
+    const uint8_t* const* wd = (const uint8_t* const*)Wdown;
+    const uint8_t** pd = (const uint8_t**)(work + w.pd);
+    hipLaunchKernelGGL(k_moe1_up, dim3(kt_r8(F), k), dim3(64 * ((ksu + 1) / 2)), kt_moe1_up_lds(ksu), s, logits, E, k,
+                       wu, wd, F, H, (const float*)x, u, ids, gw, pd, ksu);
+    KT_LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_moe1_down, dim3(kt_r8(H)), dim3(64 * ksd * ((k + 1) / 2)), kt_moe1_down_lds(k, ksd), s,
+                       (const uint8_t* const*)pd, (const float*)gw, k, H, F, (const float*)u, yd, x, ysh, ksd);
+    KT_LAUNCH_CHECK();
+    return 0;
+  }
+  /* 1: router, top-k, lists */
+  hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(256), 0, s, logits, M, E, k, ids, gw, cnt, off, xrow, where, act, nact,
+                     (const float*)nullptr, 0, 0, (int8_t*)nullptr, 0, (float*)nullptr, 0);
+  KT_LAUNCH_CHECK();
+  const int n = M * k;
+  /* 2: up = W_e x[xrow[p]] per entry, x quantized in the staging */
+  KtGroupedArgs a = {};
+  a.wexp = (const uint8_t* const*)Wup;
+  a.R = F; a.C = H; a.NU = H / 32;
+  a.cnt = cnt; a.off = off; a.act = act; a.nact = nact; a.xrow = xrow;
+  a.ldy = F; a.nrows = M; a.y = u;
+  a.xf = x; a.ldxf = ldx;
+  int rc = kt_grouped_xf<KT_FMT_Q8X>(a, E, n, M, s);
+  if(rc) return rc;
+  /* 3: down = W_e relu^2(u[p]) per entry, quantized in the staging */
+  KtGroupedArgs b = {};
+  b.wexp = (const uint8_t* const*)Wdown;
+  b.R = H; b.C = F; b.NU = F / 32;
+  b.cnt = cnt; b.off = off; b.act = act; b.nact = nact; b.xrow = nullptr;
+  b.ldy = H; b.nrows = n; b.y = yd;
+  b.xf = u; b.ldxf = F;
+  rc = kt_grouped_xf<KT_FMT_Q8R>(b, E, n, M, s);
+  if(rc) return rc;
+  /* 4: x[t] += sum_j gw yd[where] (+ ysh) */
+  hipLaunchKernelGGL(k_moe_combine, dim3((H + 255) / 256, M), dim3(256), 0, s, (const float*)yd, ysh,
+                     (const int*)where, (const float*)gw, k, H, x, ldx);
+  KT_LAUNCH_CHECK();
+  return 0;
 }
 
 extern "C" {
@@ -521,9 +618,21 @@ int kt_moe_combine(const float* yd, const float* ysh, const int* where, const fl
   if(M == 0) return 0;
   if(!yd || !where || !gw || !x || M < 0 || M > 65535 || k <= 0 || k > 16 || cols <= 0) return KT_INVALID;
   hipLaunchKernelGGL(k_moe_combine, dim3((cols + 255) / 256, M), dim3(256), 0, kt_stream(stream), yd, ysh, where, gw,
-                     k, cols, x);
+                     k, cols, x, cols);
   KT_LAUNCH_CHECK();
   return 0;
+}
+
+size_t kt_moe_decode_workspace(int M, int k, int E, int H, int F){
+  KtMoeWork w;
+  return kt_moe_work(M, k, E, H, F, w) ? w.total : 0;
+}
+
+int kt_moe_decode(const void* const* Wup, const void* const* Wdown, int E, int H, int F, int k, const float* logits,
+                  int M, float* x, int ldx, const float* ysh, void* work, size_t work_bytes, void* stream){
+  if(M == 0) return 0;
+  return kt_moe_decode_run(Wup, Wdown, E, H, F, k, logits, M, x, ldx, ysh, (uint8_t*)work, work_bytes,
+                           kt_stream(stream));
 }
 
 /* ------------------------------------------------------------------ fused input producers (kt_fold.hip) */

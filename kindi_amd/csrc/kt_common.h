@@ -30,7 +30,10 @@
 #define KT_KL 8                       /* lanes along K per row = units per step */
 #define KT_MAXMAT 3                   /* matrices sharing one input in a launch (q/k/v, gate/up) */
 
-enum { KT_FMT_TERN = 0, KT_FMT_Q8 = 1 };
+/* KT_FMT_Q8X / KT_FMT_Q8R: q8_0 weights whose int8 activations are made in the product's own staging from fp32
+   rows (kt_q8_quant's numbers, per 32-column unit, so each wave quantizes exactly the units it reads); Q8R applies
+   relu^2 first (the MoE down projection's input) */
+enum { KT_FMT_TERN = 0, KT_FMT_Q8 = 1, KT_FMT_Q8X = 2, KT_FMT_Q8R = 3 };
 
 /* the one-round-trip decode product (kt_flat.h): slice length and LDS sizes */
 #ifndef KT_SL
@@ -153,6 +156,8 @@ struct KtGroupedArgs {
   const int* xrow;                    /* nullable: input row of list entry p (else p itself) */
   int ldq, ldd, ldy, nrows;           /* nrows: input rows (M with xrow, else the entries) */
   float* y;                           /* output rows [entries][ldy] */
+  const float* xf;                    /* Q8X / Q8R: the fp32 input rows [nrows][ldxf] (replace q / d) */
+  int ldxf, pad2;
 };
 
 /* the value of lane l ^ X (X = 1 .. 32) on the VALU, without the LDS crossbar: DPP quad permutes and mirrors inside a

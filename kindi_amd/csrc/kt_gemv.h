@@ -79,6 +79,29 @@ __device__ __forceinline__ void kt_pin(uint4* v, uint32_t* w){
   else if(N == 8) asm("" : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]), "+v"(q[4]), "+v"(q[5]), "+v"(q[6]), "+v"(q[7]), "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(w[4]), "+v"(w[5]), "+v"(w[6]), "+v"(w[7]), "+v"(w[8]), "+v"(w[9]), "+v"(w[10]), "+v"(w[11]), "+v"(w[12]), "+v"(w[13]), "+v"(w[14]), "+v"(w[15]));
 }
 
+/* kt_q8_quant's numbers for the 8 lanes of one 32-column unit (lane bits 0..2 = r: floats 4 r .. 4 r + 3 of the
+   unit): relu^2 first when RELU; amax by three VALU exchanges (exact in any order); q = rne(v 127 / amax) packed
+   little-endian; d = fp16(amax / 127) as f32 (llama.cpp's CPU q8_0 rounding, lt_quant2 lightning.cu:470) */
+template <bool RELU>
+__device__ __forceinline__ uint32_t kt_q8_unit_quant(const uint4 raw, float& d){
+  float v[4] = {__uint_as_float(raw.x), __uint_as_float(raw.y), __uint_as_float(raw.z), __uint_as_float(raw.w)};
+  float a = 0.0f;
+#pragma unroll
+  for(int i = 0; i < 4; ++i){
+    if(RELU){ v[i] = fmaxf(v[i], 0.0f); v[i] = v[i] * v[i]; }
+    a = fmaxf(a, fabsf(v[i]));
+  }
+  a = fmaxf(a, kf_xorf<1>(a));
+  a = fmaxf(a, kf_xorf<2>(a));
+  a = fmaxf(a, kf_xorf<4>(a));
+  const float id = a != 0.0f ? 127.0f / a : 0.0f;
+  uint32_t q = 0;
+#pragma unroll
+  for(int i = 0; i < 4; ++i) q |= (uint32_t)(uint8_t)(int8_t)__float2int_rn(v[i] * id) << (8 * i);
+  d = __half2float(__float2half_rn(a / 127.0f));
+  return q;
+}
+
 __device__ __forceinline__ void kt_wave_sync(){
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -91,6 +114,8 @@ __device__ __forceinline__ void kt_gemv_flat_body(const KtGemvArgs& a, const KtG
   extern __shared__ __attribute__((aligned(16))) uint8_t kt_lds[];
   using F = KtFlat<FMT, MT>;
   constexpr int UW = F::UW, UP = F::UP, SL = KT_SL;
+  constexpr bool XF = FMT == KT_FMT_Q8X || FMT == KT_FMT_Q8R;         /* activations quantized here from fp32 */
+  constexpr int WF = XF ? KT_FMT_Q8 : FMT;                           /* the weights' format */
   const int NU = GRP ? ga.NU : a.NU, S = kt_steps(NU);
   const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), r = lane & 7, c = lane >> 3;
   const int g = blockIdx.x;
@@ -168,22 +193,46 @@ __device__ __forceinline__ void kt_gemv_flat_body(const KtGemvArgs& a, const KtG
 #pragma unroll
         for(int t = 0; t < MT; ++t){
           const int pe = p0 + t0 + (t < nt ? t : 0), n = xrow ? xrow[pe] : pe;
-          sa[0][j][t] = __float_as_uint(xs[(long long)n * ldxs + uu]);
-          sa[1][j][t] = FMT == KT_FMT_TERN ? (uint32_t)xa[(long long)n * ldxs + uu] : 0u;
-          const int oc = o < nc * UW ? o : 0;
-          stg[j][t] = *(const uint4*)(xq + (long long)n * ldq + (long long)s * KT_KL * UW + oc);
+          if(XF){
+            /* 4 floats a lane: unit c = lane / 8 of the step, floats 4 r .. (lanes of a unit past a ragged step read
+               the step's first floats; that unit is never used) */
+            const int of = lane * 4, ofc = of < nc * 32 ? of : 0;
+            sa[0][j][t] = 0u;
+            sa[1][j][t] = 0u;
+            stg[j][t] = *(const uint4*)(ga.xf + (long long)n * ga.ldxf + (long long)s * KT_KL * 32 + ofc);
+          } else {
+            (void)uu;
+            sa[0][j][t] = __float_as_uint(xs[(long long)n * ldxs + uu]);
+            sa[1][j][t] = FMT == KT_FMT_TERN ? (uint32_t)xa[(long long)n * ldxs + uu] : 0u;
+            const int oc = o < nc * UW ? o : 0;
+            stg[j][t] = *(const uint4*)(xq + (long long)n * ldq + (long long)s * KT_KL * UW + oc);
+          }
         }
       }
       kt_pin<SL * MT>(&stg[0][0], &sa[0][0][0]);                                  /* every load above is issued before a write */
       /* unconditional writes: a slot of a unit, step or token that does not exist is never read; q8_0 rows are 256
          bytes a step, so lanes past them write the wave's dump slot */
-      const bool in = o < KT_KL * UW;
-      const int lo = (o / UW) * UP + o % UW;
+      if(XF){
+        /* the lane's 4 bytes of unit c at byte 4 r, and the unit's scale (every lane of the unit has it: the lanes
+           that use unit c are exactly these) */
 #pragma unroll
-      for(int j = 0; j < SL; ++j)
+        for(int j = 0; j < SL; ++j)
 #pragma unroll
-        for(int t = 0; t < MT; ++t)
-          *(uint4*)(xw + (in ? (t * SL + j) * KT_KL * UP + lo : F::XW - 16)) = stg[j][t];
+          for(int t = 0; t < MT; ++t){
+            float d;
+            const uint32_t q = kt_q8_unit_quant<FMT == KT_FMT_Q8R>(stg[j][t], d);
+            *(uint32_t*)(xw + ((t * SL + j) * KT_KL + c) * UP + 4 * r) = q;
+            sa[0][j][t] = __float_as_uint(d);
+          }
+      } else {
+        const bool in = o < KT_KL * UW;
+        const int lo = (o / UW) * UP + o % UW;
+#pragma unroll
+        for(int j = 0; j < SL; ++j)
+#pragma unroll
+          for(int t = 0; t < MT; ++t)
+            *(uint4*)(xw + (in ? (t * SL + j) * KT_KL * UP + lo : F::XW - 16)) = stg[j][t];
+      }
       kt_wave_sync();
 #pragma unroll
       for(int j = 0; j < SL; ++j){
@@ -194,7 +243,7 @@ __device__ __forceinline__ void kt_gemv_flat_body(const KtGemvArgs& a, const KtG
 #pragma unroll
           for(int t = 0; t < MT; ++t){
             if(t < nt){
-              int v = kt_unit_lds<FMT>(w[j].c0, w[j].c1, xw + ((t * SL + j) * KT_KL + (uok ? c : 0)) * UP) - (int)sa[1][j][t];
+              int v = kt_unit_lds<WF>(w[j].c0, w[j].c1, xw + ((t * SL + j) * KT_KL + (uok ? c : 0)) * UP) - (int)sa[1][j][t];
               v = uok ? v : 0;
               acc[t] = fmaf((float)v, FMT == KT_FMT_TERN ? __uint_as_float(sa[0][j][t]) * d : d * __uint_as_float(sa[0][j][t]), acc[t]);
               if(DBG && uok && row < R) dbg[((long long)(p0 + t0 + t) * R + row) * NU + u] = v;
@@ -217,7 +266,9 @@ __device__ __forceinline__ void kt_gemv_flat_body(const KtGemvArgs& a, const KtG
       for(int t = 0; t < MT; ++t){
         float v = red[t * 8 + r];
         for(int k = 1; k < KS; ++k) v += red[(k * MT + t) * 8 + r];
-        if(t < nt && row < R) yout[(long long)(p0 + t0 + t) * ldy + row] = v;
+        if(t < nt && row < R){
+          yout[(long long)(p0 + t0 + t) * ldy + row] = v;
+        }
       }
     }
     __syncthreads();

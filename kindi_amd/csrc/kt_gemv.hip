@@ -7,3 +7,6 @@
 KT_GINST2(k_gemv_flat1, 0, 1, false) KT_GINST2(k_gemv_flat, 0, 2, false) KT_GINST2(k_gemv_flat, 0, 4, false)
 KT_GINST2(k_gemv_flat1, 1, 1, false) KT_GINST2(k_gemv_flat, 1, 2, false) KT_GINST2(k_gemv_flat, 1, 4, false)
 KT_GINST2(k_gemv_flat1, 1, 1, true) KT_GINST2(k_gemv_flat, 1, 2, true) KT_GINST2(k_gemv_flat, 1, 4, true)
+/* q8_0 grouped products with their activations quantized in the staging (up: plain; down: relu^2 first) */
+KT_GINST(k_gemv_flat1, 2, 1, false, true) KT_GINST(k_gemv_flat, 2, 2, false, true)
+KT_GINST(k_gemv_flat1, 3, 1, false, true) KT_GINST(k_gemv_flat, 3, 2, false, true)

@@ -10,63 +10,11 @@
    (the grouped product itself, per active expert and its token list, is the decode product k_gemv_flat in its
    grouped mode, kt_gemv.h: the dense q8_0 product's lanes, arithmetic and summation tree; output row = entry)
      k_moe_route    k_moe_topk and k_moe_sort in one launch by one wave, for up to 64 entries.
-     k_moe_combine  x[t] += sum_j fmaf(gw[t k + j], yd[where[t k + j]], .) (+ ysh[t]).
+     k_moe_combine  x[t] += sum_j fmaf(gw[t k + j], yd[where[t k + j]], .) (+ ysh[t]); x and ysh rows ldx apart.
 */
 #include "kt_common.h"
+#include "kt_topk.h"
 
-
-/* the k largest of E <= 1024 logits by one wave, the logits in registers (lane l holds e = l + 64 i, loaded together,
-   clamped): k rounds of a wave arg-max (ties to the lower index, a chosen entry masked out) on the VALU exchanges,
-   branch-free (selects, not branches: the loads are one round trip and the rounds one straight chain). Pick j lands
-   in lane j, which writes ids[j] and the weight exp(l_j - l_max) / sum of the chosen (the sum in j order, as a
-   sequential loop over the picks). Returns lane j's pick (lanes >= k: the last one). */
-template <int NI>   /* logits a lane: E <= 64 NI */
-__device__ __forceinline__ int kt_topk_wave_n(const float* __restrict__ l, int E, int k, int* __restrict__ ids,
-                                              float* __restrict__ gw, int lane){
-  float v[NI];
-#pragma unroll
-  for(int i = 0; i < NI; ++i){
-    const int e = lane + 64 * i;
-    const float x = l[e < E ? e : E - 1];
-    v[i] = e < E ? x : -INFINITY;
-  }
-  unsigned used = 0u;
-  int mine = 0;
-  float myv = 0.0f;
-  for(int j = 0; j < k; ++j){                                      /* uniform */
-    float bv = -INFINITY;
-    int bi = 0x7FFFFFFF;
-#pragma unroll
-    for(int i = 0; i < NI; ++i){
-      const int e = lane + 64 * i;
-      const bool ok = e < E && !(used >> i & 1u) && (v[i] > bv || (v[i] == bv && e < bi));
-      bv = ok ? v[i] : bv;
-      bi = ok ? e : bi;
-    }
-#define KT_TOPK_STEP(X) { const float ov = kf_xorf<X>(bv); const int oi = kf_xor<X>(bi); \
-    const bool tk = ov > bv || (ov == bv && oi < bi); bv = tk ? ov : bv; bi = tk ? oi : bi; }
-    KT_TOPK_STEP(1) KT_TOPK_STEP(2) KT_TOPK_STEP(4) KT_TOPK_STEP(8) KT_TOPK_STEP(16) KT_TOPK_STEP(32)
-#undef KT_TOPK_STEP
-    bi = __builtin_amdgcn_readfirstlane(bi);
-    bv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(bv)));
-    used |= (bi & 63) == lane ? 1u << (bi >> 6) : 0u;
-    mine = lane == j ? bi : mine;
-    myv = lane == j ? bv : myv;
-  }
-  const float lmax = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(myv)));
-  const float p = expf(myv - lmax);
-  float sum = 0.0f;
-  for(int j = 0; j < k; ++j) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), j));
-  if(lane < k){ ids[lane] = mine; gw[lane] = p / sum; }
-  return mine;
-}
-/* the scan length by E (uniform): a lane scans only the logits it holds */
-__device__ __forceinline__ int kt_topk_wave(const float* __restrict__ l, int E, int k, int* __restrict__ ids,
-                                            float* __restrict__ gw, int lane){
-  if(E <= 128) return kt_topk_wave_n<2>(l, E, k, ids, gw, lane);
-  if(E <= 256) return kt_topk_wave_n<4>(l, E, k, ids, gw, lane);
-  return kt_topk_wave_n<16>(l, E, k, ids, gw, lane);
-}
 
 /* exclusive prefix sum over the wave's 64 lanes (6 lane shifts through ds_bpermute); *total = the sum */
 __device__ __forceinline__ int kt_wave_excl_scan(int v, int lane, int* total){
@@ -253,7 +201,7 @@ extern "C" __global__ void __launch_bounds__(256) k_moe_route(const float* __res
 }
 
 extern "C" __global__ void __launch_bounds__(256) k_moe_combine(const float* __restrict__ yd, const float* __restrict__ ysh,
-    const int* __restrict__ where, const float* __restrict__ gw, int k, int cols, float* __restrict__ x){
+    const int* __restrict__ where, const float* __restrict__ gw, int k, int cols, float* __restrict__ x, int ldx){
   /* grid (column blocks of 256, tokens): one column of one token a thread, so its k loads are in flight together;
      the pairs of the token read once a block */
   __shared__ int wp[16];
@@ -264,6 +212,6 @@ extern "C" __global__ void __launch_bounds__(256) k_moe_combine(const float* __r
   if(i < cols){
     float s = 0.0f;
     for(int j = 0; j < k; ++j) s = fmaf(gp[j], yd[(long long)wp[j] * cols + i], s);
-    x[(long long)t * cols + i] += ysh ? s + ysh[(long long)t * cols + i] : s;
+    x[(long long)t * ldx + i] += ysh ? s + ysh[(long long)t * ldx + i] : s;
   }
 }

@@ -56,6 +56,8 @@ SIGNATURES = [
     ("kt_rmsfold_q8", I, [P, I, P, I, I, P, P, I, I, I, P, I, P, I, P, I, P, I, P, P, P]),
     ("kt_fold_q8", I, [P, I, P, I, I, I, P, I, P, I, P, P, P]),
     ("kt_smfold_q8", I, [P, I, P, I, P, I, I, I, I, I, I, P, I, P, I, P, P, P]),
+    ("kt_moe_decode_workspace", S, [I, I, I, I, I]),
+    ("kt_moe_decode", I, [P, P, I, I, I, I, P, I, P, I, P, P, S, P]),
 ]
 
 _lib = [None]

@@ -159,6 +159,24 @@ class MoE(object):
         self.combine(b["yd"], lists[3], gw, x)
         return x, dict(ids=ids, gw=gw, lists=lists, **b)
 
+    def decode(self, x, logits, work=None, ysh=None):
+        """the whole layer at few tokens (M k <= 64) in three launches (kt_moe_decode): x fp32 [M, H] updated in place,
+        with the same bits as forward(); work: a uint8 device buffer of workspace(M) bytes (allocated when None)"""
+        M, H = x.shape
+        lib = gpudrv.load()
+        if work is None:
+            work = self.workspace(M)
+        rc = lib.kt_moe_decode(ptr(self.up.table), ptr(self.down.table), self.E, H, self.up.R, self.k, ptr(logits), M,
+                               ptr(x), x.stride(0), ptr(ysh), ptr(work), work.numel(), stream())
+        gpudrv.check(rc, "kt_moe_decode")
+        return x
+
+    def workspace(self, M):
+        n = gpudrv.load().kt_moe_decode_workspace(M, self.k, self.E, self.down.R, self.up.R)
+        if n == 0:
+            raise ValueError("kt_moe_decode takes M k <= 64 (M = %d, k = %d)" % (M, self.k))
+        return torch.empty(n, dtype=torch.uint8, device=self.device)
+
     def buffers(self, M):
         dev, H, F, n = self.device, self.down.R, self.up.R, M * self.k
         return dict(xq=torch.empty((M, H), dtype=torch.int8, device=dev),

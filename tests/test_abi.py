@@ -27,7 +27,7 @@ def lib():
 
 def test_exports_every_declared_symbol(lib):
     names = declared()
-    assert len(names) == 28
+    assert len(names) == 30
     for n in names:
         assert hasattr(lib, n), n
     from kindi_amd import gpudrv
@@ -151,3 +151,14 @@ def test_ptq1_validation(lib):
     assert lib.kt_tern_pack_ptq1(f, 100, 256, 0, 20, f, None) == INVALID      # a middle chunk of 20 rows
     assert lib.kt_tern_pack_ptq1(f, 100, 256, 96, 8, f, None) == INVALID      # past R
     assert lib.kt_tern_pack_ptq1(f, 100, 256, 0, 0, f, None) == 0             # nothing to do
+
+
+def test_moe_decode_validation(lib):
+    f = ctypes.c_void_p(1 << 20)
+    assert lib.kt_moe_decode_workspace(11, 6, 128, 2688, 1856) == 0           # M k > 64
+    assert lib.kt_moe_decode_workspace(1, 6, 128, 2680, 1856) == 0           # H % 32
+    n = lib.kt_moe_decode_workspace(1, 6, 128, 2688, 1856)
+    assert n > 0
+    assert lib.kt_moe_decode(f, f, 128, 2688, 1856, 6, f, 1, f, 2688, None, f, n - 1, None) == 1   # short workspace
+    assert lib.kt_moe_decode(f, f, 128, 2688, 1856, 6, f, 1, f, 2686, None, f, n, None) == 1       # ldx % 4
+    assert lib.kt_moe_decode(f, f, 128, 2688, 1856, 6, f, 0, f, 2688, None, f, n, None) == 0       # nothing to do

@@ -230,3 +230,45 @@ def test_combine_bit_exact(kt):
     xd = dev(x)
     layer.combine(dev(yd), dev(where), dev(gw), xd)
     assert np.array_equal(host(xd), orc.moe_combine(yd, None, where, gw, x))
+
+
+@pytest.mark.parametrize("E,H,F,M,k", [(128, 2688, 1856, 1, 6), (128, 2688, 1856, 4, 6), (128, 2688, 1856, 10, 6),
+                                       (8, 96, 64, 10, 6), (16, 160, 96, 64, 1), (4, 64, 32, 3, 4), (8, 128, 64, 1, 3),
+                                       (16, 96, 4096, 1, 8), (16, 96, 8192, 1, 2), (4, 64, 32, 1, 4), (64, 2688, 1856, 1, 1)])
+def test_moe_decode_chain(kt, E, H, F, M, k):
+    """kt_moe_decode (one token: two launches, the up product routing for itself and the down product combining a row
+    group of every pick; more tokens: route, up and down with the quantization in their staging, combine) gives x bit
+    for bit as the separate launches (forward: route + quant + grouped up + quant + grouped down + combine), with and
+    without the shared-expert rows, on a workspace full of garbage (it needs no initialisation), twice in a row;
+    ragged row groups (H = 96, 128: a last row group of a 32-row block), one pick a token, every expert active, k not a
+    register-set size (3), the widest down input the one-token chain takes (F = 4096) and one past it (F = 8192: the
+    four-launch chain)"""
+    lib, moe = kt
+    say("moe decode chain", E, H, F, M, k)
+    ups = moe.Q8Experts([q8_case(F, H, 3000 + e)[0] for e in range(E)], F, H)
+    downs = moe.Q8Experts([q8_case(H, F, 4000 + e)[0] for e in range(E)], H, F)
+    layer = moe.MoE(ups, downs, k)
+    x = rng(M + H).normal(0, 1, (M, H)).astype(np.float32)
+    lg = rng(M + E).normal(0, 1, (M, E)).astype(np.float32)
+    ysh = rng(7).normal(0, 1, (M, H)).astype(np.float32)
+    lgd = dev(lg)
+    want, st = layer.forward(dev(x), lgd)
+    want = host(want)
+    work = layer.workspace(M)
+    assert work.numel() == lib.kt_moe_decode_workspace(M, k, E, H, F) > 0
+    work.fill_(0xFF)
+    for rep in range(2):
+        xd = dev(x)
+        layer.decode(xd, lgd, work)
+        assert np.array_equal(host(xd).view(np.uint32), want.view(np.uint32)), rep
+    # the shared expert's rows: x += s + ysh, as kt_moe_combine with ysh
+    xs = dev(x)
+    layer.decode(xs, lgd, work, ysh=dev(ysh))
+    ref = dev(x)
+    layer.combine(st["yd"], st["lists"][3], st["gw"], ref, ysh=dev(ysh))
+    assert np.array_equal(host(xs).view(np.uint32), host(ref).view(np.uint32))
+    # the intermediates it stands for, against the oracle at the small shapes
+    if H <= 160:
+        ids, gw = orc.router_topk(lg, k)
+        assert np.array_equal(host(st["ids"]), ids)
+
