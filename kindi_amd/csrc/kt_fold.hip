@@ -274,9 +274,23 @@ template __global__ void k_fold_q8<2, 16, 16>(const KtFoldArgs);
 #define KF_FEW 32                     /* up to this many tokens, one HB block a chunk */
 
 /* host launcher (kt_api.hip validates the arguments) */
+static bool kf_overlap(const float* p, int ldp, const float* q, int ldq, int M, int C){
+  if(!p || !q) return false;
+  const uintptr_t p0 = (uintptr_t)p, p1 = p0 + ((size_t)(M - 1) * ldp + C) * 4;
+  const uintptr_t q0 = (uintptr_t)q, q1 = q0 + ((size_t)(M - 1) * ldq + C) * 4;
+  return p0 < q1 && q0 < p1;
+}
+
 hipError_t kt_fold_launch(int mode, const KtFoldArgs& a, int M, hipStream_t s){
   int cw = a.HB;
-  if(M > KF_FEW){
+  /* rmsfold over chunks of a row: every chunk's block reads the whole row (x and the parts, for the norm) while it
+     writes its own chunk of xw / xn / xo. When one of those outputs overlaps x or the parts, one block takes the row
+     (each thread writes only the columns it has read), so no block can overwrite what another has still to read. */
+  const int np = a.nparts > 0 ? a.nparts : 0;
+  const bool alias = mode == 0 && (kf_overlap(a.xw, a.ldxw, a.x, a.ldx, M, a.C) || kf_overlap(a.xn, a.ldxn, a.x, a.ldx, M, a.C)
+      || kf_overlap(a.xo, a.ldxo, a.x, a.ldx, M, a.C) || (np && (kf_overlap(a.xw, a.ldxw, a.r, a.ldr, M, np * a.C)
+      || kf_overlap(a.xn, a.ldxn, a.r, a.ldr, M, np * a.C) || kf_overlap(a.xo, a.ldxo, a.r, a.ldr, M, np * a.C))));
+  if(M > KF_FEW || alias){
     if(mode == 0) cw = a.C;
     else for(cw = (8192 / a.HB) * a.HB; cw > a.HB && a.C % cw; cw -= a.HB) {}
   }
