@@ -31,7 +31,8 @@ extern "C" {
 #endif
 
 int kt_version(void);
-/* hipSetDevice(device). gpudrv.py:83-85 (cuCtxSetCurrent) */
+/* hipSetDevice(device), and the device's address of the library's no-allocation workspace (kt_moe_decode_noalloc).
+   gpudrv.py:83-85 (cuCtxSetCurrent) */
 int kt_init(int device);
 const char* kt_error_string(int rc);
 
@@ -188,6 +189,17 @@ size_t kt_moe_decode_workspace(int M, int k, int E, int H, int F);
 int kt_moe_decode(const void* const* Wup, const void* const* Wdown, int E, int H, int F, int k, const float* logits,
                   int M, float* x, int ldx, const float* ysh, void* work, size_t work_bytes, void* stream);
 
+/* kt_moe_decode_noalloc: kt_moe_decode with its workspace in a device array of the library instead of a caller buffer,
+   for callers that cannot allocate device memory (code under graph capture, serving loops that forbid allocation).
+   No counterpart in the reference. It allocates nothing and frees nothing; the array (kt_moe_decode_noalloc_max()
+   bytes, 4 MiB) is held on every GPU the library runs on until the process ends, and its address on a device is
+   resolved by kt_init(device) or by the first call on the device. Shapes whose kt_moe_decode_workspace exceeds it
+   return hipErrorInvalidValue. Calls on one GPU share the array: calls that overlap in time on one GPU (other
+   streams, other threads) race. The same results as kt_moe_decode. */
+size_t kt_moe_decode_noalloc_max(void);
+int kt_moe_decode_noalloc(const void* const* Wup, const void* const* Wdown, int E, int H, int F, int k,
+                          const float* logits, int M, float* x, int ldx, const float* ysh, void* stream);
+
 /* ---------------------------------------------------------------- fused input producers
    One launch makes a product's int8 input from the fp32 stream, with the reference's numbers bit for bit:
    kt_rmsfold_q8 replaces k_rmsfold_qT (tcf.cu:370-390; k_rmsfold kindi.cu:350-394): per token row n,
@@ -200,7 +212,7 @@ int kt_moe_decode(const void* const* Wup, const void* const* Wdown, int E, int H
    fold = the unnormalised Walsh-Hadamard transform of each HB-column block times 1/sqrt(HB), HB in {512, 1024,
    4096}. C % HB == 0; rmsfold takes C <= 8192 (one block holds the row for the norm), fold / smfold any width up to
    2^20 (chunks of whole HB blocks). M <= 65535. xw (x + parts, only with nparts > 0), xn and xo are nullable;
-   xw may be x itself. The reference's two-row high-precision mode (hp) is not offered. */
+   xw, xn and xo may be x itself (with its row stride); they may not overlap x or the parts otherwise. The reference's two-row high-precision mode (hp) is not offered. */
 int kt_rmsfold_q8(const float* x, int ldx, const float* r, int ldr, int nparts, const float* w, const float* sg, int M,
                   int C, int HB, float* xw, int ldxw, float* xn, int ldxn, float* xo, int ldxo, int8_t* XQ, int ldq,
                   float* XS, int32_t* XA, void* stream);

@@ -5,6 +5,7 @@
 #include "kt_common.h"
 #include <vector>
 #include <algorithm>
+#include <mutex>
 #include "../../include/kt.h"
 #include "kt_fold.h"
 
@@ -241,11 +242,39 @@ static int kt_moe_decode_run(const void* const* Wup, const void* const* Wdown, i
   return 0;
 }
 
+/* the workspace of kt_moe_decode_noalloc: one array per GPU, held until the process ends. In host code the array's
+   name is not a device address; the address each device gives it is resolved once per device (kt_init, else the
+   first call on the device) with hipGetSymbolAddress and only that address is used. Calls on one GPU share it:
+   calls that overlap in time on one GPU race. */
+#define KT_SCRATCH_BYTES ((size_t)4 << 20)
+static __device__ __align__(256) uint8_t scratch[KT_SCRATCH_BYTES];
+#define KT_MAX_DEVICES 64
+static uint8_t* kt_scratch_ptr[KT_MAX_DEVICES];
+static std::mutex kt_scratch_mu;
+static int kt_scratch_resolve(int dev, uint8_t** out){
+  if(dev < 0 || dev >= KT_MAX_DEVICES) return KT_INVALID;
+  std::lock_guard<std::mutex> g(kt_scratch_mu);
+  if(!kt_scratch_ptr[dev]){
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if(e != hipSuccess) return (int)e;
+    if(!p) return KT_INVALID;
+    kt_scratch_ptr[dev] = (uint8_t*)p;
+  }
+  *out = kt_scratch_ptr[dev];
+  return 0;
+}
+
 extern "C" {
 
 int kt_version(void){ return KT_VERSION; }
 
-int kt_init(int device){ return (int)hipSetDevice(device); }
+int kt_init(int device){
+  const hipError_t e = hipSetDevice(device);
+  if(e != hipSuccess) return (int)e;
+  uint8_t* p;
+  return kt_scratch_resolve(device, &p);
+}
 
 const char* kt_error_string(int rc){ return hipGetErrorString((hipError_t)rc); }
 
@@ -633,6 +662,23 @@ int kt_moe_decode(const void* const* Wup, const void* const* Wdown, int E, int H
   if(M == 0) return 0;
   return kt_moe_decode_run(Wup, Wdown, E, H, F, k, logits, M, x, ldx, ysh, (uint8_t*)work, work_bytes,
                            kt_stream(stream));
+}
+
+size_t kt_moe_decode_noalloc_max(void){ return KT_SCRATCH_BYTES; }
+
+int kt_moe_decode_noalloc(const void* const* Wup, const void* const* Wdown, int E, int H, int F, int k,
+                          const float* logits, int M, float* x, int ldx, const float* ysh, void* stream){
+  if(M == 0) return 0;
+  KtMoeWork w;
+  if(!kt_moe_work(M, k, E, H, F, w)) return KT_INVALID;
+  if(w.total > KT_SCRATCH_BYTES) return KT_INVALID;               /* beyond the static workspace */
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  if(e != hipSuccess) return (int)e;
+  uint8_t* p = nullptr;
+  const int rc = kt_scratch_resolve(dev, &p);
+  if(rc) return rc;
+  return kt_moe_decode_run(Wup, Wdown, E, H, F, k, logits, M, x, ldx, ysh, p, KT_SCRATCH_BYTES, kt_stream(stream));
 }
 
 /* ------------------------------------------------------------------ fused input producers (kt_fold.hip) */

@@ -58,6 +58,8 @@ SIGNATURES = [
     ("kt_smfold_q8", I, [P, I, P, I, P, I, I, I, I, I, I, P, I, P, I, P, P, P]),
     ("kt_moe_decode_workspace", S, [I, I, I, I, I]),
     ("kt_moe_decode", I, [P, P, I, I, I, I, P, I, P, I, P, P, S, P]),
+    ("kt_moe_decode_noalloc_max", S, []),
+    ("kt_moe_decode_noalloc", I, [P, P, I, I, I, I, P, I, P, I, P, P]),
 ]
 
 _lib = [None]
