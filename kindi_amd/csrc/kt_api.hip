@@ -15,6 +15,8 @@ __global__ void k_gemv_flat(const KtGemvArgs, const KtGroupedArgs, const int8_t*
 template <int FMT, int MT, bool DBG, bool GRP>
 __global__ void k_gemv_flat1(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, const int*, int32_t*,
                              int);
+template <bool DBG>
+__global__ void k_gemv_pair(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
 template <int NT, bool DBG, int LB>
 __global__ void k_gemv_mma(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
 template <bool GRP, bool DBG>
@@ -48,6 +50,9 @@ size_t kt_moe1_up_lds(int KS);
 size_t kt_moe1_down_lds(int k, int KS);
 
 #define KT_INVALID ((int)hipErrorInvalidValue)
+#ifndef KT_PAIR_WAVES
+#define KT_PAIR_WAVES 6144             /* one-token grids of more waves take two row groups a block (k_gemv_pair) */
+#endif
 #define KT_RS_ROWS 8192                /* per-row prefill on small blocks below this many rows */
 #define KT_LAUNCH_CHECK() do { const hipError_t _e = hipGetLastError(); if(_e != hipSuccess) return (int)_e; } while(0)
 
@@ -111,6 +116,17 @@ static int kt_launch_gemv(const KtGemvArgs& a, int ngroups, const int8_t* xq, co
                           int32_t* dbg, hipStream_t s){
   if(FMT == KT_FMT_TERN && kt_use_mma(a)) return kt_launch_mma(a, xq, xs, dbg, s);
   const int ks = kt_kslices(a.NU);
+  bool even = true;
+  for(int i = 0; i < a.nmat; ++i) even = even && kt_r8(a.mat[i].R) % 2 == 0;
+  if(FMT == KT_FMT_TERN && a.M == 1 && even && (long long)ngroups * ks > KT_PAIR_WAVES && kt_steps(a.NU) <= KT_SL * ks){
+    /* one token on a grid too large for the wave slots: two row groups a block, one round of blocks */
+    const dim3 grid(ngroups / 2), block(64 * ks);
+    const size_t lds = (size_t)ks * KtFlat<KT_FMT_TERN, 1>::XW + (size_t)ks * 2 * 8 * 4;
+    if(dbg) hipLaunchKernelGGL((k_gemv_pair<true>), grid, block, lds, s, a, xq, xs, xa, dbg, ks);
+    else hipLaunchKernelGGL((k_gemv_pair<false>), grid, block, lds, s, a, xq, xs, xa, dbg, ks);
+    KT_LAUNCH_CHECK();
+    return 0;
+  }
   int mt = a.M <= 1 ? 1 : a.M <= 2 ? 2 : 4;
   while(mt > 1 && (mt == 4 ? KtFlat<FMT, 4>::lds(ks) : KtFlat<FMT, 2>::lds(ks)) > 65536) mt >>= 1;
   const dim3 grid(ngroups), block(64 * ks);

@@ -13,6 +13,15 @@
 #pragma once
 #include "kt_common.h"
 
+#ifdef KT_TRACE                        /* a timeline build: per-block s_memrealtime stamps, one buffer per source file */
+static __device__ unsigned long long kt_trace_buf[1 << 16];
+static __device__ int kt_trace_on;
+#define KT_GTS(k) do { if(kt_trace_on && threadIdx.x == 0 && blockIdx.x < 8192) \
+    kt_trace_buf[blockIdx.x * 4 + (k)] = __builtin_amdgcn_s_memrealtime(); } while(0)
+#else
+#define KT_GTS(k) do {} while(0)
+#endif
+
 /* the fixed xor butterfly over the 8 k-lanes of a row (lane bits 3..5): every lane ends with the same value (each
    adds the same pair); the exchanges run on the VALU (kf_xor) */
 __device__ __forceinline__ float kt_row_sum(float v){
@@ -102,6 +111,18 @@ __device__ __forceinline__ uint32_t kt_q8_unit_quant(const uint4 raw, float& d){
   return q;
 }
 
+/* the slice sums p[0], p[st], p[2 st], ... (KS <= 16 of them) added left to right, every LDS read issued before the
+   first add (a select, not a +0, past the last slice keeps the sum exact) */
+__device__ __forceinline__ float kt_slice_sum(const float* p, int st, int KS){
+  float t[KT_KSMAX];
+#pragma unroll
+  for(int q = 0; q < KT_KSMAX; ++q) t[q] = p[(q < KS ? q : 0) * st];
+  float v = t[0];
+#pragma unroll
+  for(int q = 1; q < KT_KSMAX; ++q) v = q < KS ? v + t[q] : v;
+  return v;
+}
+
 __device__ __forceinline__ void kt_wave_sync(){
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -119,6 +140,7 @@ __device__ __forceinline__ void kt_gemv_flat_body(const KtGemvArgs& a, const KtG
   const int NU = GRP ? ga.NU : a.NU, S = kt_steps(NU);
   const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), r = lane & 7, c = lane >> 3;
   const int g = blockIdx.x;
+  KT_GTS(0);
   /* the job of this block: a matrix's row group and its token rows. Dense: row group g of the launch's matrices,
      tokens 0 .. M - 1, output row t. Grouped (MoE): row group g of active expert act[blockIdx.y], the tokens of its
      list (entries off .. off + cnt - 1, input row xrow[p] or p), output row = entry p. */
@@ -210,6 +232,13 @@ __device__ __forceinline__ void kt_gemv_flat_body(const KtGemvArgs& a, const KtG
         }
       }
       kt_pin<SL * MT>(&stg[0][0], &sa[0][0][0]);                                  /* every load above is issued before a write */
+#ifdef KT_TRACE
+      { uint32_t sink = 0;
+#pragma unroll
+        for(int jj = 0; jj < SL; ++jj) sink ^= w[jj].c0.x ^ w[jj].c1.y;
+        if(sink == 0x12345u && threadIdx.x == 1) kt_trace_buf[65535] = 1; }
+      KT_GTS(1);
+#endif
       /* unconditional writes: a slot of a unit, step or token that does not exist is never read; q8_0 rows are 256
          bytes a step, so lanes past them write the wave's dump slot */
       if(XF){
@@ -253,6 +282,7 @@ __device__ __forceinline__ void kt_gemv_flat_body(const KtGemvArgs& a, const KtG
       }
       kt_wave_sync();                                                /* the staging is rewritten next */
     }
+    KT_GTS(2);
     float y[MT];
 #pragma unroll
     for(int t = 0; t < MT; ++t) y[t] = kt_row_sum(acc[t]);
@@ -273,6 +303,7 @@ __device__ __forceinline__ void kt_gemv_flat_body(const KtGemvArgs& a, const KtG
     }
     __syncthreads();
   }
+  KT_GTS(3);
 }
 
 /* one token a chunk: held to 64 VGPRs (8 waves a SIMD), so three 9-wave blocks fit a CU and the widest products

@@ -10,3 +10,12 @@ KT_GINST2(k_gemv_flat1, 1, 1, true) KT_GINST2(k_gemv_flat, 1, 2, true) KT_GINST2
 /* q8_0 grouped products with their activations quantized in the staging (up: plain; down: relu^2 first) */
 KT_GINST(k_gemv_flat1, 2, 1, false, true) KT_GINST(k_gemv_flat, 2, 2, false, true)
 KT_GINST(k_gemv_flat1, 3, 1, false, true) KT_GINST(k_gemv_flat, 3, 2, false, true)
+
+#ifdef KT_TRACE
+extern "C" int kt_trace_gemv_read(void* host){
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(kt_trace_buf), sizeof(kt_trace_buf), 0, hipMemcpyDeviceToHost);
+}
+extern "C" int kt_trace_gemv_enable(int on){
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(kt_trace_on), &on, sizeof(int), 0, hipMemcpyHostToDevice);
+}
+#endif

@@ -1,0 +1,142 @@
+/* kt_gemv2.hip - the one-token ternary decode product with two row groups a block (k_gemv_pair), for launches whose
+   one-row-group grid (k_gemv_flat1) would not fit the GPU's wave slots at once (the 27B-class gate/up pair: 4352 row
+   groups x 3 K slices = 13056 waves against 8192 slots, so a second round of blocks would issue its loads only after
+   the first round has finished).
+
+   A block takes row groups 2 b and 2 b + 1 of the launch's matrices (every matrix has an even number of row groups); wave ks takes K slice ks of both, issues the code
+   and scale loads of both and the activation row of the slice at once (one memory round trip), stages the
+   activations in LDS once for both, and computes each row group exactly as k_gemv_flat1 does: lane c chains
+   fmaf((float)(v - XA), XS d, .) over its units of the slice, the xor butterfly adds the 8 lanes of a row, and the
+   slice sums are added in slice order. So every row has the same bits as on k_gemv_flat1 (the tree depends on C
+   only). */
+#include "kt_gemv.h"
+
+/* kt_unit_lds for two row groups' code words against one unit's staged activations: each half's four activation
+   chunks are read once and feed both (integer sums: the same values as two kt_unit_lds calls), one half at a time so
+   that only four chunks are live */
+__device__ __forceinline__ void kt_unit2_lds(const uint4 a0c, const uint4 a1c, const uint4 b0c, const uint4 b1c,
+                                             const uint8_t* xrow, int (&v)[2]){
+  const uint4* q = (const uint4*)xrow;
+  int s0[3] = {0, 0, 0}, s1[3] = {0, 0, 0};
+#pragma unroll
+  for(int h = 0; h < 2; ++h){
+    const uint4 ca = h ? a1c : a0c, cb = h ? b1c : b0c;
+    const uint32_t wa[4] = {ca.x, ca.y, ca.z, ca.w}, wb[4] = {cb.x, cb.y, cb.z, cb.w};
+    uint4 x[4];
+#pragma unroll
+    for(int j = 0; j < 4; ++j) x[j] = q[4 * h + j];
+#pragma unroll
+    for(int j = 0; j < 4; ++j){
+      s0[0] = kt_dot4((int)(wa[j] & 0x03030303u), (int)x[j].x, s0[0]);
+      s0[1] = kt_dot4((int)(wa[j] & 0x0C0C0C0Cu), (int)x[j].y, s0[1]);
+      s0[2] = kt_dot4((int)(wa[j] & 0x30303030u), (int)x[j].z, s0[2]);
+      s0[0] = kt_dot4((int)((wa[j] >> 6) & 0x03030303u), (int)x[j].w, s0[0]);
+      s1[0] = kt_dot4((int)(wb[j] & 0x03030303u), (int)x[j].x, s1[0]);
+      s1[1] = kt_dot4((int)(wb[j] & 0x0C0C0C0Cu), (int)x[j].y, s1[1]);
+      s1[2] = kt_dot4((int)(wb[j] & 0x30303030u), (int)x[j].z, s1[2]);
+      s1[0] = kt_dot4((int)((wb[j] >> 6) & 0x03030303u), (int)x[j].w, s1[0]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  v[0] = s0[0] + (s0[1] >> 2) + (s0[2] >> 4);
+  v[1] = s1[0] + (s1[1] >> 2) + (s1[2] >> 4);
+}
+
+/* 7 waves a SIMD (72 VGPRs): 7168 wave slots, enough for the pair grid of the 27B gate/up launch (6528 waves) */
+template <bool DBG>
+__global__ void __launch_bounds__(64 * KT_KSMAX) __attribute__((amdgpu_waves_per_eu(7)))
+k_gemv_pair(const KtGemvArgs a, const int8_t* __restrict__ xq, const float* __restrict__ xs,
+            const int* __restrict__ xa, int32_t* __restrict__ dbg, int KS){
+  extern __shared__ __attribute__((aligned(16))) uint8_t kt_lds[];
+  using F = KtFlat<KT_FMT_TERN, 1>;
+  constexpr int UW = F::UW, UP = F::UP, SL = KT_SL;
+  const int NU = a.NU, S = kt_steps(NU);
+  const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), r = lane & 7, c = lane >> 3;
+  const int s_lo = ks * S / KS, ns = (ks + 1) * S / KS - s_lo;      /* 1 or 2 steps (the launcher checks) */
+  uint8_t* xw = kt_lds + (size_t)ks * F::XW;                         /* [SL][8][UP] */
+  float* red = (float*)(kt_lds + (size_t)KS * F::XW);                /* [KS][2][8] */
+
+  /* both row groups are in one matrix (every matrix of the launch has an even number of row groups: the launcher
+     checks), so the second one's loads are the first one's offsets from bases one row group further */
+  const int g = 2 * blockIdx.x;
+  int mi = 0;
+  if(a.nmat > 1 && g >= a.mat[1].rg0) mi = 1;
+  if(a.nmat > 2 && g >= a.mat[2].rg0) mi = 2;
+  const KtMat& m = a.mat[mi];
+  const int rg0 = g - m.rg0, R = m.R;
+  const uint4* wb0 = (const uint4*)m.codes;
+  const uint16_t* sb0 = m.scales;
+  const uint4* wb1 = wb0 + (long long)NU * 16;
+  const uint16_t* sb1 = sb0 + (long long)NU * 8;
+  float* yo = m.y;
+  KtStep w[2][SL];
+  unsigned o0[SL], o1[SL], os[SL];
+#pragma unroll
+  for(int j = 0; j < SL; ++j){
+    const int s = s_lo + j, u = s * KT_KL + c;
+    const bool ok = j < ns && u < NU;
+    o0[j] = ok ? (unsigned)kt_widx(NU, rg0, s, 0, c, r) : 0u;
+    o1[j] = ok ? (unsigned)kt_widx(NU, rg0, s, 1, c, r) : 0u;
+    os[j] = ok ? (unsigned)kt_sidx(NU, rg0, u, r) : 0u;
+  }
+#pragma unroll
+  for(int j = 0; j < SL; ++j){
+    w[0][j].c0 = kt_ldnt(wb0 + o0[j]);
+    w[0][j].c1 = kt_ldnt(wb0 + o1[j]);
+    w[0][j].hs = sb0[os[j]];
+    w[1][j].c0 = kt_ldnt(wb1 + o0[j]);
+    w[1][j].c1 = kt_ldnt(wb1 + o1[j]);
+    w[1][j].hs = sb1[os[j]];
+  }
+  /* the slice's activations (token 0): each lane's 16 bytes of a step's row, its unit's scale and sum */
+  uint32_t sa[2][SL];
+  uint4 stg[SL];
+  const int o = lane * 16;
+#pragma unroll
+  for(int j = 0; j < SL; ++j){
+    const int s = s_lo + (j < ns ? j : 0), u = s * KT_KL + c, uu = (j < ns && u < NU) ? u : 0;
+    const int nc = NU - s * KT_KL < KT_KL ? NU - s * KT_KL : KT_KL;
+    sa[0][j] = __float_as_uint(xs[uu]);
+    sa[1][j] = (uint32_t)xa[uu];
+    const int oc = o < nc * UW ? o : 0;
+    stg[j] = *(const uint4*)(xq + (long long)s * KT_KL * UW + oc);
+  }
+  kt_pin<SL>(&stg[0], &sa[0][0]);
+#pragma unroll
+  for(int j = 0; j < SL; ++j) *(uint4*)(xw + j * KT_KL * UP + (o / UW) * UP + o % UW) = stg[j];
+  kt_wave_sync();
+  float acc[2] = {0.0f, 0.0f};
+#pragma unroll
+  for(int j = 0; j < SL; ++j){
+    const int u = (s_lo + j) * KT_KL + c;
+    if(j < ns){                                                      /* wave-uniform */
+      const bool uok = u < NU;
+      int vv[2];
+      kt_unit2_lds(w[0][j].c0, w[0][j].c1, w[1][j].c0, w[1][j].c1, xw + (j * KT_KL + (uok ? c : 0)) * UP, vv);
+#pragma unroll
+      for(int q = 0; q < 2; ++q){
+        const float d = uok ? kt_h2f(w[q][j].hs) : 0.0f;
+        const int v = uok ? vv[q] - (int)sa[1][j] : 0;
+        acc[q] = fmaf((float)v, __uint_as_float(sa[0][j]) * d, acc[q]);
+        const int row = (rg0 + q) * KT_RG + r;
+        if(DBG && uok && row < R) dbg[(long long)row * NU + u] = v;
+      }
+    }
+  }
+#pragma unroll
+  for(int q = 0; q < 2; ++q){
+    const float y = kt_row_sum(acc[q]);
+    if(c == q) red[(ks * 2 + q) * 8 + r] = y;
+  }
+  __syncthreads();
+  /* lanes 8 q + r of wave 0: row r of row group q, the slice sums in slice order */
+  if(ks == 0 && c < 2){
+    const int q = c, row = (rg0 + q) * KT_RG + r;
+    float v = red[q * 8 + r];
+    for(int k = 1; k < KS; ++k) v += red[(k * 2 + q) * 8 + r];
+    if(row < R) yo[row] = v;
+  }
+}
+
+template __global__ void k_gemv_pair<false>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
+template __global__ void k_gemv_pair<true>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);

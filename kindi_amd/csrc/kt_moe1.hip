@@ -23,7 +23,6 @@
 #define KM1_KMAX 8                     /* picks a token in this chain */
 #define KM1_UP 48                      /* a staged 32-byte unit and its pad (LDS) */
 #ifdef KT_TRACE                        /* a timeline build: per-block s_memrealtime stamps, read by kt_trace_read */
-__device__ unsigned long long kt_trace_buf[1 << 16];
 #define KT_TS(slot) do { if(threadIdx.x == 0) kt_trace_buf[(slot)] = __builtin_amdgcn_s_memrealtime(); } while(0)
 extern "C" int kt_trace_read(void* host){
   return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(kt_trace_buf), sizeof(kt_trace_buf), 0, hipMemcpyDeviceToHost);
@@ -96,18 +95,6 @@ __device__ __forceinline__ void km1_tasks(const uint8_t* const (&base)[T], const
   }
 }
 
-/* a row's slice sums p[0], p[st], p[2 st], ... (KS of them, KS <= 16) added left to right, every LDS read issued
-   before the first add (a select keeps the sum exact: no +0 is added past the last slice) */
-__device__ __forceinline__ float km1_slice_sum(const float* red, int st, int r, int KS){
-  float t[KT_KSMAX];
-#pragma unroll
-  for(int q = 0; q < KT_KSMAX; ++q) t[q] = red[(q < KS ? q : 0) * st + r];
-  float v = t[0];
-#pragma unroll
-  for(int q = 1; q < KT_KSMAX; ++q) v = q < KS ? v + t[q] : v;
-  return v;
-}
-
 __global__ void __launch_bounds__(64 * KT_KSMAX / 2) __attribute__((amdgpu_waves_per_eu(4)))
 k_moe1_up(const float* __restrict__ logits, int E, int k, const uint8_t* const* __restrict__ wup,
           const uint8_t* const* __restrict__ wdown, int R, int C, const float* __restrict__ x, float* __restrict__ u,
@@ -159,7 +146,7 @@ k_moe1_up(const float* __restrict__ logits, int E, int k, const uint8_t* const* 
   }
   __syncthreads();
   const int row = rg * KT_RG + r;
-  if(wv == 0 && c == 0 && row < R) u[(long long)j * R + row] = km1_slice_sum(red, 8, r, KS);
+  if(wv == 0 && c == 0 && row < R) u[(long long)j * R + row] = kt_slice_sum(red + r, 8, KS);
   KT_TS((j * gridDim.x + rg) * 4 + 3);
 }
 
@@ -198,7 +185,7 @@ k_moe1_down(const uint8_t* const* __restrict__ pdown, const float* __restrict__ 
   if(wv == 0){
     /* lane 8 j + r: pick j's row r, its slice sums in slice order; then lane r adds the picks in selection order */
     const int jj = lane >> 3;
-    const float v = km1_slice_sum(red + jj * 8, KM1_KMAX * 8, r, KS);
+    const float v = kt_slice_sum(red + jj * 8 + r, KM1_KMAX * 8, KS);
     if(jj < k && row < R) yd[(long long)jj * R + row] = v;
     float vj[KM1_KMAX];
 #pragma unroll

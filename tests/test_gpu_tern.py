@@ -125,10 +125,11 @@ def test_gemv_27b_tokens(kt, R, C):
         assert np.array_equal(host(Y2), tree[:M]), M
 
 
-@pytest.mark.parametrize("M", [4, 16])
+@pytest.mark.parametrize("M", [1, 4, 16])
 def test_gemv3_gate_up_27b(kt, M):
-    """gate and up [17408 x 5120] in one launch at 4 and 16 tokens: each matrix's rows equal its own launch's bits
-    (the multi-matrix tile offsets of both kernels), and 64 sampled rows of each equal the oracle's tree"""
+    """gate and up [17408 x 5120] in one launch at 1, 4 and 16 tokens (one token: two row groups a block): each
+    matrix's rows equal its own launch's bits (the multi-matrix offsets of every kernel), and 64 sampled rows of each
+    equal the oracle's tree"""
     lib, linear = kt
     say("gemv3 gate/up", M)
     R, C = 17408, 5120
