@@ -94,12 +94,10 @@ static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, int32_
   for(int i = 0; i < a.nmat; ++i){ a.mat[i].pad = tiles; tiles += (kt_r8(a.mat[i].R) + 3) / 4; }
   const dim3 grid(tiles, (a.M + 15) / 16), block(64 * ks);
   const size_t lds = (size_t)ks * 16 * 32 * 4 + (size_t)ks * 256 * 4;        /* slice sums, XS */
-  /* fewer waves a block leave each more registers, so the activation loads run further ahead (4 units up to 4
-     slices, C <= 8192; 2 up to 10 slices) */
-  if(ks <= 4){
-    if(dbg) hipLaunchKernelGGL((k_gemv_mma<16, true, 256>), grid, block, lds, s, a, xq, xs, dbg, ks);
-    else hipLaunchKernelGGL((k_gemv_mma<16, false, 256>), grid, block, lds, s, a, xq, xs, dbg, ks);
-  } else if(ks <= 10){
+  /* the 640-thread bound (159 VGPRs: 3 waves a SIMD, activations 2 units ahead) up to 10 slices, also for the
+     narrow products (measured on MI355X: 27B-class step at 16 tokens 4.25 -> 4.10 ms, 2B-class layer at 8 tokens
+     28.1 -> 26.6 us against the 256-thread bound's deeper prefetch at 2 waves a SIMD) */
+  if(ks <= 10){
     if(dbg) hipLaunchKernelGGL((k_gemv_mma<16, true, 640>), grid, block, lds, s, a, xq, xs, dbg, ks);
     else hipLaunchKernelGGL((k_gemv_mma<16, false, 640>), grid, block, lds, s, a, xq, xs, dbg, ks);
   } else {

@@ -42,6 +42,7 @@ __global__ void __launch_bounds__(LB) k_gemv_mma(const KtGemvArgs a, const int8_
   const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = lane >> 5, lr = lane & 31;
   const int tile = blockIdx.x, t0 = blockIdx.y * KM_TOK;
+  KT_GTS(0);
   int mi = 0;
   if(a.nmat > 1 && tile >= a.mat[1].pad) mi = 1;
   if(a.nmat > 2 && tile >= a.mat[2].pad) mi = 2;
@@ -104,6 +105,7 @@ __global__ void __launch_bounds__(LB) k_gemv_mma(const KtGemvArgs a, const int8_
 #pragma unroll
   for(int q = 0; q < 4; ++q) xsl[lane + 64 * q] = xsv[q];
   kt_wave_sync();
+  KT_GTS(1);
 #pragma unroll
   for(int c = 0; c < KT_KL; ++c){
     float chain[NE];
@@ -157,26 +159,35 @@ __global__ void __launch_bounds__(LB) k_gemv_mma(const KtGemvArgs a, const int8_
     }
   }
   /* slices in order */
+  KT_GTS(2);
 #pragma unroll
   for(int e = 0; e < NE; ++e) red[((size_t)ks * NT + km_tok(e, lane)) * 32 + lr] = part[e];
   __syncthreads();
   if(ks == 0){
+    /* slices outer, tokens inner: each pass's 8 LDS reads are issued together (a token's sum keeps slice order) */
+    float v[NE];
+#pragma unroll
+    for(int e = 0; e < NE; ++e) v[e] = red[(size_t)km_tok(e, lane) * 32 + lr];
+    for(int k = 1; k < KS; ++k){
+      float w[NE];
+#pragma unroll
+      for(int e = 0; e < NE; ++e) w[e] = red[((size_t)k * NT + km_tok(e, lane)) * 32 + lr];
+#pragma unroll
+      for(int e = 0; e < NE; ++e) v[e] += w[e];
+    }
 #pragma unroll
     for(int e = 0; e < NE; ++e){
-      const int tl = km_tok(e, lane), t = t0 + tl;
-      float v = red[(size_t)tl * 32 + lr];
-      for(int k = 1; k < KS; ++k) v += red[((size_t)k * NT + tl) * 32 + lr];
-      if(t < a.M && rok) m.y[(long long)t * m.ldy + row] = v;
+      const int t = t0 + km_tok(e, lane);
+      if(t < a.M && rok) m.y[(long long)t * m.ldy + row] = v[e];
     }
   }
+  KT_GTS(3);
 }
 
 template __global__ void k_gemv_mma<16, false, 64 * KT_KSMAX>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
 template __global__ void k_gemv_mma<16, true, 64 * KT_KSMAX>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
 template __global__ void k_gemv_mma<16, false, 640>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
 template __global__ void k_gemv_mma<16, true, 640>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
-template __global__ void k_gemv_mma<16, false, 256>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
-template __global__ void k_gemv_mma<16, true, 256>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
 
 /* ------------------------------------------------------------------ q8_0 on the matrix cores
    The q8_0 product (kq8 weights against int8 rows with per-32 scales, lt_mv_q8 lightning.cu:258-284, k_q8
@@ -333,12 +344,20 @@ __global__ void __launch_bounds__(64 * KM_Q8_KS) k_q8_mma(const KtGemvArgs a, co
     for(int e = 0; e < NE; ++e) red[((size_t)ks * NT + km_tok(e, lane)) * 32 + lr] = part[e];
     __syncthreads();
     if(ks == 0){
+      float v[NE];
+#pragma unroll
+      for(int e = 0; e < NE; ++e) v[e] = red[(size_t)km_tok(e, lane) * 32 + lr];
+      for(int k = 1; k < KS; ++k){
+        float w[NE];
+#pragma unroll
+        for(int e = 0; e < NE; ++e) w[e] = red[((size_t)k * NT + km_tok(e, lane)) * 32 + lr];
+#pragma unroll
+        for(int e = 0; e < NE; ++e) v[e] += w[e];
+      }
 #pragma unroll
       for(int e = 0; e < NE; ++e){
-        const int tl = km_tok(e, lane), t = t0 + tl;
-        float v = red[(size_t)tl * 32 + lr];
-        for(int k = 1; k < KS; ++k) v += red[((size_t)k * NT + tl) * 32 + lr];
-        if(t < cntM && rok) yout[(long long)(p0 + t) * ldy + row] = v;
+        const int t = t0 + km_tok(e, lane);
+        if(t < cntM && rok) yout[(long long)(p0 + t) * ldy + row] = v[e];
       }
     }
     __syncthreads();                                             /* red is rewritten by the next pass */
@@ -349,3 +368,12 @@ template __global__ void k_q8_mma<false, false>(const KtGemvArgs, const KtGroupe
 template __global__ void k_q8_mma<false, true>(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
 template __global__ void k_q8_mma<true, false>(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
 template __global__ void k_q8_mma<true, true>(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
+
+#ifdef KT_TRACE
+extern "C" int kt_trace_mma_read(void* host){
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(kt_trace_buf), sizeof(kt_trace_buf), 0, hipMemcpyDeviceToHost);
+}
+extern "C" int kt_trace_mma_enable(int on){
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(kt_trace_on), &on, sizeof(int), 0, hipMemcpyHostToDevice);
+}
+#endif
