@@ -19,6 +19,8 @@ template <bool DBG>
 __global__ void k_gemv_pair(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
 template <int NT, bool DBG, int LB>
 __global__ void k_gemv_mma(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
+template <bool DBG>
+__global__ void k_gemv_m16(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
 template <bool GRP, bool DBG>
 __global__ void k_q8_mma(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
 template <int MT> __global__ void k_plan(const uint8_t*, unsigned*);
@@ -94,10 +96,15 @@ static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, int32_
   for(int i = 0; i < a.nmat; ++i){ a.mat[i].pad = tiles; tiles += (kt_r8(a.mat[i].R) + 3) / 4; }
   const dim3 grid(tiles, (a.M + 15) / 16), block(64 * ks);
   const size_t lds = (size_t)ks * 16 * 32 * 4 + (size_t)ks * 256 * 4;        /* slice sums, XS */
-  /* the 640-thread bound (159 VGPRs: 3 waves a SIMD, activations 2 units ahead) up to 10 slices, also for the
-     narrow products (measured on MI355X: 27B-class step at 16 tokens 4.25 -> 4.10 ms, 2B-class layer at 8 tokens
-     28.1 -> 26.6 us against the 256-thread bound's deeper prefetch at 2 waves a SIMD) */
-  if(ks <= 10){
+  if(a.M > 8 && ks <= 10){
+    /* 16x16x64 tiles from 9 tokens (measured on MI355X: 27B-class step at 16 tokens 4.10 -> 3.99 ms; at 8 tokens
+       the 32x32x32 kernel is faster, 2B-class layer 26.8 against 30.5 us) */
+    if(dbg) hipLaunchKernelGGL((k_gemv_m16<true>), grid, block, lds, s, a, xq, xs, dbg, ks);
+    else hipLaunchKernelGGL((k_gemv_m16<false>), grid, block, lds, s, a, xq, xs, dbg, ks);
+  } else if(ks <= 10){
+    /* the 640-thread bound (159 VGPRs: 3 waves a SIMD, activations 2 units ahead) up to 10 slices, also for the
+       narrow products (measured on MI355X: 27B-class step at 16 tokens 4.25 -> 4.10 ms, 2B-class layer at 8 tokens
+       28.1 -> 26.6 us against the 256-thread bound's deeper prefetch at 2 waves a SIMD) */
     if(dbg) hipLaunchKernelGGL((k_gemv_mma<16, true, 640>), grid, block, lds, s, a, xq, xs, dbg, ks);
     else hipLaunchKernelGGL((k_gemv_mma<16, false, 640>), grid, block, lds, s, a, xq, xs, dbg, ks);
   } else {

@@ -24,6 +24,7 @@ typedef int kt_v16i __attribute__((ext_vector_type(16)));
 #define KM_ROWS 32                    /* weight rows a tile */
 #define KM_TOK 16                     /* tokens a pass */
 
+
 /* 4 digits (0/1/2, one per byte) -> 4 signed trits (-1/0/+1): byte lookup in 0x000100FF */
 __device__ __forceinline__ int km_trits(uint32_t dig){ return (int)__builtin_amdgcn_perm(0x000100FFu, 0x000100FFu, dig); }
 
@@ -188,6 +189,184 @@ template __global__ void k_gemv_mma<16, false, 64 * KT_KSMAX>(const KtGemvArgs, 
 template __global__ void k_gemv_mma<16, true, 64 * KT_KSMAX>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
 template __global__ void k_gemv_mma<16, false, 640>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
 template __global__ void k_gemv_mma<16, true, 640>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
+
+/* ------------------------------------------------------------------ ternary, 16 tokens, V_MFMA_I32_16X16X64_I8
+   k_gemv_m16: the numbers, tree and block shape of k_gemv_mma (a tile of 32 weight rows, wave ks = K slice ks,
+   grid.y = passes of 16 tokens) on 16x16x64 MFMAs, which have no idle token rows at 16 tokens and give each unit two
+   independent accumulator chains:
+   - lane l = 16 g + n loads one 16-byte kt2 chunk of the unit: half g % 2 (columns 64 (g % 2) .. + 63) of row
+     16 (g / 2) + n of the tile, so the wave's 64 loads are the unit's 1 KB in contiguous 128-byte runs;
+   - a 4 x 4 transpose of words across the four 16-lane rows (two permlane32 swaps, two permlane16 swaps) leaves lane
+     (g, n) with word g of the four chunks of its row n: for chunk m (row block m / 2, half m % 2) the four lanes of
+     row n hold its 64 columns 64 (m % 2) + 16 g .. + 15 (g = 0 .. 3); unpacked to signed trits they are the B
+     operand (column n = the weight row), and the A operand is token n's activations of the same columns
+     (V_MFMA_I32_16X16X64_I8: lane 16 g + n holds row / column n, k = 16 g .. + 15 in byte order, measured);
+   - row block b chains its two halves on one accumulator: lane (g, n) register j = v(token 4 g + j, row 16 b + n),
+     the exact int32 unit value (any pairing of columns gives the same integer).
+   The fp32 epilogue is k_gemv_mma's (and k_gemv_flat's) order: per k-lane c the chain over the slice's units 8 s + c
+   in increasing s, fmaf((float)v, XS[t][u] * d[r][u], .), the butterfly's tree over c, the slices in order. */
+__device__ __forceinline__ void km_swap32(unsigned& a, unsigned& b){
+  const auto t = __builtin_amdgcn_permlane32_swap(a, b, false, false); a = t[0]; b = t[1];
+}
+__device__ __forceinline__ void km_swap16(unsigned& a, unsigned& b){
+  const auto t = __builtin_amdgcn_permlane16_swap(a, b, false, false); a = t[0]; b = t[1];
+}
+/* one kt2 word (16 digits, byte b bits 2k.. = column 4 k + b) -> 16 signed trits in column order */
+__device__ __forceinline__ kt_v4i km_unpack16(uint32_t w){
+  kt_v4i B;
+  B[0] = km_trits(w & 0x03030303u);
+  B[1] = km_trits((w >> 2) & 0x03030303u);
+  B[2] = km_trits((w >> 4) & 0x03030303u);
+  B[3] = km_trits((w >> 6) & 0x03030303u);
+  return B;
+}
+
+/* up to 10 K slices (640 threads, 158 VGPRs: 3 waves a SIMD, activations 4 units ahead) */
+template <bool DBG>
+__global__ void __launch_bounds__(640) k_gemv_m16(const KtGemvArgs a, const int8_t* __restrict__ xq,
+                                                  const float* __restrict__ xs, int32_t* __restrict__ dbg, int KS){
+  constexpr int NT = KM_TOK, KM_PF = 4;                          /* tokens a pass, activation units loaded ahead */
+  extern __shared__ __attribute__((aligned(16))) uint8_t kt_lds[];
+  float* red = (float*)kt_lds;                                   /* [KS][NT][32] slice sums */
+  const int NU = a.NU, S = kt_steps(NU);
+  const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, n = lane & 15;
+  const int tile = blockIdx.x, t0 = blockIdx.y * NT;
+  int mi = 0;
+  if(a.nmat > 1 && tile >= a.mat[1].pad) mi = 1;
+  if(a.nmat > 2 && tile >= a.mat[2].pad) mi = 2;
+  const KtMat& m = a.mat[mi];
+  const int rg0 = (tile - m.pad) * 4;                            /* the tile's first row group (of the matrix) */
+  const int crg = rg0 + 2 * (g >> 1) + (n >> 3), cr = n & 7, ch = g & 1;   /* this lane's chunks */
+  const bool cok = crg * KT_RG + cr < m.R;
+  /* the rows of this lane's results: 16 b + n of the tile (row block b = 0, 1) */
+  int orow[2];
+  bool ook[2];
+#pragma unroll
+  for(int b = 0; b < 2; ++b){ orow[b] = (rg0 + 2 * b + (n >> 3)) * KT_RG + cr; ook[b] = orow[b] < m.R; }
+  const int nt = min(NT, a.M - t0);
+  const int s_lo = ks * S / KS, ns = (ks + 1) * S / KS - s_lo;   /* this slice's steps (1 or 2) */
+  const uint4* __restrict__ wb = (const uint4*)m.codes;
+  const uint16_t* __restrict__ sb = m.scales;
+
+  /* the slice's XS [16 units][16 tokens] to this wave's LDS region (after the weight loads are issued) */
+  float* xsl = (float*)(kt_lds + (size_t)KS * NT * 32 * 4) + (size_t)ks * 256;
+  float xsv[4];
+#pragma unroll
+  for(int i = 0; i < 4; ++i){
+    const int idx = lane + 64 * i, un = idx >> 4, tl = idx & 15;
+    const int u = (s_lo + (un >> 3)) * KT_KL + (un & 7);
+    const int t = t0 + tl < a.M ? t0 + tl : t0;
+    xsv[i] = xs[(long long)t * a.ldxs + (u < NU ? u : 0)];
+  }
+  float part[8], t01[8], t23[8], t45[8], pend[8];
+#pragma unroll
+  for(int e = 0; e < 8; ++e){ part[e] = 0.0f; t01[e] = 0.0f; t23[e] = 0.0f; t45[e] = 0.0f; pend[e] = 0.0f; }
+
+  /* the slice's 16 units' chunks (k-lane-major) and both row blocks' scales (b = 0 | b = 1 << 16), unconditional */
+  uint4 wq[2][KT_KL];
+  uint32_t hq[2][KT_KL];
+#pragma unroll
+  for(int c = 0; c < KT_KL; ++c)
+#pragma unroll
+    for(int j = 0; j < 2; ++j){
+      const int s = s_lo + j, u = s * KT_KL + c;
+      const bool ok = j < ns && u < NU;
+      wq[j][c] = kt_ldnt(wb + (ok && cok ? kt_widx(NU, crg, s, ch, c, cr) : 0));
+      const uint32_t h0 = sb[ok && ook[0] ? kt_sidx(NU, rg0 + (n >> 3), u, cr) : 0];
+      const uint32_t h1 = sb[ok && ook[1] ? kt_sidx(NU, rg0 + 2 + (n >> 3), u, cr) : 0];
+      hq[j][c] = h0 | h1 << 16;
+    }
+  /* activations through a buffer resource over the M token rows (lanes past the pass's tokens: past the range,
+     zeros without a memory access) */
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, a.M * a.ldq, 0x00020000);
+  const uint32_t xoff = n < nt ? (uint32_t)((t0 + n) * a.ldq + 16 * g) : (1u << 30);
+  uint4 xa[KM_PF][2];
+  auto ld_act = [&](int un, uint4* dst){                         /* unit un = 2 c + j: both halves */
+    const int c = un >> 1, j = un & 1, u = (s_lo + j) * KT_KL + c;
+    const int uu = (j < ns && u < NU) ? u : 0;
+    dst[0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + uu * 128, 0, 0));
+    dst[1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + uu * 128 + 64, 0, 0));
+  };
+#pragma unroll
+  for(int un = 0; un < KM_PF; ++un) ld_act(un, xa[un]);
+#pragma unroll
+  for(int i = 0; i < 4; ++i) xsl[lane + 64 * i] = xsv[i];
+  kt_wave_sync();
+#pragma unroll
+  for(int c = 0; c < KT_KL; ++c){
+    float chain[8];                                              /* element 4 b + e: row block b, token 4 g + e */
+#pragma unroll
+    for(int e = 0; e < 8; ++e) chain[e] = 0.0f;
+#pragma unroll
+    for(int j = 0; j < 2; ++j){
+      const int un = 2 * c + j, u = (s_lo + j) * KT_KL + c;
+      const bool uok = j < ns && u < NU;                         /* wave-uniform */
+      const uint4 x0 = xa[un % KM_PF][0], x1 = xa[un % KM_PF][1];
+      if(un + KM_PF < 2 * KT_KL) ld_act(un + KM_PF, xa[un % KM_PF]);
+      if(uok){
+        /* word g of the four chunks of row n */
+        unsigned w0 = wq[j][c].x, w1 = wq[j][c].y, w2 = wq[j][c].z, w3 = wq[j][c].w;
+        km_swap32(w0, w2); km_swap32(w1, w3);
+        km_swap16(w0, w1); km_swap16(w2, w3);
+        const kt_v4i A0 = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w};
+        const kt_v4i A1 = {(int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+        kt_v4i d0 = {0, 0, 0, 0}, d1 = {0, 0, 0, 0};
+        d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, km_unpack16(w0), d0, 0, 0, 0);   /* row block 0, half 0 */
+        d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, km_unpack16(w2), d1, 0, 0, 0);   /* row block 1, half 0 */
+        d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, km_unpack16(w1), d0, 0, 0, 0);   /* row block 0, half 1 */
+        d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, km_unpack16(w3), d1, 0, 0, 0);   /* row block 1, half 1 */
+        const float dd0 = ook[0] ? kt_h2f((uint16_t)hq[j][c]) : 0.0f;
+        const float dd1 = ook[1] ? kt_h2f((uint16_t)(hq[j][c] >> 16)) : 0.0f;
+        const float4 sx = *(const float4*)(xsl + (j * 8 + c) * 16 + 4 * g);                /* tokens 4 g .. + 3 */
+        const float sxv[4] = {sx.x, sx.y, sx.z, sx.w};
+#pragma unroll
+        for(int e = 0; e < 4; ++e){
+          chain[e] = fmaf((float)d0[e], sxv[e] * dd0, chain[e]);
+          chain[4 + e] = fmaf((float)d1[e], sxv[e] * dd1, chain[4 + e]);
+          if(DBG){
+            const int t = t0 + 4 * g + e;
+            if(t < a.M && ook[0]) dbg[((long long)t * m.R + orow[0]) * NU + u] = d0[e];
+            if(t < a.M && ook[1]) dbg[((long long)t * m.R + orow[1]) * NU + u] = d1[e];
+          }
+        }
+      }
+    }
+    /* the butterfly's tree over c, as it completes */
+#pragma unroll
+    for(int e = 0; e < 8; ++e){
+      if(c == 0 || c == 2 || c == 4 || c == 6) pend[e] = chain[e];
+      else if(c == 1) t01[e] = pend[e] + chain[e];
+      else if(c == 3) t23[e] = t01[e] + (pend[e] + chain[e]);
+      else if(c == 5) t45[e] = pend[e] + chain[e];
+      else part[e] = t23[e] + (t45[e] + (pend[e] + chain[e]));
+    }
+  }
+  /* slices in order */
+#pragma unroll
+  for(int e = 0; e < 8; ++e) red[((size_t)ks * NT + 4 * g + (e & 3)) * 32 + 16 * (e >> 2) + n] = part[e];
+  __syncthreads();
+  if(ks == 0){
+    float v[8];
+#pragma unroll
+    for(int e = 0; e < 8; ++e) v[e] = red[(size_t)(4 * g + (e & 3)) * 32 + 16 * (e >> 2) + n];
+    for(int k = 1; k < KS; ++k){
+      float w[8];
+#pragma unroll
+      for(int e = 0; e < 8; ++e) w[e] = red[((size_t)k * NT + 4 * g + (e & 3)) * 32 + 16 * (e >> 2) + n];
+#pragma unroll
+      for(int e = 0; e < 8; ++e) v[e] += w[e];
+    }
+#pragma unroll
+    for(int e = 0; e < 8; ++e){
+      const int t = t0 + 4 * g + (e & 3);
+      if(t < a.M && ook[e >> 2]) m.y[(long long)t * m.ldy + orow[e >> 2]] = v[e];
+    }
+  }
+}
+
+template __global__ void k_gemv_m16<false>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
+template __global__ void k_gemv_m16<true>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
 
 /* ------------------------------------------------------------------ q8_0 on the matrix cores
    The q8_0 product (kq8 weights against int8 rows with per-32 scales, lt_mv_q8 lightning.cu:258-284, k_q8
