@@ -44,6 +44,8 @@ def parse():
     ap.add_argument("--plan", action="store_true",
                     help="headline over the decode plan (kt_plan_run: one persistent launch per step) instead of one "
                          "launch per product")
+    ap.add_argument("--only", choices=("c0", "c1", "c2", "c4", "producers"),
+                    help="run one secondary config alone and print its figures (for profiler runs)")
     ap.add_argument("--calib", action="store_true",
                     help="only a plain 1 GiB device copy (the known-size kernel that scales FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
@@ -211,8 +213,12 @@ def config2(torch, linear, synth, timer, steps):
             Y16 = torch.empty((M, R), dtype=torch.float16, device="cuda")
             ms = timer.run(lambda: L.gemm("w", act, Y16=Y16), max(steps // 2, 3), 2)
             tops = 2.0 * M * R * C / ms / 1e9
+            # every MFMA the kernels issue is useful work (2 M R C operations exactly, counted by
+            # SQ_INSTS_VALU_MFMA_MOPS_I8 in profiles/prefill_pmc.md), so the MFMA utilisation against the int8 peak is
+            # the achieved rate over the peak; the counters put the clock under this load at 2.08-2.16 GHz
             res["%s M=%d" % (n, M)] = {"shape": [R, C], "us": round(ms * 1e3, 1), "TOPS": round(tops, 1),
-                                       "frac_int8_peak": round(tops / INT8_PEAK, 4)}
+                                       "frac_int8_peak": round(tops / INT8_PEAK, 4),
+                                       "mfma_util": round(tops / INT8_PEAK, 4)}
             # the vendor's plain int8 GEMM (hipBLASLt through torch._int_mm: int32 out, no scales, no trit unpack)
             # on the same shapes and box, as the practical ceiling of an int8 product here
             try:
@@ -415,6 +421,14 @@ def main():
         return
     timer = Timer(torch)
     use_graph = not a.no_graph
+    if a.only:
+        fn = {"c0": lambda: config0(torch, linear, synth, timer, a.steps, use_graph),
+              "c1": lambda: config1(torch, linear, synth, timer, a.steps, use_graph),
+              "c2": lambda: config2(torch, linear, synth, timer, a.steps),
+              "c4": lambda: config4(torch, moe, synth, timer, a.steps, use_graph),
+              "producers": lambda: producers(torch, linear, synth, timer, a.steps, use_graph)}[a.only]
+        print(json.dumps({"only": a.only, "result": fn()}))
+        return
 
     t0 = time.time()
     log("building the 27B-class weights")

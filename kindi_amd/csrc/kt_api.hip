@@ -21,7 +21,7 @@ template <int NT, bool DBG, int LB>
 __global__ void k_gemv_mma(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
 template <bool DBG>
 __global__ void k_gemv_m16(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
-template <bool GRP, bool DBG>
+template <bool GRP, bool DBG, bool MS>
 __global__ void k_q8_mma(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
 template <int MT> __global__ void k_plan(const uint8_t*, unsigned*);
 size_t kt_splan_lds(int smax, int numax, int tmax);
@@ -578,8 +578,8 @@ int kt_q8_gemv(const void* W, int R, int C, const int8_t* Q, int ldq, const floa
     const dim3 grid((kt_r8(R) + 3) / 4), block(64 * ks);
     const size_t lds = (size_t)ks * 16 * 32 * 4 + (size_t)ks * 256 * 4;          /* slice sums, D */
     const KtGroupedArgs ga = {};
-    if(dbg) hipLaunchKernelGGL((k_q8_mma<false, true>), grid, block, lds, kt_stream(stream), a, ga, Q, D, dbg, ks);
-    else hipLaunchKernelGGL((k_q8_mma<false, false>), grid, block, lds, kt_stream(stream), a, ga, Q, D, dbg, ks);
+    if(dbg) hipLaunchKernelGGL((k_q8_mma<false, true, false>), grid, block, lds, kt_stream(stream), a, ga, Q, D, dbg, ks);
+    else hipLaunchKernelGGL((k_q8_mma<false, false, false>), grid, block, lds, kt_stream(stream), a, ga, Q, D, dbg, ks);
     KT_LAUNCH_CHECK();
     return 0;
   }
@@ -640,8 +640,16 @@ int kt_q8_grouped(const void* const* Wexp, int R, int C, int E, const int* cnt, 
     const dim3 grid((kt_r8(R) + 3) / 4, ny), block(64 * ks);
     const size_t lds = (size_t)ks * 16 * 32 * 4 + (size_t)ks * 256 * 4;          /* slice sums, D */
     const KtGemvArgs da = {};
-    if(dbg) hipLaunchKernelGGL((k_q8_mma<true, true>), grid, block, lds, s, da, a, Q, D, dbg, ks);
-    else hipLaunchKernelGGL((k_q8_mma<true, false>), grid, block, lds, s, da, a, Q, D, dbg, ks);
+    if(ks > 2){
+      /* two waves a block taking the slices in turn (the same slice sums in the same order): blocks of 2 waves at
+         2 waves a SIMD fill every wave slot of a CU, where KS-wave blocks left slots empty (6 slices: 6 of 8) and
+         with them weight bytes in flight (measured on MI355X, config 4 M=256: up 223 -> 162 us, down 161 -> 158 us;
+         one wave a block 169 / 157, three 185 / 210) */
+      const dim3 blk(128);
+      if(dbg) hipLaunchKernelGGL((k_q8_mma<true, true, true>), grid, blk, lds, s, da, a, Q, D, dbg, ks);
+      else hipLaunchKernelGGL((k_q8_mma<true, false, true>), grid, blk, lds, s, da, a, Q, D, dbg, ks);
+    } else if(dbg) hipLaunchKernelGGL((k_q8_mma<true, true, false>), grid, block, lds, s, da, a, Q, D, dbg, ks);
+    else hipLaunchKernelGGL((k_q8_mma<true, false, false>), grid, block, lds, s, da, a, Q, D, dbg, ks);
     KT_LAUNCH_CHECK();
     return 0;
   }

@@ -374,19 +374,21 @@ template __global__ void k_gemv_m16<true>(const KtGemvArgs, const int8_t*, const
    M - 1) or grouped (GRP: one active expert a block row, its token list: entry p reads input row xrow[p] or p and
    writes output row p, lt_mm_* lightning.cu:958-1168). A q8_0 unit (32 columns) is one V_MFMA_I32_32X32X32_I8:
    lane l holds weight row l % 32 and token l % 32, columns 16 h .. 16 h + 15 of the unit (h = l / 32), which is
-   exactly one 16-byte load of the kq8 layout (kt_widx with half h). Block: KS waves over one tile of 32 weight rows
-   (4 row groups), wave ks the K slice ks; the slice's weights are loaded once and serve every pass of 16 tokens of
-   the block's list. Epilogue as k_gemv_flat: per k-lane c the chain fmaf((float)v, d * D[t][u], .) over the slice's
+   exactly one 16-byte load of the kq8 layout (kt_widx with half h). Block: one tile of 32 weight rows (4 row
+   groups); with KS waves, wave ks takes K slice ks and its weights are loaded once for every pass of 16 tokens of
+   the block's list; with MS, W waves take the slices in turn (wave w: slices w, w + W, ...), reading each slice's
+   weights again every pass. Epilogue as k_gemv_flat: per k-lane c the chain fmaf((float)v, d * D[t][u], .) over the slice's
    units 8 s + c, the butterfly's tree over c, the slices in order. */
 #define KM_Q8_KS 8                    /* at most 8 K slices (q8_0 C <= 4096): 256 VGPRs a lane */
-template <bool GRP, bool DBG>
+template <bool GRP, bool DBG, bool MS>   /* MS: wave w takes slices w, w + W, ... (W waves a block) */
 __global__ void __launch_bounds__(64 * KM_Q8_KS) k_q8_mma(const KtGemvArgs a, const KtGroupedArgs ga,
                                                           const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                           int32_t* __restrict__ dbg, int KS){
   constexpr int NT = KM_TOK, NE = NT / 2;
   extern __shared__ __attribute__((aligned(16))) uint8_t kt_lds[];
   float* red = (float*)kt_lds;                                   /* [KS][NT][32] slice sums */
-  const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = blockDim.x >> 6;
   const int h = lane >> 5, lr = lane & 31;
   const int tile = blockIdx.x;
   const uint4* __restrict__ wb;
@@ -415,7 +417,9 @@ __global__ void __launch_bounds__(64 * KM_Q8_KS) k_q8_mma(const KtGemvArgs a, co
   const int S = kt_steps(NU);
   const int rg = tile * 4 + (lr >> 3), r = lr & 7, row = rg * KT_RG + r;
   const bool rok = row < R;
-  const int s_lo = ks * S / KS, ns = (ks + 1) * S / KS - s_lo;   /* this slice's steps (1 or 2) */
+  int ks = wv, s_lo = 0, ns = 0;                                 /* the current slice and its steps (1 or 2) */
+  auto set_slice = [&](int k){ ks = k; s_lo = k * S / KS; ns = (k + 1) * S / KS - s_lo; };
+  set_slice(wv);
   const int nrows = GRP ? ga.nrows : cntM;
 
   /* a pass's loads, all unconditional (clamped) and issued together: the D scales of the slice's 16 units x 16
@@ -423,7 +427,7 @@ __global__ void __launch_bounds__(64 * KM_Q8_KS) k_q8_mma(const KtGemvArgs a, co
      activations of the 16 units through a buffer resource over the input rows (lanes past the pass's tokens read at
      2^31, past the range, which gives zeros without a memory access; the launcher keeps the rows below 2^31 bytes) */
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, nrows * ldq, 0x00020000);
-  float* xsl = (float*)(kt_lds + (size_t)KS * NT * 32 * 4) + (size_t)ks * 256;
+  float* xsl = (float*)(kt_lds + (size_t)KS * NT * 32 * 4) + (size_t)wv * 256;
   float xsv[4];
   uint4 xa[2 * KT_KL];
   /* the pass's input rows (the list indirection) first, the loads that need them after */
@@ -455,28 +459,22 @@ __global__ void __launch_bounds__(64 * KM_Q8_KS) k_q8_mma(const KtGemvArgs a, co
       xa[n] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo + uu * 32, 0, 0));
     }
   };
-  /* the input rows of pass 0, then the weights (independent of them), then the pass's D and activations, so the
-     weight stream overlaps the list indirection */
-  ld_rows(0);
-  __builtin_amdgcn_sched_barrier(0);
-
-  /* the slice's 16 units in k-lane-major order, loaded once (unconditional: a unit past the slice or the matrix
-     reads offset 0) */
+  /* the slice's 16 units in k-lane-major order (unconditional: a unit past the slice or the matrix reads offset 0) */
   uint4 wq[2][KT_KL];
   uint16_t hq[2][KT_KL];
+  auto ld_w = [&](){
 #pragma unroll
-  for(int c = 0; c < KT_KL; ++c)
+    for(int c = 0; c < KT_KL; ++c)
 #pragma unroll
-    for(int j = 0; j < 2; ++j){
-      const int s = s_lo + j, u = s * KT_KL + c;
-      const bool ok = rok && j < ns && u < NU;
-      wq[j][c] = kt_ldnt(wb + (ok ? kt_widx(NU, rg, s, h, c, r) : 0));
-      hq[j][c] = sb[ok ? kt_sidx(NU, rg, u, r) : 0];
-    }
-  __builtin_amdgcn_sched_barrier(0);
-  ld_pass(0);
-
-  for(int t0 = 0; t0 < cntM; t0 += NT){                          /* uniform: the block's list in passes */
+      for(int j = 0; j < 2; ++j){
+        const int s = s_lo + j, u = s * KT_KL + c;
+        const bool ok = rok && j < ns && u < NU;
+        wq[j][c] = kt_ldnt(wb + (ok ? kt_widx(NU, rg, s, h, c, r) : 0));
+        hq[j][c] = sb[ok ? kt_sidx(NU, rg, u, r) : 0];
+      }
+  };
+  /* the slice's products for the pass at t0 into red[ks] */
+  auto compute = [&](int t0){
 #pragma unroll
     for(int q = 0; q < 4; ++q) xsl[lane + 64 * q] = xsv[q];
     kt_wave_sync();
@@ -518,11 +516,13 @@ __global__ void __launch_bounds__(64 * KM_Q8_KS) k_q8_mma(const KtGemvArgs a, co
         else part[e] = t23[e] + (t45[e] + (pend[e] + chain[e]));
       }
     }
-    if(t0 + NT < cntM){ ld_rows(t0 + NT); ld_pass(t0 + NT); }                          /* uniform: the next pass's loads in flight */
 #pragma unroll
     for(int e = 0; e < NE; ++e) red[((size_t)ks * NT + km_tok(e, lane)) * 32 + lr] = part[e];
+  };
+  /* the pass's slice sums in slice order, by wave 0 */
+  auto finish = [&](int t0){
     __syncthreads();
-    if(ks == 0){
+    if(wv == 0){
       float v[NE];
 #pragma unroll
       for(int e = 0; e < NE; ++e) v[e] = red[(size_t)km_tok(e, lane) * 32 + lr];
@@ -540,13 +540,43 @@ __global__ void __launch_bounds__(64 * KM_Q8_KS) k_q8_mma(const KtGemvArgs a, co
       }
     }
     __syncthreads();                                             /* red is rewritten by the next pass */
+  };
+
+  if(!MS){
+    /* one slice a wave, its weights loaded once for every pass: the input rows of pass 0, then the weights
+       (independent of them), then the pass's D and activations, so the weight stream overlaps the list
+       indirection; each pass issues the next pass's loads before its slice sums */
+    ld_rows(0);
+    __builtin_amdgcn_sched_barrier(0);
+    ld_w();
+    __builtin_amdgcn_sched_barrier(0);
+    ld_pass(0);
+    for(int t0 = 0; t0 < cntM; t0 += NT){                        /* uniform: the block's list in passes */
+      compute(t0);
+      if(t0 + NT < cntM){ ld_rows(t0 + NT); ld_pass(t0 + NT); }  /* uniform: the next pass's loads in flight */
+      finish(t0);
+    }
+  } else {
+    /* several slices a wave, one after the other (each with its own weights, read again every pass: from L2
+       after the first), so blocks are small and more of them share a CU's wave slots */
+    for(int t0 = 0; t0 < cntM; t0 += NT){
+      ld_rows(t0);
+      for(int k = wv; k < KS; k += W){                           /* uniform */
+        set_slice(k);
+        ld_w();
+        ld_pass(t0);
+        compute(t0);
+      }
+      finish(t0);
+    }
   }
 }
 
-template __global__ void k_q8_mma<false, false>(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
-template __global__ void k_q8_mma<false, true>(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
-template __global__ void k_q8_mma<true, false>(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
-template __global__ void k_q8_mma<true, true>(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
+#define KQ8(GRP, DBG, MS) template __global__ void k_q8_mma<GRP, DBG, MS>(const KtGemvArgs, const KtGroupedArgs, \
+    const int8_t*, const float*, int32_t*, int);
+KQ8(false, false, false) KQ8(false, true, false) KQ8(true, false, false) KQ8(true, true, false)
+KQ8(true, false, true) KQ8(true, true, true)
+#undef KQ8
 
 #ifdef KT_TRACE
 extern "C" int kt_trace_mma_read(void* host){

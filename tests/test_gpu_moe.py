@@ -53,6 +53,41 @@ def test_q8_gemv(kt, R, C, M):
     assert max_rel(y, orc.q8_out(acc, rows, R, C, d)) < TOL
 
 
+@pytest.mark.parametrize("C", [512, 1024, 1536, 2688, 3584, 4096])
+def test_grouped_mma_widths(kt, C):
+    """the grouped matrix-core q8_0 product (16 entries an expert on average) at widths of 1 to 8 K slices: one slice
+    a wave (up to 2 slices) and two waves taking the slices in turn (3 to 8, odd counts included). int32 unit values
+    exact against the oracle, and every expert's rows bit-identical to the dense product of the same tokens"""
+    lib, moe = kt
+    E, k, M, R = 16, 4, 64, 96
+    say("grouped mma", C, "KS", lib.kt_decode_kslices(C, 1))
+    rows = [q8_case(R, C, 300 + e)[0] for e in range(E)]
+    ups = moe.Q8Experts(rows, R, C)
+    downs = moe.Q8Experts([q8_case(C, R, 400 + e)[0] for e in range(E)], C, R)
+    layer = moe.MoE(ups, downs, k)
+    r = rng(C)
+    ids = np.stack([r.permutation(E)[:k] for _ in range(M)]).astype(np.int32)
+    lists = layer.lists(dev(ids))
+    X = r.normal(0, 1, (M, C)).astype(np.float32)
+    Q, D = moe.q8_quantize(dev(X))
+    q, d = orc.q8_quant(X)
+    n = M * k
+    Y = torch.empty((n, R), dtype=torch.float32, device="cuda")
+    dbg = torch.empty((n, R, C // 32), dtype=torch.int32, device="cuda")
+    ups.grouped(lists, M, Q, D, Y, xrow=True, dbg=dbg)
+    Y2 = torch.full((n, R), float("nan"), dtype=torch.float32, device="cuda")
+    ups.grouped(lists, M, Q, D, Y2, xrow=True)
+    assert np.array_equal(host(Y).view(np.uint32), host(Y2).view(np.uint32))
+    cnt, off, xrow, where = orc.moe_sort(ids, E)
+    y, g = host(Y), host(dbg)
+    for e in range(E):
+        p = np.arange(off[e], off[e] + cnt[e])
+        assert np.array_equal(g[p], orc.q8_acc(rows[e], R, C, q[xrow[p]])), e
+        idx = torch.from_numpy(xrow[p]).cuda().long()
+        dense = moe.Q8Matrix(rows[e], R, C).gemv(Q[idx], D[idx])
+        assert np.array_equal(host(dense).view(np.uint32), y[p].view(np.uint32)), e
+
+
 @pytest.mark.parametrize("E,M", [(60, 1), (60, 300), (1024, 200), (1000, 700)])
 def test_sort_wide(kt, E, M):
     """kt_moe_sort at other expert counts (not a power of two, the 1024 maximum), one expert taking half the
