@@ -447,7 +447,7 @@ def main():
         nlaunch, kernel = 1, "k_plan<1> (decode plan, %d stages, grid %d x %d waves)" % (
             len(stages), plan.info.grid, plan.info.waves + 1)
     else:
-        ms, nlaunch, kernel = ms_l, len(calls), "k_gemv_flat1<ternary,MT=1>"
+        ms, nlaunch, kernel = ms_l, len(calls), "k_gemv_flat1<ternary,MT=1> (q/k/v, o, down) + k_gemv_pair (gate/up)"
     gbs = nbytes / ms / 1e6
     # the dominant kernel is the whole step (plan) or every launch of it (launches, back to back in the graph): its
     # average duration is the timed region over the launch count (an upper bound: it includes the gaps)
