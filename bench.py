@@ -46,6 +46,9 @@ def parse():
                          "launch per product")
     ap.add_argument("--only", choices=("c0", "c1", "c2", "c4", "producers"),
                     help="run one secondary config alone and print its figures (for profiler runs)")
+    ap.add_argument("--cpu-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--cpu-runs", type=int, default=5, help=argparse.SUPPRESS)
+    ap.add_argument("--cpu-run-s", type=float, default=2.0, help=argparse.SUPPRESS)
     ap.add_argument("--calib", action="store_true",
                     help="only a plain 1 GiB device copy (the known-size kernel that scales FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
@@ -331,10 +334,40 @@ def producers(torch, linear, synth, timer, steps, use_graph):
 
 
 # ----------------------------------------------------------------------------------------------- CPU baseline
-def cpu_baseline(synth, budget_s=12.0, nlayers=4):
-    """kcpu.c's pair-table GEMV over 27B layers (7 matrices each), on the host's cores. nlayers distinct layers
-    (352 MB of codes) rotate so the sample streams from DRAM rather than the host's caches."""
+def physical_cores():
+    """the physical cores (package, core id) among the CPUs this process may run on, and the first CPU of each"""
+    cores = {}
+    for cpu in sorted(os.sched_getaffinity(0)):
+        base = "/sys/devices/system/cpu/cpu%d/topology/" % cpu
+        try:
+            key = (open(base + "physical_package_id").read().strip(), open(base + "core_id").read().strip())
+        except OSError:
+            key = ("?", str(cpu))
+        cores.setdefault(key, cpu)
+    return cores
+
+
+def cpu_baseline(synth, runs=5, run_s=2.0):
+    """kcpu.c's pair-table GEMV over 27B layers, timed in a child process that owns its OpenMP setup: one thread per
+    physical core this process may use, OMP_PROC_BIND=close, OMP_PLACES=cores; a warm-up pass, then `runs` timed
+    runs of about run_s seconds; the median run is the value"""
+    import subprocess
+    cores = physical_cores()
+    env = dict(os.environ, OMP_NUM_THREADS=str(len(cores)), OMP_PROC_BIND="close", OMP_PLACES="cores")
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-child", "--cpu-runs", str(runs),
+                        "--cpu-run-s", str(run_s)], env=env, capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        raise RuntimeError("cpu baseline child failed:\n" + r.stderr[-2000:])
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    out["allowed_cpus"] = len(os.sched_getaffinity(0))         # before the child's OpenMP binding narrows its mask
+    return out
+
+
+def cpu_child(runs, run_s, nlayers=4):
+    """the measurement cpu_baseline starts: nlayers distinct layers (352 MB of codes) rotate so the sample streams
+    from DRAM rather than the host's caches"""
     import numpy as np
+    from kindi_amd import synth
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
     ref = orc.ref_kcpu() is not None
@@ -357,15 +390,21 @@ def cpu_baseline(synth, budget_s=12.0, nlayers=4):
         for Pc, S, R, C in mats:
             gemv(Pc, S, R, C, xs[C])
 
-    for mats in layers:
+    for mats in layers:                                          # warm-up: every layer once
         layer(mats)
-    reps = 0
-    t0 = time.perf_counter()
-    while reps < 8 or time.perf_counter() - t0 < budget_s:
-        layer(layers[reps % nlayers])
-        reps += 1
-    el = time.perf_counter() - t0
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count()))
+    rates, passes, total = [], 0, 0.0
+    for _ in range(runs):
+        reps = 0
+        t0 = time.perf_counter()
+        while reps < nlayers or time.perf_counter() - t0 < run_s:
+            layer(layers[reps % nlayers])
+            reps += 1
+        el = time.perf_counter() - t0
+        rates.append(nbytes * reps / el / 1e9)
+        passes += reps
+        total += el
+    rates.sort()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0"))
     model = ""
     try:
         for ln in open("/proc/cpuinfo"):
@@ -374,11 +413,15 @@ def cpu_baseline(synth, budget_s=12.0, nlayers=4):
                 break
     except OSError:
         pass
-    return {"value": round(nbytes * reps / el / 1e9, 2), "unit": "GB/s", "cores": threads,
-            "cpu": model, "host_cpus": os.cpu_count(), "kind": "reference" if ref else "port",
-            "sample": "%d layer passes of the 27B-class decode (q,k,v,o,gate,up,down; %.1f MB of ternary weights per "
-                      "layer, %d distinct layers rotating) in %.1f s: fp32 pair-table GEMV (kcpu.c gemv), %d OpenMP "
-                      "threads" % (reps, nbytes / 1e6, nlayers, el, threads)}
+    print(json.dumps({
+        "value": round(rates[len(rates) // 2], 2), "unit": "GB/s", "cores": threads, "cpu": model,
+        "host_cpus": os.cpu_count(),
+        "kind": "reference" if ref else "port", "runs_GBs": [round(x, 2) for x in rates],
+        "omp": "OMP_NUM_THREADS=%d (physical cores allowed) OMP_PROC_BIND=%s OMP_PLACES=%s" % (
+            threads, os.environ.get("OMP_PROC_BIND"), os.environ.get("OMP_PLACES")),
+        "sample": "median of %d runs (%d layer passes in %.1f s after a warm-up) of the 27B-class decode (q,k,v,o,gate,"
+                  "up,down; %.1f MB of ternary weights per layer, %d distinct layers rotating): fp32 pair-table GEMV "
+                  "(kcpu.c gemv), %d OpenMP threads" % (runs, passes, total, nbytes / 1e6, nlayers, threads)}))
 
 
 # ----------------------------------------------------------------------------------------------- HBM traffic
@@ -409,6 +452,9 @@ def pmc_traffic():
 # ----------------------------------------------------------------------------------------------- main
 def main():
     a = parse()
+    if a.cpu_child:                                              # the CPU baseline's own process (no GPU)
+        cpu_child(a.cpu_runs, a.cpu_run_s)
+        return
     if a.gpus != 1:
         print("bench.py: this build measures one GPU; the product shards per GPU (see DESIGN.md) but multi-GPU "
               "runs are not part of it. Use --gpus 1.", file=sys.stderr)
