@@ -159,6 +159,43 @@ def sweep_step(torch, linear, layers, M, seed=7):
     return step, nbytes, calls, launches, stages
 
 
+def step_with_producers(torch, linear, layers, M=1):
+    """config 3's decode step with each product's input made by its fused producer, as Kindi's decode runs them: per
+    layer rmsfold (one residual part) -> q/k/v, fold -> o, rmsfold (one part) -> gate/up, smfold (17408 columns) ->
+    down: 512 dependent launches a step. One set of fp32 input buffers serves every layer (the timing does not depend
+    on their values); each product reads the int8 row its producer just wrote."""
+    H, F = 5120, 17408
+    Lin = linear.Linear({})
+    g = torch.Generator(device="cuda").manual_seed(70)
+    x, r = (torch.randn((M, H), device="cuda", generator=g) for _ in range(2))
+    a, b2 = (torch.randn((M, F), device="cuda", generator=g) for _ in range(2))
+    w = torch.ones(H, device="cuda")
+    sgH = torch.where(torch.rand(H, device="cuda", generator=g) < 0.5, -1.0, 1.0).float()
+    sgF = torch.where(torch.rand(F, device="cuda", generator=g) < 0.5, -1.0, 1.0).float()
+    xw = torch.empty_like(x)
+    aH, aO, aG = (linear._act_out(M, H, "cuda") for _ in range(3))
+    aF = linear._act_out(M, F, "cuda")
+    outs = []
+    for l, mats in enumerate(layers):
+        for n, m in mats.items():
+            Lin.add("%d.%s" % (l, n), m)
+        outs.append({n: torch.empty((M, m.R), dtype=torch.float32, device="cuda") for n, m in mats.items()})
+
+    def step():
+        for l in range(len(layers)):
+            p, o = "%d." % l, outs[l]
+            linear.rmsfold(x, w, sgH, 1024, r=r, nparts=1, xw=xw, out=aH)
+            Lin.gemv_q([p + "q", p + "k", p + "v"], aH, [o["q"], o["k"], o["v"]])
+            linear.fold(x, sgH, 1024, out=aO)
+            Lin.gemv_q([p + "o"], aO, [o["o"]])
+            linear.rmsfold(x, w, sgH, 1024, r=r, nparts=1, xw=xw, out=aG)
+            Lin.gemv_q([p + "gate", p + "up"], aG, [o["gate"], o["up"]])
+            linear.smfold(a, b2, sgF, 1024, out=aF)
+            Lin.gemv_q([p + "down"], aF, [o["down"]])
+
+    return step
+
+
 # ----------------------------------------------------------------------------------------------- other configs
 def config0(torch, linear, synth, timer, steps, use_graph):
     R, C = synth.CFG["c0"]["R"], synth.CFG["c0"]["C"]
@@ -372,7 +409,7 @@ def cpu_child(runs, run_s, nlayers=4):
     import oracle as orc
     ref = orc.ref_kcpu() is not None
     layers = []
-    nbytes = 0
+    nbytes = kbytes = 0
     for l in range(nlayers):
         mats = []
         for i, (n, R, C) in enumerate(synth.CFG["c3"]["mats"]):
@@ -382,6 +419,9 @@ def cpu_child(runs, run_s, nlayers=4):
             mats.append((orc.paircodes_fast(bc, R, C), orc.pair_scales(dpm, R, C), R, C))
             if l == 0:
                 nbytes += tern_bytes(R, C, 1)
+                # what kcpu.c streams: 4-bit pair codes (2 bits a weight), fp32 scales per (row, 128 columns), fp32
+                # x in and y out
+                kbytes += R * C // 4 + R * (C // 128) * 4 + C * 4 + R * 4
         layers.append(mats)
     xs = {C: np.random.default_rng(C).normal(0, 1, C).astype(np.float32) for C in (5120, 17408)}
     gemv = orc.ref_gemv if ref else orc.pair_gemv
@@ -400,7 +440,7 @@ def cpu_child(runs, run_s, nlayers=4):
             layer(layers[reps % nlayers])
             reps += 1
         el = time.perf_counter() - t0
-        rates.append(nbytes * reps / el / 1e9)
+        rates.append(reps / el)                                  # layer passes a second
         passes += reps
         total += el
     rates.sort()
@@ -413,15 +453,19 @@ def cpu_child(runs, run_s, nlayers=4):
                 break
     except OSError:
         pass
+    med = rates[len(rates) // 2]
     print(json.dumps({
-        "value": round(rates[len(rates) // 2], 2), "unit": "GB/s", "cores": threads, "cpu": model,
+        "value": round(nbytes * med / 1e9, 2), "unit": "GB/s", "cores": threads, "cpu": model,
+        "kcpu_stream_GBs": round(kbytes * med / 1e9, 2),
         "host_cpus": os.cpu_count(),
-        "kind": "reference" if ref else "port", "runs_GBs": [round(x, 2) for x in rates],
+        "kind": "reference" if ref else "port", "runs_GBs": [round(nbytes * x / 1e9, 2) for x in rates],
         "omp": "OMP_NUM_THREADS=%d (physical cores allowed) OMP_PROC_BIND=%s OMP_PLACES=%s" % (
             threads, os.environ.get("OMP_PROC_BIND"), os.environ.get("OMP_PLACES")),
         "sample": "median of %d runs (%d layer passes in %.1f s after a warm-up) of the 27B-class decode (q,k,v,o,gate,"
                   "up,down; %.1f MB of ternary weights per layer, %d distinct layers rotating): fp32 pair-table GEMV "
-                  "(kcpu.c gemv), %d OpenMP threads" % (runs, passes, total, nbytes / 1e6, nlayers, threads)}))
+                  "(kcpu.c gemv), %d OpenMP threads. value counts the GPU line's algorithmic bytes per layer (the same "
+                  "work unit); kcpu_stream_GBs the %.1f MB a layer kcpu.c itself streams (2-bit pair codes, fp32 "
+                  "scales and vectors)" % (runs, passes, total, nbytes / 1e6, nlayers, threads, kbytes / 1e6)}))
 
 
 # ----------------------------------------------------------------------------------------------- HBM traffic
@@ -521,6 +565,15 @@ def main():
         cfgs = {"c3 M=1 launches": {"ms_per_step": round(ms_l, 4), "GB/s": round(nbytes / ms_l / 1e6, 1),
                                     "frac_hbm": round(nbytes / ms_l / 1e6 / HBM_PEAK, 4),
                                     "note": "%d graph-captured launches (kt_tern_gemv / gemv3) per step" % len(calls)}}
+        log("config 3, M=1 with producers")
+        stepP = step_with_producers(torch, linear, layers, 1)
+        msP = timer.run(graphed(torch, stepP, use_graph), a.steps, a.warmup)
+        cfgs["c3 M=1 step with producers"] = {
+            "ms_per_step": round(msP, 4), "launches_per_step": 8 * len(layers),
+            "products_GB/s": round(nbytes / msP / 1e6, 1),
+            "note": "the headline's 256 products, each input made by its fused producer (rmsfold / fold / rmsfold / "
+                    "smfold) in the launch before it; products_GB/s counts only the products' bytes"}
+        del stepP
         log("config 3, M=16")
         step16, nb16, calls16, _, _ = sweep_step(torch, linear, layers, 16)
         ms16 = timer.run(graphed(torch, step16, use_graph), max(a.steps // 2, 3), 2)
