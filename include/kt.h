@@ -54,7 +54,12 @@ int kt_tern_pack_ptq1(const uint8_t* raw, int R, int C, int row0, int nrows, voi
 /* ---------------------------------------------------------------- activations
    X fp32 [M][ldx] -> XQ int8 [M][ldq] (natural column order, ldq % 16 == 0), XS f32 / XA i32 [M][C/128].
    per_row = 0: the reference's per-128-group scale (k_tc_q8, tc_hip.cu:43-74; tcq128 tc.cu:160-194; k_q8x_T
-   chunk.cu:781-802). per_row = 1: one amax per token row (the same formula; XS repeated per group). */
+   chunk.cu:781-802). per_row = 1: one amax per token row (the same formula; XS repeated per group).
+   per_row = 2: hp, k_tc_q8 with hp (tc.cu:195-209; KINDI_TC_HP spec.py:63-67): two rows a token, XQ / XS / XA with 2M
+   rows. Row 2n is the per-group row of per_row 0; row 2n + 1 quantizes the residual r = fma(-q, amax / 127, x) with
+   the fixed amax a2 = amax / 254: q2 = clamp(rne(r (127 / a2)), -127, 127), XS = a2 / 127, XA = sum q2. The decode
+   products take such rows with M | KT_HP. Other values: hipErrorInvalidValue. */
+#define KT_HP (1 << 30)               /* hp flag, carried in the decode products' M and the producers' HB (tc.cu tc_hp) */
 int kt_quant_q8(const float* X, int ldx, int M, int C, int per_row, int8_t* XQ, int ldq, float* XS, int32_t* XA,
                 void* stream);
 
@@ -68,6 +73,10 @@ int kt_quant_q8(const float* X, int ldx, int M, int C, int per_row, int8_t* XQ, 
    ((l4 + l5) + (l6 + l7)), and the slice sums are added left to right. No workspace, no second pass.
    Replaces k_tc_mv{2,4,8} + k_tc_sum (tc_hip.cu:180-199, 236-240, 271-279; spec.py:619-657). */
 int kt_decode_kslices(int C, int q8);
+/* M | KT_HP (kt_tern_gemv and kt_tern_gemv3): M tokens of two input rows each (kt_quant_q8 per_row 2, or a producer
+   with HB | KT_HP); Y row t = the fp32 results of input rows 2t and 2t + 1 added, in that order (tc.cu:405-407).
+   Each row's result is the one-row product's, so Y[t] == Y1[2t] + Y1[2t + 1] for the product Y1 of the 2M rows
+   without the flag. dbg then has 2M rows. */
 int kt_tern_gemv(const void* W, int R, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M,
                  float* Y, int ldy, int32_t* dbg, void* stream);
 
@@ -212,7 +221,10 @@ int kt_moe_decode_noalloc(const void* const* Wup, const void* const* Wdown, int 
    fold = the unnormalised Walsh-Hadamard transform of each HB-column block times 1/sqrt(HB), HB in {512, 1024,
    4096}. C % HB == 0; rmsfold takes C <= 8192 (one block holds the row for the norm), fold / smfold any width up to
    2^20 (chunks of whole HB blocks). M <= 65535. xw (x + parts, only with nparts > 0), xn and xo are nullable;
-   xw, xn and xo may be x itself (with its row stride); they may not overlap x or the parts otherwise. The reference's two-row high-precision mode (hp) is not offered. */
+   xw, xn and xo may be x itself (with its row stride); they may not overlap x or the parts otherwise.
+   HB | KT_HP: the reference's two-row form (hp, ff_q8 tcf.cu:150-205): XQ / XS / XA with 2M rows, row 2n the int8
+   row above, row 2n + 1 the residual r = fma(-q, amax / 127, xo) at the fixed scale amax / 32258:
+   q2 = clamp(rne(r (32258 / amax)), -127, 127), XS = amax / 32258, XA = sum q2 (0 when amax = 0). */
 int kt_rmsfold_q8(const float* x, int ldx, const float* r, int ldr, int nparts, const float* w, const float* sg, int M,
                   int C, int HB, float* xw, int ldxw, float* xn, int ldxn, float* xo, int ldxo, int8_t* XQ, int ldq,
                   float* XS, int32_t* XA, void* stream);

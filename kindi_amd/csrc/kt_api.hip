@@ -134,6 +134,7 @@ static int kt_launch_gemv(const KtGemvArgs& a, int ngroups, const int8_t* xq, co
   }
   int mt = a.M <= 1 ? 1 : a.M <= 2 ? 2 : 4;
   while(mt > 1 && (mt == 4 ? KtFlat<FMT, 4>::lds(ks) : KtFlat<FMT, 2>::lds(ks)) > 65536) mt >>= 1;
+  if(a.hp && mt < 2) return KT_INVALID;                      /* a token's two rows share a chunk */
   const dim3 grid(ngroups), block(64 * ks);
   const KtGroupedArgs ga = {};
 #define KT_F(K, MT) do { const size_t lds = KtFlat<FMT, MT>::lds(ks); \
@@ -148,7 +149,14 @@ static int kt_launch_gemv(const KtGemvArgs& a, int ngroups, const int8_t* xq, co
 static int kt_tern_gemv_n(int nmat, const void* const* W, const int* Rs, float* const* Ys, const int* ldys, int C,
                           const int8_t* XQ, int ldq, const float* XS, const int32_t* XA, int M, int32_t* dbg,
                           void* stream){
+  /* M | KT_HP: M tokens of two input rows each (kt_quant_q8 per_row 2, the producers' HB | KT_HP) */
+  const int hp = (M & KT_HP) ? 1 : 0;
+  M &= ~KT_HP;
   if(M == 0) return 0;
+  if(hp){
+    if(M < 0 || M > (1 << 29)) return KT_INVALID;
+    M *= 2;                                                  /* input rows */
+  }
   if(M < 0 || C <= 0 || C % 128 || !XQ || !XS || !XA || ldq < C || ldq % 16 || !kt_al(XQ, 16)) return KT_INVALID;
   KtGemvArgs a = {};
   const int NG = C / 128;
@@ -169,6 +177,7 @@ static int kt_tern_gemv_n(int nmat, const void* const* W, const int* Rs, float* 
   a.ldq = ldq;
   a.ldxs = NG;
   a.M = M;
+  a.hp = hp;
   return kt_launch_gemv<KT_FMT_TERN>(a, groups, XQ, XS, (const int*)XA, dbg, kt_stream(stream));
 }
 
@@ -335,8 +344,8 @@ int kt_quant_q8(const float* X, int ldx, int M, int C, int per_row, int8_t* XQ, 
                 void* stream){
   if(M == 0) return 0;
   if(!X || !XQ || !XS || !XA || M < 0 || C <= 0 || C % 128 || ldx < C || ldq < C || ldx % 2 || ldq % 16
-     || !kt_al(X, 8) || !kt_al(XQ, 16)) return KT_INVALID;
-  hipLaunchKernelGGL(k_quant_tern, dim3(M), dim3(256), 0, kt_stream(stream), X, ldx, C, per_row ? 1 : 0, XQ, ldq,
+     || !kt_al(X, 8) || !kt_al(XQ, 16) || per_row < 0 || per_row > 2) return KT_INVALID;
+  hipLaunchKernelGGL(k_quant_tern, dim3(M), dim3(256), 0, kt_stream(stream), X, ldx, C, per_row, XQ, ldq,
                      XS, (int*)XA);
   KT_LAUNCH_CHECK();
   return 0;
@@ -724,27 +733,33 @@ static int kt_fold_run(int mode, const KtFoldArgs& a, int M, void* stream){
 int kt_rmsfold_q8(const float* x, int ldx, const float* r, int ldr, int nparts, const float* w, const float* sg, int M,
                   int C, int HB, float* xw, int ldxw, float* xn, int ldxn, float* xo, int ldxo, int8_t* XQ, int ldq,
                   float* XS, int32_t* XA, void* stream){
+  const int hp = (HB & KT_HP) ? 1 : 0;                      /* HB | KT_HP: two int8 rows a token */
+  HB &= ~KT_HP;
   if(!kt_fold_shape(M, C, HB, sg, XQ, ldq, XS, XA) || C > 8192 || !x || !w || ldx < C || nparts < 0 || nparts > 8
      || (nparts > 0 && (!r || ldr < nparts * C)) || (xw && ldxw < C) || (xn && ldxn < C) || (xo && ldxo < C))
     return KT_INVALID;
-  KtFoldArgs a = {x, ldx, r, ldr, nparts, w, sg, 1, 1, 1, xw, ldxw, xn, ldxn, xo, ldxo, C, HB, XQ, ldq, XS, XA};
+  KtFoldArgs a = {x, ldx, r, ldr, nparts, w, sg, 1, 1, 1, xw, ldxw, xn, ldxn, xo, ldxo, C, HB, XQ, ldq, XS, XA, hp};
   return kt_fold_run(0, a, M, stream);
 }
 
 int kt_fold_q8(const float* x, int ldx, const float* sg, int M, int C, int HB, float* xo, int ldxo, int8_t* XQ,
                int ldq, float* XS, int32_t* XA, void* stream){
+  const int hp = (HB & KT_HP) ? 1 : 0;                      /* HB | KT_HP: two int8 rows a token */
+  HB &= ~KT_HP;
   if(!kt_fold_shape(M, C, HB, sg, XQ, ldq, XS, XA) || !x || ldx < C || (xo && ldxo < C)) return KT_INVALID;
-  KtFoldArgs a = {x, ldx, nullptr, 0, 0, nullptr, sg, 1, 1, 1, nullptr, 0, nullptr, 0, xo, ldxo, C, HB, XQ, ldq, XS, XA};
+  KtFoldArgs a = {x, ldx, nullptr, 0, 0, nullptr, sg, 1, 1, 1, nullptr, 0, nullptr, 0, xo, ldxo, C, HB, XQ, ldq, XS, XA, hp};
   return kt_fold_run(1, a, M, stream);
 }
 
 int kt_smfold_q8(const float* a_, int lda, const float* b, int ldb, const float* sg, int hd, int nk, int rep, int M,
                  int C, int HB, float* xo, int ldxo, int8_t* XQ, int ldq, float* XS, int32_t* XA, void* stream){
+  const int hp = (HB & KT_HP) ? 1 : 0;                      /* HB | KT_HP: two int8 rows a token */
+  HB &= ~KT_HP;
   if(!kt_fold_shape(M, C, HB, sg, XQ, ldq, XS, XA) || !a_ || !b || lda < C || ldb < C || (xo && ldxo < C) || rep < 1
      || (rep > 1 && (hd <= 0 || nk <= 0 || (long long)hd * nk * rep != C)))
     return KT_INVALID;
   KtFoldArgs a = {a_, lda, b, ldb, 0, nullptr, sg, hd, nk, rep, nullptr, 0, nullptr, 0, xo, ldxo, C, HB, XQ, ldq, XS,
-                  XA};
+                  XA, hp};
   return kt_fold_run(2, a, M, stream);
 }
 

@@ -109,11 +109,14 @@ struct KtMat {
   int R, ldy, rg0, pad;
 };
 
+#define KT_HP (1 << 30)                /* the hp flag carried in an int argument (tc.cu tc_hp) */
+
 struct KtGemvArgs {
   KtMat mat[KT_MAXMAT];
   int nmat, NU;                       /* matrices; units (groups / blocks) along C */
   int ldq, ldxs;                      /* activation row stride (bytes); xs / xa row stride (units) */
-  int M, pad;                         /* tokens */
+  int M, hp;                          /* input rows; hp: two rows a token (2t: the int8 row, 2t + 1: its residual),
+                                         output row t = the fp32 results of rows 2t and 2t + 1 added (tc.cu:405-407) */
 };
 
 /* a decode plan in device memory: header, stages, then the stage counters and the status word */

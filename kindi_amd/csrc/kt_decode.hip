@@ -138,7 +138,10 @@ __device__ __forceinline__ int kt_wave_sum(int v){
 }
 
 /* grid (M), block 256: one token row. Each wave takes groups w, w + 4, ...; a lane holds columns 2l, 2l+1 of the
-   group. per_row: amax over the whole row first (the same formula with one scale per row). */
+   group. per_row 1: amax over the whole row first (the same formula with one scale per row). per_row 2 (hp, k_tc_q8
+   with hp, tc.cu:195-209): two rows a token, 2n the group's int8 row as per_row 0, 2n + 1 its residual
+   r = v - q (amax / 127) (one fma, as the reference's compiler contracts it) quantized with the fixed amax
+   a2 = amax / 254: q2 = clamp(rne(r (127 / a2)), -127, 127), XS = a2 / 127, XA = sum q2 (tcq128 tc.cu:160-194). */
 extern "C" __global__ void __launch_bounds__(256) k_quant_tern(const float* __restrict__ X, int ldx, int C, int per_row,
                                                                int8_t* __restrict__ Q, int ldq, float* __restrict__ XS,
                                                                int* __restrict__ XA){
@@ -146,7 +149,7 @@ extern "C" __global__ void __launch_bounds__(256) k_quant_tern(const float* __re
   const float* x = X + (long long)n * ldx;
   __shared__ float red[4];
   float rmax = 0.0f;
-  if(per_row){
+  if(per_row == 1){
     float a = 0.0f;
     for(int c = threadIdx.x * 2; c < C; c += 512){
       const float2 v = *(const float2*)(x + c);
@@ -159,14 +162,26 @@ extern "C" __global__ void __launch_bounds__(256) k_quant_tern(const float* __re
   }
   for(int g = w; g < NG; g += 4){
     const float2 v = *(const float2*)(x + g * 128 + 2 * lane);
-    const float amax = per_row ? rmax : kt_wave_max(fmaxf(fabsf(v.x), fabsf(v.y)));
+    const float amax = per_row == 1 ? rmax : kt_wave_max(fmaxf(fabsf(v.x), fabsf(v.y)));
     const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
     const int q0 = __float2int_rn(v.x * id), q1 = __float2int_rn(v.y * id);
     const int s = kt_wave_sum(q0 + q1);
-    *(uint16_t*)(Q + (long long)n * ldq + g * 128 + 2 * lane) = (uint16_t)((q0 & 255) | ((q1 & 255) << 8));
+    const long long n0 = per_row == 2 ? 2 * n : n;
+    *(uint16_t*)(Q + n0 * ldq + g * 128 + 2 * lane) = (uint16_t)((q0 & 255) | ((q1 & 255) << 8));
     if(lane == 0){
-      XS[(long long)n * NG + g] = amax / 127.0f;
-      XA[(long long)n * NG + g] = s;
+      XS[n0 * NG + g] = amax / 127.0f;
+      XA[n0 * NG + g] = s;
+    }
+    if(per_row == 2){                                               /* wave-uniform */
+      const float sc = amax / 127.0f, a2 = amax / 254.0f, id2 = a2 != 0.0f ? 127.0f / a2 : 0.0f;
+      const float r0 = fmaf(-(float)q0, sc, v.x), r1 = fmaf(-(float)q1, sc, v.y);
+      const int p0 = max(-127, min(127, __float2int_rn(r0 * id2))), p1 = max(-127, min(127, __float2int_rn(r1 * id2)));
+      const int s2 = kt_wave_sum(p0 + p1);
+      *(uint16_t*)(Q + (n0 + 1) * ldq + g * 128 + 2 * lane) = (uint16_t)((p0 & 255) | ((p1 & 255) << 8));
+      if(lane == 0){
+        XS[(n0 + 1) * NG + g] = a2 / 127.0f;
+        XA[(n0 + 1) * NG + g] = s2;
+      }
     }
   }
 }

@@ -15,7 +15,8 @@ struct KtFoldArgs {
   float* xo; int ldxo;             /* the folded, scaled row (nullable) */
   int C, HB;
   int8_t* Q; int ldq;              /* int8 row, natural column order */
-  float* XS; int32_t* XA;          /* [M][C/128] */
+  float* XS; int32_t* XA;          /* [M][C/128], or [2M][C/128] with hp */
+  int hp;                          /* two rows a token: 2n the int8 row, 2n + 1 its residual (ff_q8 tcf.cu:150-205) */
 };
 
 hipError_t kt_fold_launch(int mode, const KtFoldArgs& a, int M, hipStream_t s);

@@ -81,7 +81,7 @@ __global__ void __launch_bounds__(512) k_fold_q8(const KtFoldArgs a){
   __shared__ float sm[NM * 512];
   __shared__ double red[16];
   __shared__ float qm[NM * 8];
-  __shared__ int qs[NM * 8];
+  __shared__ int qs[NM * 8], qs2[NM * 8];
   const int j = threadIdx.x, n = blockIdx.y, lane = j & 63, w = j >> 6, C = NM * 512, c0 = blockIdx.x * C;
   float v[NM];
   if(MODE == 0){
@@ -174,7 +174,10 @@ __global__ void __launch_bounds__(512) k_fold_q8(const KtFoldArgs a){
     if(lane == 0) qm[k * 8 + w] = m;
   }
   __syncthreads();
-  int8_t* Q = a.Q + (long long)n * a.ldq;
+  /* hp: rows 2n (the int8 row) and 2n + 1 (the residual r = v - q (amax / 127), one fma as the reference's compiler
+     contracts it, at the fixed scale amax / 32258: q2 = clamp(rne(r (32258 / amax)), -127, 127); ff_q8 tcf.cu:150-205) */
+  const long long n0 = a.hp ? 2 * n : n;
+  int8_t* Q = a.Q + n0 * a.ldq;
   const int NG = a.C >> 7;
 #pragma unroll
   for(int k = 0; k < NM; ++k){
@@ -184,6 +187,13 @@ __global__ void __launch_bounds__(512) k_fold_q8(const KtFoldArgs a){
     Q[c0 + j + 512 * k] = (int8_t)qi;
     const int sum = kf_wave_sum(qi);
     if(lane == 0) qs[k * 8 + w] = sum;
+    if(a.hp){                                                    /* block-uniform */
+      const float r = fmaf(-(float)qi, amax / 127.0f, v[k]);
+      const int q2 = max(-127, min(127, __float2int_rn(r * (amax != 0.0f ? 32258.0f / amax : 0.0f))));
+      Q[a.ldq + c0 + j + 512 * k] = (int8_t)q2;
+      const int sum2 = kf_wave_sum(q2);
+      if(lane == 0) qs2[k * 8 + w] = sum2;
+    }
   }
   __syncthreads();
   if(lane == 0 && !(w & 1)){
@@ -191,8 +201,12 @@ __global__ void __launch_bounds__(512) k_fold_q8(const KtFoldArgs a){
     for(int k = 0; k < NM; ++k){
       const int g = (c0 >> 7) + 4 * k + (w >> 1);
       const float amax = fmaxf(qm[k * 8 + w], qm[k * 8 + w + 1]);
-      a.XS[(long long)n * NG + g] = amax / 127.0f;
-      a.XA[(long long)n * NG + g] = qs[k * 8 + w] + qs[k * 8 + w + 1];
+      a.XS[n0 * NG + g] = amax / 127.0f;
+      a.XA[n0 * NG + g] = qs[k * 8 + w] + qs[k * 8 + w + 1];
+      if(a.hp){
+        a.XS[(n0 + 1) * NG + g] = amax / 32258.0f;
+        a.XA[(n0 + 1) * NG + g] = qs2[k * 8 + w] + qs2[k * 8 + w + 1];
+      }
     }
   }
 }

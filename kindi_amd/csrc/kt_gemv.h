@@ -292,12 +292,19 @@ __device__ __forceinline__ void kt_gemv_flat_body(const KtGemvArgs& a, const KtG
     }
     __syncthreads();                                                 /* every wave runs the same token chunks */
     if(ks == 0 && c == 0){
+      float vv[MT];
 #pragma unroll
       for(int t = 0; t < MT; ++t){
         float v = red[t * 8 + r];
         for(int k = 1; k < KS; ++k) v += red[(k * MT + t) * 8 + r];
-        if(t < nt && row < R){
-          yout[(long long)(p0 + t0 + t) * ldy + row] = v;
+        vv[t] = v;
+      }
+#pragma unroll
+      for(int t = 0; t < MT; ++t){
+        if(!GRP && a.hp){                                             /* rows 2t, 2t + 1 -> token t (MT even) */
+          if(MT > 1 && !(t & 1) && t < nt && row < R) yout[(long long)((t0 + t) >> 1) * ldy + row] = vv[t] + vv[t + 1 < MT ? t + 1 : t];
+        } else if(t < nt && row < R){
+          yout[(long long)(p0 + t0 + t) * ldy + row] = vv[t];
         }
       }
     }

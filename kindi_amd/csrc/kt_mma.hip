@@ -178,8 +178,10 @@ __global__ void __launch_bounds__(LB) k_gemv_mma(const KtGemvArgs a, const int8_
     }
 #pragma unroll
     for(int e = 0; e < NE; ++e){
-      const int t = t0 + km_tok(e, lane);
-      if(t < a.M && rok) m.y[(long long)t * m.ldy + row] = v[e];
+      const int t = t0 + km_tok(e, lane);                        /* even e: an even row, its pair in e + 1 */
+      if(a.hp){
+        if(!(e & 1) && t < a.M && rok) m.y[(long long)(t >> 1) * m.ldy + row] = v[e] + v[e + 1];
+      } else if(t < a.M && rok) m.y[(long long)t * m.ldy + row] = v[e];
     }
   }
   KT_GTS(3);
@@ -359,8 +361,10 @@ __global__ void __launch_bounds__(640) k_gemv_m16(const KtGemvArgs a, const int8
     }
 #pragma unroll
     for(int e = 0; e < 8; ++e){
-      const int t = t0 + 4 * g + (e & 3);
-      if(t < a.M && ook[e >> 2]) m.y[(long long)t * m.ldy + orow[e >> 2]] = v[e];
+      const int t = t0 + 4 * g + (e & 3);                        /* even e: an even row, its pair in e + 1 */
+      if(a.hp){
+        if(!(e & 1) && t < a.M && ook[e >> 2]) m.y[(long long)(t >> 1) * m.ldy + orow[e >> 2]] = v[e] + v[e + 1];
+      } else if(t < a.M && ook[e >> 2]) m.y[(long long)t * m.ldy + orow[e >> 2]] = v[e];
     }
   }
 }

@@ -120,30 +120,36 @@ def load_ptq1(path, offset, R, C, device="cuda", W=None, chunk_rows=8192):
     return m
 
 
-Act = namedtuple("Act", "XQ XS XA M C per_row")
+# hp (tc.cu tc_hp, KINDI_TC_HP spec.py:63-67): two int8 rows a token, row 2n its int8 row and 2n + 1 the residual's,
+# for about 14 bits of activation precision at the same weight traffic; the decode products add each token's two
+# row results. XQ / XS / XA then hold 2M rows.
+Act = namedtuple("Act", "XQ XS XA M C per_row hp", defaults=(False,))
+KT_HP = 1 << 30                                    # the flag carried in M (products) and HB (producers)
 
 
-def quantize(X, per_row=False, out=None):
-    """fp32 [M, C] -> int8 rows per 128-column group (k_tc_q8, tc_hip.cu:43-74) or per row. Returns Act."""
+def quantize(X, per_row=False, out=None, hp=False):
+    """fp32 [M, C] -> int8 rows per 128-column group (k_tc_q8, tc_hip.cu:43-74) or per row; hp: the two-row form
+    (k_tc_q8 with hp, tc.cu:195-209, per group). Returns Act."""
     if X.dim() == 1:
         X = X.reshape(1, -1)
     M, C = X.shape
     if X.dtype != torch.float32 or X.stride(1) != 1:
         raise ValueError("quantize takes fp32 rows with unit column stride")
+    if hp and per_row:
+        raise ValueError("hp is per 128-column group")
     if out is None:
-        out = Act(torch.empty((M, C), dtype=torch.int8, device=X.device),
-                  torch.empty((M, C // 128), dtype=torch.float32, device=X.device),
-                  torch.empty((M, C // 128), dtype=torch.int32, device=X.device), M, C, per_row)
+        out = _act_out(M, C, X.device, hp)
     lib = gpudrv.load()
-    gpudrv.check(lib.kt_quant_q8(ptr(X), X.stride(0), M, C, 1 if per_row else 0, ptr(out.XQ), out.XQ.stride(0),
-                                 ptr(out.XS), ptr(out.XA), stream()), "kt_quant_q8")
-    return Act(out.XQ, out.XS, out.XA, M, C, per_row)
+    gpudrv.check(lib.kt_quant_q8(ptr(X), X.stride(0), M, C, 2 if hp else (1 if per_row else 0), ptr(out.XQ),
+                                 out.XQ.stride(0), ptr(out.XS), ptr(out.XA), stream()), "kt_quant_q8")
+    return Act(out.XQ, out.XS, out.XA, M, C, per_row, hp)
 
 
-def _act_out(M, C, device):
-    return Act(torch.empty((M, C), dtype=torch.int8, device=device),
-               torch.empty((M, C // 128), dtype=torch.float32, device=device),
-               torch.empty((M, C // 128), dtype=torch.int32, device=device), M, C, False)
+def _act_out(M, C, device, hp=False):
+    Mq = 2 * M if hp else M
+    return Act(torch.empty((Mq, C), dtype=torch.int8, device=device),
+               torch.empty((Mq, C // 128), dtype=torch.float32, device=device),
+               torch.empty((Mq, C // 128), dtype=torch.int32, device=device), M, C, False, hp)
 
 
 def _f32_rows(t, what):
@@ -154,46 +160,50 @@ def _f32_rows(t, what):
     return t
 
 
-def rmsfold(x, w, sg, HB, r=None, nparts=0, xw=None, xn=None, xo=None, out=None):
+def rmsfold(x, w, sg, HB, r=None, nparts=0, xw=None, xn=None, xo=None, out=None, hp=False):
     """k_rmsfold_qT (tcf.cu:370-390; k_rmsfold kindi.cu:350-394) as one launch: x [M, C] fp32 (+ the nparts residual
     parts of r [M, >= nparts C], C apart, in part order) -> RMS norm (weights w) -> sign sg -> Hadamard fold of each
-    HB block -> int8 row. Returns the Act; xw (x + parts), xn (normed) and xo (folded) are written when given."""
+    HB block -> int8 row (hp: the two-row form, ff_q8 tcf.cu:150-205). Returns the Act; xw (x + parts), xn (normed)
+    and xo (folded) are written when given."""
     x = _f32_rows(x.reshape(1, -1) if x.dim() == 1 else x, "x")
     M, C = x.shape
     _f32_rows(r, "r"), _f32_rows(xw, "xw"), _f32_rows(xn, "xn"), _f32_rows(xo, "xo")
-    out = out or _act_out(M, C, x.device)
+    out = out or _act_out(M, C, x.device, hp)
     gpudrv.check(gpudrv.load().kt_rmsfold_q8(
-        ptr(x), x.stride(0), ptr(r), r.stride(0) if r is not None else 0, nparts, ptr(w), ptr(sg), M, C, HB,
+        ptr(x), x.stride(0), ptr(r), r.stride(0) if r is not None else 0, nparts, ptr(w), ptr(sg), M, C,
+        HB | (KT_HP if hp else 0),
         ptr(xw), xw.stride(0) if xw is not None else 0, ptr(xn), xn.stride(0) if xn is not None else 0,
         ptr(xo), xo.stride(0) if xo is not None else 0, ptr(out.XQ), out.XQ.stride(0), ptr(out.XS), ptr(out.XA),
         stream()), "kt_rmsfold_q8")
-    return Act(out.XQ, out.XS, out.XA, M, C, False)
+    return Act(out.XQ, out.XS, out.XA, M, C, False, hp)
 
 
-def fold(x, sg, HB, xo=None, out=None):
-    """k_fold_fwht_qT (tcf.cu:410-426): sign, Hadamard fold of each HB block, int8 row"""
+def fold(x, sg, HB, xo=None, out=None, hp=False):
+    """k_fold_fwht_qT (tcf.cu:410-426): sign, Hadamard fold of each HB block, int8 row (hp: two rows a token)"""
     x = _f32_rows(x.reshape(1, -1) if x.dim() == 1 else x, "x")
     M, C = x.shape
     _f32_rows(xo, "xo")
-    out = out or _act_out(M, C, x.device)
-    gpudrv.check(gpudrv.load().kt_fold_q8(ptr(x), x.stride(0), ptr(sg), M, C, HB, ptr(xo),
+    out = out or _act_out(M, C, x.device, hp)
+    gpudrv.check(gpudrv.load().kt_fold_q8(ptr(x), x.stride(0), ptr(sg), M, C, HB | (KT_HP if hp else 0), ptr(xo),
                                           xo.stride(0) if xo is not None else 0, ptr(out.XQ), out.XQ.stride(0),
                                           ptr(out.XS), ptr(out.XA), stream()), "kt_fold_q8")
-    return Act(out.XQ, out.XS, out.XA, M, C, False)
+    return Act(out.XQ, out.XS, out.XA, M, C, False, hp)
 
 
-def smfold(a, b, sg, HB, perm=(1, 1, 1), xo=None, out=None):
-    """k_smfold_qT (tcf.cu:392-408): SiLU(a) * b in the grouped-head order perm = (hd, nk, rep), sign, fold, int8"""
+def smfold(a, b, sg, HB, perm=(1, 1, 1), xo=None, out=None, hp=False):
+    """k_smfold_qT (tcf.cu:392-408): SiLU(a) * b in the grouped-head order perm = (hd, nk, rep), sign, fold, int8
+    (hp: two rows a token)"""
     a = _f32_rows(a.reshape(1, -1) if a.dim() == 1 else a, "a")
     b = _f32_rows(b.reshape(1, -1) if b.dim() == 1 else b, "b")
     M, C = a.shape
     _f32_rows(xo, "xo")
-    out = out or _act_out(M, C, a.device)
+    out = out or _act_out(M, C, a.device, hp)
     gpudrv.check(gpudrv.load().kt_smfold_q8(ptr(a), a.stride(0), ptr(b), b.stride(0), ptr(sg), perm[0], perm[1],
-                                            perm[2], M, C, HB, ptr(xo), xo.stride(0) if xo is not None else 0,
+                                            perm[2], M, C, HB | (KT_HP if hp else 0), ptr(xo),
+                                            xo.stride(0) if xo is not None else 0,
                                             ptr(out.XQ), out.XQ.stride(0), ptr(out.XS), ptr(out.XA), stream()),
                  "kt_smfold_q8")
-    return Act(out.XQ, out.XS, out.XA, M, C, False)
+    return Act(out.XQ, out.XS, out.XA, M, C, False, hp)
 
 
 class Linear(object):
@@ -203,11 +213,12 @@ class Linear(object):
     the matrix cores (kt_tern_gemm). Within one kernel a token's result does not depend on how many tokens share
     the pass (tc_hip.cu:14-15)."""
 
-    def __init__(self, mats=None, device="cuda", decode_max=16, per_row=False):
+    def __init__(self, mats=None, device="cuda", decode_max=16, per_row=False, hp=False):
         self.w = dict(mats or {})
         self.device = device
         self.decode_max = decode_max
         self.per_row = per_row
+        self.hp = hp                               # gemv quantizes x in the two-row form (KINDI_TC_HP)
 
     def add(self, name, mat):
         self.w[name] = mat
@@ -226,9 +237,10 @@ class Linear(object):
         for m, o in zip(ms, outs):
             if o.dtype != torch.float32 or o.shape[-1] != m.R or o.numel() < act.M * m.R or not o.is_contiguous():
                 raise ValueError("output for %d rows x %d tokens" % (m.R, act.M))
+        Mf = act.M | (KT_HP if act.hp else 0)          # hp: M tokens of two rows, each output row their sum
         if len(ms) == 1:
             rc = lib.kt_tern_gemv(ptr(ms[0].W), ms[0].R, C, ptr(act.XQ), act.XQ.stride(0), ptr(act.XS), ptr(act.XA),
-                                  act.M, ptr(outs[0]), ms[0].R, ptr(dbg), stream())
+                                  Mf, ptr(outs[0]), ms[0].R, ptr(dbg), stream())
             return gpudrv.check(rc, "kt_tern_gemv") or 1
         if dbg is not None:
             raise ValueError("dbg takes a single tensor")
@@ -236,14 +248,14 @@ class Linear(object):
         Ws = [ptr(m.W) for m in ms] + [None] * (3 - len(ms))
         Ys = [ptr(o) for o in outs] + [None] * (3 - len(ms))
         rc = lib.kt_tern_gemv3(Ws[0], Rs[0], Ys[0], Ws[1], Rs[1], Ys[1], Ws[2], Rs[2], Ys[2], C, ptr(act.XQ),
-                               act.XQ.stride(0), ptr(act.XS), ptr(act.XA), act.M, stream())
+                               act.XQ.stride(0), ptr(act.XS), ptr(act.XA), Mf, stream())
         return gpudrv.check(rc, "kt_tern_gemv3") or 1
 
     def gemv(self, names, x, outs, parts_ok=False):
         """Engine.gemv (engine.py:254-274): up to three ternary tensors with the same fp32 input x ([C] or [M, C]).
         The input is quantized once (the int8 path); every row's sum is completed inside the launch, so the part
         count returned is always 1 (parts_ok is accepted for the reference's signature)."""
-        act = quantize(x, self.per_row)
+        act = quantize(x, self.per_row, hp=self.hp)
         outs = [o.reshape(act.M, -1) for o in outs]
         return self.gemv_q(names, act, outs)
 
@@ -254,6 +266,8 @@ class Linear(object):
         m = self.w[name]
         if act.C != m.C:
             raise ValueError("input width %d != %d" % (act.C, m.C))
+        if act.hp:
+            raise ValueError("the prefill product takes one int8 row a token (hp is a decode form)")
         if Y is None and Y16 is None:
             Y = torch.empty((act.M, m.R), dtype=torch.float32, device=act.XQ.device)
         ldy = (Y if Y is not None else Y16).stride(0)
@@ -290,6 +304,8 @@ class Plan(object):
         for k, (mats, act, outs) in enumerate(stages):
             if not 1 <= len(mats) <= 3 or len(outs) != len(mats):
                 raise ValueError("stage %d: 1 to 3 matrices with one output each" % k)
+            if act.hp:
+                raise ValueError("stage %d: the decode plan takes one int8 row a token (no hp)" % k)
             st = arr[k]
             for i, (m, o) in enumerate(zip(mats, outs)):
                 if m.C != act.C or o.dtype != torch.float32 or not o.is_contiguous() or o.numel() < act.M * m.R:

@@ -67,29 +67,51 @@ uint16_t or_f2h(float f){                    /* round to nearest even, as F16C _
 /* ------------------------------------------------------------------ int8 activations, 128-column groups
    Follows k_tc_q8 (tc_hip.cu:43-74) and tcq128 (tc.cu:160-194): amax = max |x| over the group, id = 127 / amax
    (0 when amax = 0), q = round-to-nearest-even(x * id), XS = amax / 127, XA = sum q.
-   per_row != 0: the BASELINE configs' per-token absmax: amax over the whole row, the same XS for every group of the
-   row (the formula is unchanged); XA stays per group. Q is [M][ldq] int8 in natural column order. */
+   per_row = 1: the BASELINE configs' per-token absmax: amax over the whole row, the same XS for every group of the
+   row (the formula is unchanged); XA stays per group. Q is [M][ldq] int8 in natural column order.
+   per_row = 2 / 3 (hp: two rows a token, Q / XS / XA with 2M rows): row 2n is the per-group row above; row 2n + 1
+   quantizes the residual r = fma(-q, amax / 127, x) (the reference's compiler contracts x - q (amax / 127) into one
+   fma) at a fixed amax:
+     2: k_tc_q8 with hp (tc.cu:195-209, tcq128 tc.cu:160-194): a2 = amax / 254, q2 = clamp(rne(r (127 / a2)), -127,
+        127), XS = a2 / 127;
+     3: the producers' ff_q8 with hp (tcf.cu:150-205): q2 = clamp(rne(r (32258 / amax)), -127, 127), XS = amax / 32258.
+   XA = the sum of the row's q2. Both residual scales are 0 when amax = 0 (every q2 is then 0). */
+static int or_clamp127(int q){ return q < -127 ? -127 : (q > 127 ? 127 : q); }
+
 void or_quant_q8(const float* X, int ldx, int M, int C, int per_row, int8_t* Q, int ldq, float* XS, int* XA){
-  const int NG = C / 128;
+  const int NG = C / 128, hp = per_row >= 2;
   for(int n = 0; n < M; ++n){
     const float* x = X + (size_t)n * ldx;
+    const size_t n0 = hp ? 2 * (size_t)n : (size_t)n;
     float rmax = 0.0f;
-    if(per_row) for(int c = 0; c < C; ++c) rmax = fmaxf(rmax, fabsf(x[c]));
+    if(per_row == 1) for(int c = 0; c < C; ++c) rmax = fmaxf(rmax, fabsf(x[c]));
     for(int g = 0; g < NG; ++g){
       float amax = rmax;
-      if(!per_row){
+      if(per_row != 1){
         amax = 0.0f;
         for(int e = 0; e < 128; ++e) amax = fmaxf(amax, fabsf(x[g * 128 + e]));
       }
       const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-      int sum = 0;
+      int sum = 0, sum2 = 0;
+      const float sc = amax / 127.0f, a2 = amax / 254.0f;
+      const float id2 = per_row == 2 ? (a2 != 0.0f ? 127.0f / a2 : 0.0f) : (amax != 0.0f ? 32258.0f / amax : 0.0f);
       for(int e = 0; e < 128; ++e){
         const int q = (int)nearbyintf(x[g * 128 + e] * id);
-        Q[(size_t)n * ldq + g * 128 + e] = (int8_t)q;
+        Q[n0 * ldq + g * 128 + e] = (int8_t)q;
         sum += q;
+        if(hp){
+          const float r = fmaf(-(float)q, sc, x[g * 128 + e]);
+          const int q2 = or_clamp127((int)nearbyintf(r * id2));
+          Q[(n0 + 1) * ldq + g * 128 + e] = (int8_t)q2;
+          sum2 += q2;
+        }
       }
-      XS[(size_t)n * NG + g] = amax / 127.0f;
-      XA[(size_t)n * NG + g] = sum;
+      XS[n0 * NG + g] = sc;
+      XA[n0 * NG + g] = sum;
+      if(hp){
+        XS[(n0 + 1) * NG + g] = per_row == 2 ? a2 / 127.0f : amax / 32258.0f;
+        XA[(n0 + 1) * NG + g] = sum2;
+      }
     }
   }
 }
@@ -491,6 +513,8 @@ void or_fwht_blocks(float* v, int C, int HB){
 void or_rmsfold_q8(const float* x, int ldx, const float* r, int ldr, int nparts, const float* w, const float* sg,
                    int M, int C, int HB, float* xw, int ldxw, float* xn, int ldxn, float* xo, int ldxo,
                    int8_t* Q, int ldq, float* XS, int* XA){
+  const int hp = (HB >> 30) & 1;                 /* HB | 1 << 30: two int8 rows a token (ff_q8 hp) */
+  HB &= ~(1 << 30);
   float* xf = (float*)malloc(sizeof(float) * C);
   float* v = (float*)malloc(sizeof(float) * C);
   for(int n = 0; n < M; ++n){
@@ -514,19 +538,23 @@ void or_rmsfold_q8(const float* x, int ldx, const float* r, int ldr, int nparts,
     }
     or_fwht_blocks(v, C, HB);
     if(xo) memcpy(xo + (size_t)n * ldxo, v, sizeof(float) * C);
-    or_quant_q8(v, C, 1, C, 0, Q + (size_t)n * ldq, ldq, XS + (size_t)n * (C / 128), XA + (size_t)n * (C / 128));
+    const size_t n0 = hp ? 2 * (size_t)n : (size_t)n;
+    or_quant_q8(v, C, 1, C, hp ? 3 : 0, Q + n0 * ldq, ldq, XS + n0 * (C / 128), XA + n0 * (C / 128));
   }
   free(xf); free(v);
 }
 
 void or_fold_q8(const float* x, int ldx, const float* sg, int M, int C, int HB, float* xo, int ldxo,
                 int8_t* Q, int ldq, float* XS, int* XA){
+  const int hp = (HB >> 30) & 1;                 /* HB | 1 << 30: two int8 rows a token (ff_q8 hp) */
+  HB &= ~(1 << 30);
   float* v = (float*)malloc(sizeof(float) * C);
   for(int n = 0; n < M; ++n){
     for(int e = 0; e < C; ++e) v[e] = sg[e] * x[(size_t)n * ldx + e];
     or_fwht_blocks(v, C, HB);
     if(xo) memcpy(xo + (size_t)n * ldxo, v, sizeof(float) * C);
-    or_quant_q8(v, C, 1, C, 0, Q + (size_t)n * ldq, ldq, XS + (size_t)n * (C / 128), XA + (size_t)n * (C / 128));
+    const size_t n0 = hp ? 2 * (size_t)n : (size_t)n;
+    or_quant_q8(v, C, 1, C, hp ? 3 : 0, Q + n0 * ldq, ldq, XS + n0 * (C / 128), XA + n0 * (C / 128));
   }
   free(v);
 }
@@ -540,6 +568,8 @@ int or_perm_src(int e, int hd, int nk, int rep){
 
 void or_smfold_q8(const float* a, int lda, const float* b, int ldb, const float* sg, int hd, int nk, int rep,
                   int M, int C, int HB, float* xo, int ldxo, int8_t* Q, int ldq, float* XS, int* XA){
+  const int hp = (HB >> 30) & 1;                 /* HB | 1 << 30: two int8 rows a token (ff_q8 hp) */
+  HB &= ~(1 << 30);
   float* v = (float*)malloc(sizeof(float) * C);
   for(int n = 0; n < M; ++n){
     for(int e = 0; e < C; ++e){
@@ -550,7 +580,8 @@ void or_smfold_q8(const float* a, int lda, const float* b, int ldb, const float*
     }
     or_fwht_blocks(v, C, HB);
     if(xo) memcpy(xo + (size_t)n * ldxo, v, sizeof(float) * C);
-    or_quant_q8(v, C, 1, C, 0, Q + (size_t)n * ldq, ldq, XS + (size_t)n * (C / 128), XA + (size_t)n * (C / 128));
+    const size_t n0 = hp ? 2 * (size_t)n : (size_t)n;
+    or_quant_q8(v, C, 1, C, hp ? 3 : 0, Q + n0 * ldq, ldq, XS + n0 * (C / 128), XA + n0 * (C / 128));
   }
   free(v);
 }

@@ -200,13 +200,17 @@ def f2h(f):
 
 
 def quant_q8(X, per_row=False):
-    """fp32 [M, C] -> (Q int8 [M, C], XS f32 [M, C/128], XA i32 [M, C/128])"""
+    """fp32 [M, C] -> (Q int8 [M', C], XS f32 [M', C/128], XA i32 [M', C/128]). per_row: 0 / False per 128-column
+    group, 1 / True per row, 2 hp as k_tc_q8 (tc.cu:195-209), 3 hp as the producers' ff_q8 (tcf.cu:150-205); with hp
+    M' = 2M (row 2n the int8 row, 2n + 1 its residual), else M' = M"""
     X = _c(X, np.float32)
     M, C = X.shape
-    Q = np.empty((M, C), np.int8)
-    XS = np.empty((M, C // 128), np.float32)
-    XA = np.empty((M, C // 128), np.int32)
-    lib().or_quant_q8(_p(X), C, M, C, 1 if per_row else 0, _p(Q), C, _p(XS), _p(XA))
+    mode = int(per_row)
+    Mo = 2 * M if mode >= 2 else M
+    Q = np.empty((Mo, C), np.int8)
+    XS = np.empty((Mo, C // 128), np.float32)
+    XA = np.empty((Mo, C // 128), np.int32)
+    lib().or_quant_q8(_p(X), C, M, C, mode, _p(Q), C, _p(XS), _p(XA))
     return Q, XS, XA
 
 
@@ -410,9 +414,13 @@ def ref_k_q8g(g4, R, C, q, d):
 
 
 # ----------------------------------------------------------------------------------------------- fused producers
-def _prod_out(M, C):
-    return (np.empty((M, C), np.float32), np.empty((M, C), np.int8), np.empty((M, C // 128), np.float32),
-            np.empty((M, C // 128), np.int32))
+HP = 1 << 30                                   # HB | HP: the producers' two-row (hp) int8 output
+
+
+def _prod_out(M, C, hp=False):
+    Mq = 2 * M if hp else M
+    return (np.empty((M, C), np.float32), np.empty((Mq, C), np.int8), np.empty((Mq, C // 128), np.float32),
+            np.empty((Mq, C // 128), np.int32))
 
 
 def sumsq(xf):
@@ -428,34 +436,38 @@ def fwht_blocks(v, HB):
     return v
 
 
-def rmsfold_q8(x, r, nparts, w, sg, HB):
-    """k_rmsfold_qT: x [M, C]; r [M, nparts * C] (parts C apart) or None -> dict xw, xn, xo, Q, XS, XA"""
+def rmsfold_q8(x, r, nparts, w, sg, HB, hp=False):
+    """k_rmsfold_qT: x [M, C]; r [M, nparts * C] (parts C apart) or None -> dict xw, xn, xo, Q, XS, XA (hp: Q, XS, XA
+    with rows 2n / 2n + 1, ff_q8 tcf.cu:150-205)"""
     x = _c(x, np.float32)
     M, C = x.shape
     rr = _c(r, np.float32).reshape(M, -1) if nparts else None
     xw = np.empty((M, C), np.float32)
     xn = np.empty((M, C), np.float32)
-    xo, Q, XS, XA = _prod_out(M, C)
+    xo, Q, XS, XA = _prod_out(M, C, hp)
     lib().or_rmsfold_q8(_p(x), C, _p(rr), rr.shape[1] if nparts else 0, nparts, _p(_c(w, np.float32)),
-                        _p(_c(sg, np.float32)), M, C, HB, _p(xw), C, _p(xn), C, _p(xo), C, _p(Q), C, _p(XS), _p(XA))
+                        _p(_c(sg, np.float32)), M, C, HB | (HP if hp else 0), _p(xw), C, _p(xn), C, _p(xo), C, _p(Q), C,
+                        _p(XS), _p(XA))
     return dict(xw=xw if nparts else None, xn=xn, xo=xo, Q=Q, XS=XS, XA=XA)
 
 
-def fold_q8(x, sg, HB):
+def fold_q8(x, sg, HB, hp=False):
     """k_fold_fwht_qT: x [M, C] -> dict xo, Q, XS, XA"""
     x = _c(x, np.float32)
     M, C = x.shape
-    xo, Q, XS, XA = _prod_out(M, C)
-    lib().or_fold_q8(_p(x), C, _p(_c(sg, np.float32)), M, C, HB, _p(xo), C, _p(Q), C, _p(XS), _p(XA))
+    xo, Q, XS, XA = _prod_out(M, C, hp)
+    lib().or_fold_q8(_p(x), C, _p(_c(sg, np.float32)), M, C, HB | (HP if hp else 0), _p(xo), C, _p(Q), C, _p(XS),
+                     _p(XA))
     return dict(xo=xo, Q=Q, XS=XS, XA=XA)
 
 
-def smfold_q8(a, b, sg, HB, perm=(1, 1, 1)):
+def smfold_q8(a, b, sg, HB, perm=(1, 1, 1), hp=False):
     """k_smfold_qT: SiLU(a) * b at the permuted columns (perm = (hd, nk, rep)) -> dict xo, Q, XS, XA"""
     a = _c(a, np.float32)
     b = _c(b, np.float32)
     M, C = a.shape
-    xo, Q, XS, XA = _prod_out(M, C)
-    lib().or_smfold_q8(_p(a), C, _p(b), C, _p(_c(sg, np.float32)), perm[0], perm[1], perm[2], M, C, HB, _p(xo), C,
+    xo, Q, XS, XA = _prod_out(M, C, hp)
+    lib().or_smfold_q8(_p(a), C, _p(b), C, _p(_c(sg, np.float32)), perm[0], perm[1], perm[2], M, C,
+                       HB | (HP if hp else 0), _p(xo), C,
                        _p(Q), C, _p(XS), _p(XA))
     return dict(xo=xo, Q=Q, XS=XS, XA=XA)

@@ -58,6 +58,9 @@ def test_validation_rejects_bad_shapes(lib):
     # C not a multiple of 128
     assert lib.kt_tern_pack(fake, fake, 64, 100, fake, None) == INVALID
     assert lib.kt_quant_q8(fake, 100, 1, 100, 0, fake, 112, fake, fake, None) == INVALID
+    assert lib.kt_quant_q8(fake, 128, 1, 128, 3, fake, 128, fake, fake, None) == INVALID   # modes 0, 1, 2 (hp)
+    assert lib.kt_tern_gemv(fake, 64, 256, fake, 256, fake, fake, (1 << 30) | (1 << 29) + 1, fake, 64, None,
+                            None) == INVALID                                               # hp token count
     # ldq not a multiple of 16
     assert lib.kt_tern_gemv(fake, 64, 256, fake, 260, fake, fake, 1, fake, 64, None, None) == INVALID
     # ldy < R

@@ -108,3 +108,32 @@ def test_smfold(lin, M, C, HB, perm):
     dq = np.abs(host(act.XQ).astype(np.int32) - want["Q"].astype(np.int32))
     assert dq.max() <= 1 and (dq > 0).mean() <= 1e-3
     assert np.allclose(host(act.XS), want["XS"], rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("M,C,HB", [(1, 5120, 1024), (3, 4096, 4096), (40, 5120, 1024), (2, 17408, 1024)])
+def test_producers_hp_bit_exact(lin, M, C, HB):
+    """the producers' two-row (hp) output (ff_q8 tcf.cu:150-205): rmsfold and fold bit-exact in every row, scale and
+    sum; smfold's rows follow its folded row (the exponential's last bit aside), so its two rows are checked against
+    the oracle's quantizer of the GPU's own folded row"""
+    say("producers hp", M, C, HB)
+    r = rng(C + 3 * M)
+    x = r.standard_normal((M, C)).astype(np.float32)
+    w = (1.0 + 0.1 * r.standard_normal(C)).astype(np.float32)
+    sg = signs(C, 11)
+    if C <= 8192:
+        want = orc.rmsfold_q8(x, None, 0, w, sg, HB, hp=True)
+        xo = torch.empty((M, C), dtype=torch.float32, device="cuda")
+        act = lin.rmsfold(dev(x), dev(w), dev(sg), HB, xo=xo, hp=True)
+        torch.cuda.synchronize()
+        assert act.hp and act.XQ.shape[0] == 2 * M and same(host(xo), want["xo"])
+        assert np.array_equal(host(act.XQ), want["Q"])
+        assert same(host(act.XS), want["XS"]) and np.array_equal(host(act.XA), want["XA"])
+    want = orc.fold_q8(x, sg, HB, hp=True)
+    act = lin.fold(dev(x), dev(sg), HB, hp=True)
+    assert np.array_equal(host(act.XQ), want["Q"])
+    assert same(host(act.XS), want["XS"]) and np.array_equal(host(act.XA), want["XA"])
+    b = r.standard_normal((M, C)).astype(np.float32)
+    xo = torch.empty((M, C), dtype=torch.float32, device="cuda")
+    act = lin.smfold(dev(x), dev(b), dev(sg), HB, xo=xo, hp=True)
+    Q, XS, XA = orc.quant_q8(host(xo), 3)
+    assert np.array_equal(host(act.XQ), Q) and same(host(act.XS), XS) and np.array_equal(host(act.XA), XA)

@@ -72,6 +72,51 @@ def test_gemv_m1(kt, R, C):
     assert np.array_equal(host(Y2), y)
 
 
+@pytest.mark.parametrize("M,C", [(1, 128), (5, 2048), (33, 17408)])
+def test_quantizer_hp_bit_exact(kt, M, C):
+    """the two-row (hp) quantizer (k_tc_q8 with hp, tc.cu:195-209): both rows, scales and sums bit-exact"""
+    lib, linear = kt
+    say("quant hp", M, C)
+    X = (rng(M + C).normal(0, 1, (M, C)) * np.exp(rng(M).normal(0, 2, (M, 1)))).astype(np.float32)
+    X[0, :128] = 0.0
+    act = linear.quantize(dev(X), hp=True)
+    Q, XS, XA = orc.quant_q8(X, 2)
+    assert act.hp and act.M == M and act.XQ.shape[0] == 2 * M
+    assert np.array_equal(host(act.XQ), Q) and np.array_equal(host(act.XS), XS) and np.array_equal(host(act.XA), XA)
+
+
+@pytest.mark.parametrize("R,C", [(640, 1024), (1024, 5120), (5120, 17408), (256, 24576)])
+def test_gemv_hp_pairs(kt, R, C):
+    """hp decode (tc.cu:405-407): token t's output is the fp32 sum of its two rows' results, row 2t first. Every row's
+    result does not depend on M, so the hp product must equal, bit for bit, the one-row product of the same 2M rows
+    with each pair added; checked at 1 .. 16 tokens (2 .. 32 rows: the v_dot4 chunks and both matrix-core kernels)
+    and against the oracle's tree"""
+    lib, linear = kt
+    say("gemv hp", R, C)
+    W, dig, bc, dpm = upload(linear, R, C, 7 * R + C)
+    L = linear.Linear({"w": W})
+    X = rng(R + C).normal(0, 1, (16, C)).astype(np.float32)
+    Q, XS, XA = orc.quant_q8(X, 2)
+    acc = orc.tern_acc(bc, R, C, Q)
+    dq = dpm.view(np.float16).astype(np.float32)
+    tree = orc.out_lanes(acc, XS, dq, 8, 0, lib.kt_decode_kslices(C, 0))
+    want = (tree[0::2] + tree[1::2]).astype(np.float32)
+    xd = dev(X)
+    for M in (1, 2, 3, 4, 5, 8, 16):
+        say("  M", M)
+        act = linear.quantize(xd[:M], hp=True)
+        Y = torch.full((M, R), float("nan"), dtype=torch.float32, device="cuda")
+        dbg = torch.empty((2 * M, R, C // 128), dtype=torch.int32, device="cuda")
+        L.gemv_q(["w"], act, [Y], dbg=dbg)
+        assert np.array_equal(host(dbg), acc[:2 * M]), M
+        assert np.array_equal(host(Y), want[:M]), M
+        rows = linear.Act(act.XQ, act.XS, act.XA, 2 * M, C, False)          # the same rows without hp
+        Y2 = torch.empty((2 * M, R), dtype=torch.float32, device="cuda")
+        L.gemv_q(["w"], rows, [Y2])
+        y2 = host(Y2)
+        assert np.array_equal(host(Y), (y2[0::2] + y2[1::2]).astype(np.float32)), M
+
+
 @pytest.mark.parametrize("R,C", [(640, 1024), (2048, 6144), (4096, 4096)])
 def test_gemv_token_invariance(kt, R, C):
     """a token's output does not depend on how many tokens share the pass (tc_hip.cu:14-15), for M = 1 .. 32: the

@@ -136,6 +136,52 @@ def test_quant_per_row_matches_reference_on_uniform_groups(orc):
     assert all(np.array_equal(a, b) for a, b in zip(orc.quant_q8(X), orc.quant_q8(X, per_row=True)))
 
 
+@pytest.mark.parametrize("mode", [2, 3])
+def test_quant_hp_two_rows(orc, mode):
+    """hp (tc.cu:195-209 mode 2; tcf.cu:150-205 mode 3): row 2n is the plain per-group row bit for bit; row 2n + 1
+    stays within +-127, and together they rebuild x to within half a residual step (x - q XS - q2 XS2 is the
+    residual's own rounding, about 14 bits of precision instead of 8); an all-zero group gives zeros; the two modes'
+    residual scales agree to 2 ulp (amax / 254 / 127 against amax / 32258)"""
+    r = rng(40 + mode)
+    X = (r.standard_normal((5, 512)) * np.exp(r.normal(0, 2, (5, 1)))).astype(np.float32)
+    X[3, 128:256] = 0.0
+    X[4, 0] = 1e-30                                 # a tiny amax
+    Q, XS, XA = orc.quant_q8(X, mode)
+    Q0, XS0, XA0 = orc.quant_q8(X)
+    assert Q.shape == (10, 512)
+    assert np.array_equal(Q[0::2], Q0) and np.array_equal(XS[0::2], XS0) and np.array_equal(XA[0::2], XA0)
+    q2 = Q[1::2].astype(np.int64)
+    assert np.abs(q2).max() <= 127 and np.abs(q2).max() >= 120      # the residual row uses its range
+    assert np.array_equal(XA[1::2], q2.reshape(5, 4, 128).sum(2))
+    xs, xs2 = np.repeat(XS[0::2], 128, 1).astype(np.float64), np.repeat(XS[1::2], 128, 1).astype(np.float64)
+    rec = Q[0::2].astype(np.float64) * xs + q2 * xs2
+    err = np.abs(rec - X.astype(np.float64))
+    amax = np.repeat(np.abs(X).reshape(5, 4, 128).max(2), 128, 1).astype(np.float64)
+    assert (err <= 0.5 * xs2 * 1.01 + 1e-6 * amax).all()
+    assert (err.max(1) < np.abs(X.astype(np.float64) - Q0.astype(np.float64) * xs).max(1) / 50).all()
+    assert (Q[6, 128:256] == 0).all() and (Q[7, 128:256] == 0).all() and XS[7, 1] == 0 and XA[7, 1] == 0
+    a = np.abs(X).reshape(5, 4, 128).max(2)
+    other = (a / np.float32(254) / np.float32(127)) if mode == 3 else (a / np.float32(32258))
+    assert np.all(np.abs(XS[1::2] - other) <= 2 * np.spacing(XS[1::2]))
+
+
+def test_producers_hp(orc):
+    """the producers' two-row output is their folded row xo through the mode-3 quantizer, and its even rows are the
+    one-row producer's int8 row"""
+    M, C, HB = 3, 4096, 1024
+    r = rng(45)
+    x = r.standard_normal((M, C)).astype(np.float32)
+    w = (1.0 + 0.1 * r.standard_normal(C)).astype(np.float32)
+    sg = np.where(r.random(C) < 0.5, -1.0, 1.0).astype(np.float32)
+    for d, d1 in ((orc.rmsfold_q8(x, None, 0, w, sg, HB, hp=True), orc.rmsfold_q8(x, None, 0, w, sg, HB)),
+                  (orc.fold_q8(x, sg, HB, hp=True), orc.fold_q8(x, sg, HB)),
+                  (orc.smfold_q8(x, x[::-1].copy(), sg, HB, hp=True), orc.smfold_q8(x, x[::-1].copy(), sg, HB))):
+        assert np.array_equal(d["xo"], d1["xo"])
+        Q, XS, XA = orc.quant_q8(d["xo"], 3)
+        assert np.array_equal(Q, d["Q"]) and np.array_equal(XS, d["XS"]) and np.array_equal(XA, d["XA"])
+        assert np.array_equal(d["Q"][0::2], d1["Q"]) and np.array_equal(d["XS"][0::2], d1["XS"])
+
+
 # ------------------------------------------------------------------------------------------- ternary products
 def test_tern_acc_brute_force(orc):
     """the exact group values equal an int64 matmul of the decoded trits (sum (d - 1) q, tc_hip.cu:12-15)"""
