@@ -400,6 +400,50 @@ def cpu_baseline(synth, runs=5, run_s=2.0):
     return out
 
 
+def cpu_child_moe(orc, runs, run_s, nsets=16):
+    """config 4 at one token on the host with the reference's q8_0 kernel (dsv41_cpu.c k_q8g, oracle/_ref): per token
+    its 6 experts' up products, relu^2 and the reference's quantizer (quant_q8), their down products. nsets sets of 6
+    experts rotate (1 GB of q8_0 weights: copies of one generated set at distinct addresses, beyond the host's
+    caches) so the sample streams from DRAM."""
+    import numpy as np
+    from kindi_amd import synth
+    c = synth.CFG["c4"]
+    k, H, F = c["k"], c["H"], c["F"]
+    up0 = [orc.q8_0_group4(synth.q8_rows(F, H, 40_000 + e).numpy(), F, H) for e in range(k)]
+    down0 = [orc.q8_0_group4(synth.q8_rows(H, F, 50_000 + e).numpy(), H, F) for e in range(k)]
+    ups = [up0[e % k].copy() for e in range(k * nsets)]
+    downs = [down0[e % k].copy() for e in range(k * nsets)]
+    x = np.random.default_rng(42).normal(0, 1, H).astype(np.float32)
+    u = np.empty(F, np.float32)
+    yd = np.empty(H, np.float32)
+    nbytes = k * (F * H + H * F) * 34 // 32
+
+    def token(i):
+        q, d = orc.ref_quant_q8(x)
+        for e in range(k * (i % nsets), k * (i % nsets) + k):
+            orc.ref_q8_matvec(ups[e], F, H, q, d, u)
+            r = np.maximum(u, np.float32(0))
+            q2, d2 = orc.ref_quant_q8(r * r)
+            orc.ref_q8_matvec(downs[e], H, F, q2, d2, yd)
+
+    for i in range(nsets):
+        token(i)
+    rates = []
+    for _ in range(runs):
+        n, t0 = 0, time.perf_counter()
+        while n < nsets or time.perf_counter() - t0 < run_s:
+            token(n)
+            n += 1
+        rates.append(n / (time.perf_counter() - t0))
+    rates.sort()
+    med = rates[len(rates) // 2]
+    return {"value": round(nbytes * med / 1e9, 2), "unit": "GB/s", "us_per_token": round(1e6 / med, 1),
+            "runs_GBs": [round(nbytes * r / 1e9, 2) for r in rates],
+            "sample": "config 4 at M=1 (6 experts: up [1856x2688] q8_0 product, relu^2 + quant_q8, down [2688x1856]; "
+                      "%.1f MB of q8_0 weights a token, %d expert sets rotating): dsv41_cpu.c k_q8g over OpenMP "
+                      "threads, median of %d runs" % (nbytes / 1e6, nsets, runs)}
+
+
 def cpu_child(runs, run_s, nlayers=4):
     """the measurement cpu_baseline starts: nlayers distinct layers (352 MB of codes) rotate so the sample streams
     from DRAM rather than the host's caches"""
@@ -444,6 +488,7 @@ def cpu_child(runs, run_s, nlayers=4):
         passes += reps
         total += el
     rates.sort()
+    moe = cpu_child_moe(orc, runs, run_s / 2) if orc.ref_dsv41() is not None else None
     threads = int(os.environ.get("OMP_NUM_THREADS", "0"))
     model = ""
     try:
@@ -461,6 +506,7 @@ def cpu_child(runs, run_s, nlayers=4):
         "kind": "reference" if ref else "port", "runs_GBs": [round(nbytes * x / 1e9, 2) for x in rates],
         "omp": "OMP_NUM_THREADS=%d (physical cores allowed) OMP_PROC_BIND=%s OMP_PLACES=%s" % (
             threads, os.environ.get("OMP_PROC_BIND"), os.environ.get("OMP_PLACES")),
+        "moe_c4": moe,
         "sample": "median of %d runs (%d layer passes in %.1f s after a warm-up) of the 27B-class decode (q,k,v,o,gate,"
                   "up,down; %.1f MB of ternary weights per layer, %d distinct layers rotating): fp32 pair-table GEMV "
                   "(kcpu.c gemv), %d OpenMP threads. value counts the GPU line's algorithmic bytes per layer (the same "

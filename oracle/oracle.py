@@ -372,6 +372,7 @@ def ref_dsv41():
             h = ctypes.CDLL(REF_DSV41)
             h.ref_quant_q8.argtypes = [P, I, P, P]
             h.ref_k_q8g.argtypes = [P, I, I, P, P, I, P, I]
+            h.ref_q8_matvec.argtypes = [P, I, I, I, P, P, P, I]
         _ref["dsv41"] = h
     return _ref["dsv41"]
 
@@ -398,6 +399,13 @@ def ref_quant_q8(x):
     d = np.empty(x.size // 32, np.float32)
     h.ref_quant_q8(_p(x), x.size, _p(q), _p(d))
     return q, d
+
+
+def ref_q8_matvec(g4, R, C, q, d, y):
+    """every 4-row group of one matrix through k_q8g (the reference's AVX2 q8_0 kernel), threads over groups; q, d one
+    token's int8 row and block scales (quant_q8); y fp32 [R]"""
+    ref_dsv41().ref_q8_matvec(_p(g4), R, C, 1, _p(q), _p(d), _p(y), 1)
+    return y
 
 
 def ref_k_q8g(g4, R, C, q, d):

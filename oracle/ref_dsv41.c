@@ -11,3 +11,13 @@ void ref_quant_q8(const float* x, int n, int8_t* q, float* d){ quant_q8(x, n, q,
 void ref_k_q8g(const uint8_t* w, int nb, int T, const int8_t* xq, const float* xd, int xs, float* y, int ys){
   k_q8g(w, nb, T, xq, xd, xs, y, ys);
 }
+
+/* a whole matrix through k_q8g: R / 4 row groups of the repacked layout (nb = C / 32 blocks each), T tokens, the
+   groups split over OpenMP threads (this driver is ours; each group's arithmetic is the reference's kernel). Used
+   as the q8_0 CPU baseline beside the MoE products. */
+void ref_q8_matvec(const uint8_t* g4, int R, int C, int T, const int8_t* xq, const float* xd, float* y, int ys){
+  const int nb = C / 32, ng = R / 4;
+  #pragma omp parallel for schedule(static)
+  for(int g = 0; g < ng; ++g)
+    k_q8g(g4 + (size_t)g * nb * 136, nb, T, xq, xd, C, y + (size_t)g * 4, ys);
+}
