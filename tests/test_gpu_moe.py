@@ -53,18 +53,20 @@ def test_q8_gemv(kt, R, C, M):
     assert max_rel(y, orc.q8_out(acc, rows, R, C, d)) < TOL
 
 
+@pytest.mark.parametrize("R", [96, 100])
 @pytest.mark.parametrize("C", [512, 1024, 1536, 2688, 3584, 4096])
-def test_grouped_mma_widths(kt, C):
+def test_grouped_mma_widths(kt, C, R):
     """the grouped matrix-core q8_0 product (16 entries an expert on average) at widths of 1 to 8 K slices: one slice
     a wave (up to 2 slices) and two waves taking the slices in turn (3 to 8, odd counts included). int32 unit values
     exact against the oracle, and every expert's rows bit-identical to the dense product of the same tokens"""
     lib, moe = kt
-    E, k, M, R = 16, 4, 64, 96
-    say("grouped mma", C, "KS", lib.kt_decode_kslices(C, 1))
+    E, k, M = 16, 4, 64
+    say("grouped mma", R, C, "KS", lib.kt_decode_kslices(C, 1))
     rows = [q8_case(R, C, 300 + e)[0] for e in range(E)]
     ups = moe.Q8Experts(rows, R, C)
-    downs = moe.Q8Experts([q8_case(C, R, 400 + e)[0] for e in range(E)], C, R)
-    layer = moe.MoE(ups, downs, k)
+    # the token lists depend on the ids and E only: a layer of small placeholder experts makes them
+    layer = moe.MoE(moe.Q8Experts([q8_case(32, 32, e)[0] for e in range(E)], 32, 32),
+                    moe.Q8Experts([q8_case(32, 32, 50 + e)[0] for e in range(E)], 32, 32), k)
     r = rng(C)
     ids = np.stack([r.permutation(E)[:k] for _ in range(M)]).astype(np.int32)
     lists = layer.lists(dev(ids))

@@ -356,24 +356,38 @@ def test_gemm_config2_sampled(kt, R, C, M):
     assert max_rel(host(Yd), y[:16]) < 1e-5
 
 
-@pytest.mark.parametrize("R,C", [(8, 128), (24, 384), (200, 1152), (64, 896)])
+@pytest.mark.parametrize("R,C", [(8, 128), (24, 384), (200, 1152), (64, 896), (100, 2944), (1000, 1408)])
 def test_gemv_ragged_units(kt, R, C):
-    """widths whose group count is not a multiple of 8 (a partial last step) and row counts of one row group"""
+    """widths whose group count is not a multiple of 8 (a partial last step), row counts of one row group and rows
+    that end inside a 32-row tile, at every decode kernel's token counts (v_dot4 chunks 1 .. 5, the 32x32x32
+    matrix-core kernel at 6 .. 8, the 16x16x64 one above 8) and in the two-row (hp) form"""
     lib, linear = kt
     say("gemv ragged", R, C)
     W, dig, bc, dpm = upload(linear, R, C, 7 * R + C)
     L = linear.Linear({"w": W})
-    X = rng(R).normal(0, 1, (3, C)).astype(np.float32)
-    act = linear.quantize(dev(X))
-    Y = torch.empty((3, R), dtype=torch.float32, device="cuda")
-    dbg = torch.empty((3, R, C // 128), dtype=torch.int32, device="cuda")
-    L.gemv_q(["w"], act, [Y], dbg=dbg)
+    X = rng(R).normal(0, 1, (32, C)).astype(np.float32)
     Q, XS, XA = orc.quant_q8(X)
     acc = orc.tern_acc(bc, R, C, Q)
-    assert np.array_equal(host(dbg), acc)
-    assert np.array_equal(host(Y), orc.out_lanes(acc, XS, dpm.view(np.float16).astype(np.float32), 8, 0, lib.kt_decode_kslices(C, 0)))
+    dq = dpm.view(np.float16).astype(np.float32)
+    tree = orc.out_lanes(acc, XS, dq, 8, 0, lib.kt_decode_kslices(C, 0))
+    xd = dev(X)
+    for M in (1, 3, 6, 8, 9, 13, 16, 32):
+        act = linear.quantize(xd[:M])
+        Y = torch.full((M, R), float("nan"), dtype=torch.float32, device="cuda")
+        dbg = torch.empty((M, R, C // 128), dtype=torch.int32, device="cuda")
+        L.gemv_q(["w"], act, [Y], dbg=dbg)
+        assert np.array_equal(host(dbg), acc[:M]), M
+        assert np.array_equal(host(Y), tree[:M]), M
+    act = linear.quantize(xd[:3])
     Yp = L.gemm("w", act)
-    assert np.array_equal(host(Yp), orc.tern_out(acc, XS, dpm, R, C))
+    assert np.array_equal(host(Yp), orc.tern_out(acc[:3], XS[:3], dpm, R, C))
+    Qh, XSh, XAh = orc.quant_q8(X[:16], 2)
+    th = orc.out_lanes(orc.tern_acc(bc, R, C, Qh), XSh, dq, 8, 0, lib.kt_decode_kslices(C, 0))
+    for M in (1, 3, 5, 16):                                     # hp: 2 .. 32 rows
+        act = linear.quantize(xd[:M], hp=True)
+        Y = torch.full((M, R), float("nan"), dtype=torch.float32, device="cuda")
+        L.gemv_q(["w"], act, [Y])
+        assert np.array_equal(host(Y), (th[0:2 * M:2] + th[1:2 * M:2]).astype(np.float32)), M
 
 
 def test_gemv_full_size_linearity(kt):
