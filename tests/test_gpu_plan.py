@@ -121,3 +121,42 @@ def test_plan_stage_reads_earlier_output(linear, synth, M):
         assert plan.status() == 0
         for i in range(4):
             assert np.array_equal(host(outs[i]).view(np.uint32), host(ref[i]).view(np.uint32)), (rep, i)
+
+
+@pytest.mark.parametrize("M", [1, 2])
+def test_plan_graph_replays(linear, synth, M):
+    """the plan run (its reset kernel and the plan kernel) captured in a HIP graph and replayed with new activations
+    quantized eagerly between replays: every replay equals the single launches on the same inputs"""
+    say("plan graph M=%d" % M)
+    shapes = [("q", 256, 1024), ("k", 64, 1024), ("v", 64, 1024), ("o", 1024, 256), ("gate", 512, 1024),
+              ("up", 512, 1024), ("down", 1024, 512)]
+    stages, _ = _layer_stages(linear, synth, shapes, 2, M, 900)
+    plan = linear.Plan(stages)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        plan.run()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        plan.run()
+    torch.cuda.synchronize()
+    L = linear.Linear({})
+    for it in range(4):
+        for k, (mats, act, outs) in enumerate(stages):         # new inputs, quantized into the stages' buffers
+            x = synth.activations(M, act.C, 5000 + 10 * it + k, device="cuda")
+            linear.quantize(x, out=act)
+        a = torch.randn((256, 256), device="cuda")
+        (a @ a).sum().item()
+        g.replay()
+        torch.cuda.synchronize()
+        assert plan.status() == 0, it
+        for k, (mats, act, outs) in enumerate(stages):
+            for i, m in enumerate(mats):
+                L.add("m", m)
+                ref = torch.empty_like(outs[i])
+                L.gemv_q(["m"], act, [ref])
+                torch.cuda.synchronize()
+                assert np.array_equal(host(outs[i]).view(np.uint32), host(ref).view(np.uint32)), (it, k, i)
