@@ -583,7 +583,7 @@ def main():
         nlaunch, kernel = 1, "k_plan<1> (decode plan, %d stages, grid %d x %d waves)" % (
             len(stages), plan.info.grid, plan.info.waves + 1)
     else:
-        ms, nlaunch, kernel = ms_l, len(calls), "k_gemv_flat1<ternary,MT=1> (q/k/v, o, down) + k_gemv_pair (gate/up)"
+        ms, nlaunch, kernel = ms_l, len(calls), "k_gemv_step<1> (q/k/v, o) + k_gemv_step<2> (gate/up) + k_gemv_flat1 (down)"
     gbs = nbytes / ms / 1e6
     # the dominant kernel is the whole step (plan) or every launch of it (launches, back to back in the graph): its
     # average duration is the timed region over the launch count (an upper bound: it includes the gaps)

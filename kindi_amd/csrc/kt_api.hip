@@ -15,6 +15,8 @@ __global__ void k_gemv_flat(const KtGemvArgs, const KtGroupedArgs, const int8_t*
 template <int FMT, int MT, bool DBG, bool GRP>
 __global__ void k_gemv_flat1(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, const int*, int32_t*,
                              int);
+template <int RG, bool DBG>
+__global__ void k_gemv_step(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
 template <bool DBG>
 __global__ void k_gemv_pair(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
 template <int NT, bool DBG, int LB>
@@ -123,6 +125,23 @@ static int kt_launch_gemv(const KtGemvArgs& a, int ngroups, const int8_t* xq, co
   const int ks = kt_kslices(a.NU);
   bool even = true;
   for(int i = 0; i < a.nmat; ++i) even = even && kt_r8(a.mat[i].R) % 2 == 0;
+  if(FMT == KT_FMT_TERN && a.M == 1 && kt_steps(a.NU) <= 8){
+    /* one step a wave (rows of up to 8 steps, the same tree), two row groups a block where the one-row-group grid
+       exceeds the wave slots (measured on MI355X, 27B-class one-token launches against two steps a wave: gate/up
+       11.5 -> 10.9 us, q/k/v 5.6 -> 5.1 us, o 5.0 -> 4.7 us; step 1.91 -> 1.81 ms). Wider rows (the 27B down
+       projection: 17 steps) stay on k_gemv_flat1: 16-wave blocks of one step each were slower there */
+    const int S = kt_steps(a.NU);
+    const bool two = even && (long long)ngroups * ks > KT_PAIR_WAVES;
+    const size_t lds = (size_t)S * KT_KL * KtFlat<KT_FMT_TERN, 1>::UP + (size_t)(two ? 2 : 1) * S * 64 * 4 * 2;
+    const dim3 block(64 * S);
+#define KT_ST(RG) do { const dim3 grid(ngroups / RG); \
+    if(dbg) hipLaunchKernelGGL((k_gemv_step<RG, true>), grid, block, lds, s, a, xq, xs, xa, dbg, ks); \
+    else hipLaunchKernelGGL((k_gemv_step<RG, false>), grid, block, lds, s, a, xq, xs, xa, dbg, ks); } while(0)
+    if(two) KT_ST(2); else KT_ST(1);
+#undef KT_ST
+    KT_LAUNCH_CHECK();
+    return 0;
+  }
   if(FMT == KT_FMT_TERN && a.M == 1 && even && (long long)ngroups * ks > KT_PAIR_WAVES && kt_steps(a.NU) <= KT_SL * ks){
     /* one token on a grid too large for the wave slots: two row groups a block, one round of blocks */
     const dim3 grid(ngroups / 2), block(64 * ks);

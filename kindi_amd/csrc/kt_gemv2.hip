@@ -140,3 +140,92 @@ k_gemv_pair(const KtGemvArgs a, const int8_t* __restrict__ xq, const float* __re
 
 template __global__ void k_gemv_pair<false>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
 template __global__ void k_gemv_pair<true>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
+
+/* ------------------------------------------------------------------ one step a wave
+   k_gemv_step: the one-token ternary product for rows of up to 8 steps (C <= 8192) with the work of a K slice split
+   over its steps: wave j of a block takes step j (8 units) of RG row groups (RG = 2: the pair kernel's grid, for
+   launches too large for the wave slots). It loads its step's codes, scales and activation row (one memory round
+   trip, half of a two-step slice's bytes, so the wave finishes sooner), computes each lane's exact unit value as
+   k_gemv_flat1 does, and writes (float)(v - XA) and XS d (the same product k_gemv_flat1 forms) to LDS. After one
+   block barrier wave 0 runs, for every K slice (kt_decode_kslices, unchanged), each lane's chain over the slice's
+   steps in order, fmaf(f, m, 0) then fmaf(f, m, acc), the xor butterfly and the slice sums left to right: the same
+   operations in the same order as k_gemv_flat1, so the same bits. */
+template <int RG, bool DBG>
+__global__ void __launch_bounds__(64 * 8) __attribute__((amdgpu_waves_per_eu(8)))
+k_gemv_step(const KtGemvArgs a, const int8_t* __restrict__ xq, const float* __restrict__ xs,
+            const int* __restrict__ xa, int32_t* __restrict__ dbg, int KS){
+  extern __shared__ __attribute__((aligned(16))) uint8_t kt_lds[];
+  using F = KtFlat<KT_FMT_TERN, 1>;
+  constexpr int UW = F::UW, UP = F::UP;
+  const int NU = a.NU, S = kt_steps(NU);
+  const int lane = threadIdx.x & 63, j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), r = lane & 7, c = lane >> 3;
+  uint8_t* xw = kt_lds + (size_t)j * KT_KL * UP;                    /* this wave's step: [8 units][UP] */
+  float* fv = (float*)(kt_lds + (size_t)S * KT_KL * UP);            /* [RG][S][64]: (float)(v - XA) */
+  float* mv = fv + RG * S * 64;                                     /* [RG][S][64]: XS d */
+
+  /* the block's row groups are in one matrix (RG = 2: every matrix has an even number of row groups, the launcher
+     checks) */
+  const int g = RG * blockIdx.x;
+  int mi = 0;
+  if(a.nmat > 1 && g >= a.mat[1].rg0) mi = 1;
+  if(a.nmat > 2 && g >= a.mat[2].rg0) mi = 2;
+  const KtMat& m = a.mat[mi];
+  const int rg0 = g - m.rg0, R = m.R;
+  const uint4* wb = (const uint4*)m.codes;
+  const uint16_t* sb = m.scales;
+  const int u = j * KT_KL + c;
+  const bool uok = u < NU;
+  const unsigned o0 = uok ? (unsigned)kt_widx(NU, rg0, j, 0, c, r) : 0u;
+  const unsigned o1 = uok ? (unsigned)kt_widx(NU, rg0, j, 1, c, r) : 0u;
+  const unsigned os = uok ? (unsigned)kt_sidx(NU, rg0, uok ? u : 0, r) : 0u;
+  KtStep w[RG];
+#pragma unroll
+  for(int q = 0; q < RG; ++q){                                      /* row group rg0 + q: one row group further */
+    w[q].c0 = kt_ldnt(wb + (long long)q * NU * 16 + o0);
+    w[q].c1 = kt_ldnt(wb + (long long)q * NU * 16 + o1);
+    w[q].hs = sb[(long long)q * NU * 8 + os];
+  }
+  /* the step's activation row (token 0): each lane's 16 bytes, its unit's scale and sum */
+  const int nc = NU - j * KT_KL < KT_KL ? NU - j * KT_KL : KT_KL;
+  const int o = lane * 16, oc = o < nc * UW ? o : 0;
+  uint4 stg = *(const uint4*)(xq + (long long)j * KT_KL * UW + oc);
+  uint32_t sa[2] = {__float_as_uint(xs[uok ? u : 0]), (uint32_t)xa[uok ? u : 0]};
+  kt_pin<1>(&stg, sa);
+  *(uint4*)(xw + (o / UW) * UP + o % UW) = stg;
+  kt_wave_sync();
+  int vv[2];
+  if(RG == 2) kt_unit2_lds(w[0].c0, w[0].c1, w[1].c0, w[1].c1, xw + (uok ? c : 0) * UP, vv);
+  else vv[0] = kt_unit_lds<KT_FMT_TERN>(w[0].c0, w[0].c1, xw + (uok ? c : 0) * UP);
+#pragma unroll
+  for(int q = 0; q < RG; ++q){
+    const float d = uok ? kt_h2f(w[q].hs) : 0.0f;
+    const int v = uok ? vv[q] - (int)sa[1] : 0;
+    fv[(q * S + j) * 64 + lane] = (float)v;
+    mv[(q * S + j) * 64 + lane] = __uint_as_float(sa[0]) * d;
+    const int row = (rg0 + q) * KT_RG + r;
+    if(DBG && uok && row < R) dbg[(long long)row * NU + u] = v;
+  }
+  __syncthreads();
+  if(j == 0){
+#pragma unroll
+    for(int q = 0; q < RG; ++q){
+      float tot = 0.0f;
+      for(int k = 0; k < KS; ++k){                                  /* uniform */
+        const int s_lo = k * S / KS, ns = (k + 1) * S / KS - s_lo;
+        const float* f = fv + (q * S + s_lo) * 64 + lane;
+        const float* mm = mv + (q * S + s_lo) * 64 + lane;
+        float acc = fmaf(f[0], mm[0], 0.0f);
+        if(ns > 1) acc = fmaf(f[64], mm[64], acc);
+        const float y = kt_row_sum(acc);
+        tot = k == 0 ? y : tot + y;
+      }
+      const int row = (rg0 + q) * KT_RG + r;
+      if(c == 0 && row < R) m.y[row] = tot;
+    }
+  }
+}
+
+template __global__ void k_gemv_step<1, false>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
+template __global__ void k_gemv_step<1, true>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
+template __global__ void k_gemv_step<2, false>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
+template __global__ void k_gemv_step<2, true>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);

@@ -43,7 +43,10 @@ def test_quantizer_bit_exact(kt, M, C, per_row):
     assert np.array_equal(host(act.XA), XA)
 
 
-SHAPES = [(64, 128), (100, 256), (6144, 2048), (1024, 5120), (2048, 6144), (5120, 17408)]
+# one token: k_gemv_step (up to 8 steps: C <= 8192; two row groups a block on large grids), k_gemv_flat1 (wider),
+# k_gemv_pair (wider rows on grids beyond the wave slots: 10240 x 12288)
+SHAPES = [(64, 128), (100, 256), (6144, 2048), (1024, 5120), (2048, 6144), (5120, 17408), (34816, 5120),
+          (10240, 12288)]
 
 
 @pytest.mark.parametrize("R,C", SHAPES)
