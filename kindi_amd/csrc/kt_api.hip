@@ -17,6 +17,9 @@ __global__ void k_gemv_flat1(const KtGemvArgs, const KtGroupedArgs, const int8_t
                              int);
 template <int RG, bool DBG>
 __global__ void k_gemv_step(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
+template <int MT, bool DBG>
+__global__ void k_gemv_stepm(const KtGemvArgs a, const int8_t* __restrict__ xq, const float* __restrict__ xs,
+                             const int* __restrict__ xa, int32_t* __restrict__ dbg, int KS);
 template <bool DBG>
 __global__ void k_gemv_pair(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
 template <int NT, bool DBG, int LB>
@@ -55,6 +58,7 @@ size_t kt_moe1_down_lds(int k, int KS);
 
 #define KT_INVALID ((int)hipErrorInvalidValue)
 #ifndef KT_PAIR_WAVES
+#define KT_STEPM_WAVES 2048           /* multi-token grids of at most this many one-step waves take k_gemv_stepm */
 #define KT_PAIR_WAVES 6144             /* one-token grids of more waves take two row groups a block (k_gemv_pair) */
 #endif
 #define KT_RS_ROWS 8192                /* per-row prefill on small blocks below this many rows */
@@ -139,6 +143,23 @@ static int kt_launch_gemv(const KtGemvArgs& a, int ngroups, const int8_t* xq, co
     else hipLaunchKernelGGL((k_gemv_step<RG, false>), grid, block, lds, s, a, xq, xs, xa, dbg, ks); } while(0)
     if(two) KT_ST(2); else KT_ST(1);
 #undef KT_ST
+    KT_LAUNCH_CHECK();
+    return 0;
+  }
+  if(FMT == KT_FMT_TERN && a.M > 1 && kt_steps(a.NU) <= 8 && (long long)ngroups * kt_steps(a.NU) <= KT_STEPM_WAVES){
+    /* 2-5 tokens (the two-row form included), one step a wave, on grids that leave the CUs short of waves: 8 a CU
+       or fewer once split (measured on MI355X, 2B-class launches at 4 tokens against k_gemv_flat: q/k/v 5.40 ->
+       4.90 us, o 5.21 -> 4.66 us; the larger gate/up grid was slower split, 5.93 -> 6.25 us, and stays on
+       k_gemv_flat) */
+    const int S = kt_steps(a.NU), mt = a.M <= 2 ? 2 : 4;
+    const size_t lds = (size_t)S * mt * KT_KL * KtFlat<KT_FMT_TERN, 1>::UP + (size_t)S * mt * 64 * 4 * 2;
+    const dim3 grid(ngroups), block(64 * S);
+#define KT_STM(MT) do { \
+    if(dbg) hipLaunchKernelGGL((k_gemv_stepm<MT, true>), grid, block, lds, s, a, xq, xs, xa, dbg, ks); \
+    else hipLaunchKernelGGL((k_gemv_stepm<MT, false>), grid, block, lds, s, a, xq, xs, xa, dbg, ks); } while(0)
+    if(mt == 2) KT_STM(2);
+    else KT_STM(4);
+#undef KT_STM
     KT_LAUNCH_CHECK();
     return 0;
   }

@@ -229,3 +229,120 @@ template __global__ void k_gemv_step<1, false>(const KtGemvArgs, const int8_t*, 
 template __global__ void k_gemv_step<1, true>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
 template __global__ void k_gemv_step<2, false>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
 template __global__ void k_gemv_step<2, true>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
+
+/* ------------------------------------------------------------------ one step a wave, several tokens
+   k_gemv_stepm: k_gemv_step for 2-5 tokens (the launcher's range below the matrix-core kernels; with the two-row form
+   a token's two rows are adjacent tokens here). Wave j loads step j's codes and scales of its row group once and
+   serves the tokens in chunks of MT: it stages the chunk's activation rows of its step, computes each lane's exact
+   unit value per token as k_gemv_flat does, and writes (float)(v - XA) and XS d to LDS. After a block barrier wave 0
+   runs, per token, every K slice's chain over its steps in order, the xor butterfly and the slice sums left to right:
+   k_gemv_flat's operations in its order, so the same bits. With hp the chunk's row pairs (MT is even, so a pair never
+   straddles two chunks) are added in the store. 4 waves a SIMD (76 VGPRs, no spills; 8 a SIMD spilled). */
+template <int MT, bool DBG>
+__global__ void __launch_bounds__(64 * 8) __attribute__((amdgpu_waves_per_eu(4)))
+k_gemv_stepm(const KtGemvArgs a, const int8_t* __restrict__ xq, const float* __restrict__ xs,
+            const int* __restrict__ xa, int32_t* __restrict__ dbg, int KS){
+  constexpr int RG = 1;
+  extern __shared__ __attribute__((aligned(16))) uint8_t kt_lds[];
+  using F = KtFlat<KT_FMT_TERN, MT>;
+  constexpr int UW = F::UW, UP = F::UP;
+  const int NU = a.NU, S = kt_steps(NU), M = a.M;
+  const int lane = threadIdx.x & 63, j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), r = lane & 7, c = lane >> 3;
+  uint8_t* xw = kt_lds + (size_t)j * MT * KT_KL * UP;               /* this wave's step: [MT][8 units][UP] */
+  float* fv = (float*)(kt_lds + (size_t)S * MT * KT_KL * UP);       /* [RG][S][MT][64]: (float)(v - XA) */
+  float* mv = fv + RG * S * MT * 64;                                /* [RG][S][MT][64]: XS d */
+
+  /* the block's row groups are in one matrix (RG = 2: every matrix has an even number of row groups, the launcher
+     checks) */
+  const int g = RG * blockIdx.x;
+  int mi = 0;
+  if(a.nmat > 1 && g >= a.mat[1].rg0) mi = 1;
+  if(a.nmat > 2 && g >= a.mat[2].rg0) mi = 2;
+  const KtMat& m = a.mat[mi];
+  const int rg0 = g - m.rg0, R = m.R;
+  const uint4* wb = (const uint4*)m.codes;
+  const uint16_t* sb = m.scales;
+  const int u = j * KT_KL + c;
+  const bool uok = u < NU;
+  const int uu = uok ? u : 0;
+  const unsigned o0 = uok ? (unsigned)kt_widx(NU, rg0, j, 0, c, r) : 0u;
+  const unsigned o1 = uok ? (unsigned)kt_widx(NU, rg0, j, 1, c, r) : 0u;
+  const unsigned os = uok ? (unsigned)kt_sidx(NU, rg0, u, r) : 0u;
+  KtStep w[RG];
+#pragma unroll
+  for(int q = 0; q < RG; ++q){                                      /* row group rg0 + q: one row group further */
+    w[q].c0 = kt_ldnt(wb + (long long)q * NU * 16 + o0);
+    w[q].c1 = kt_ldnt(wb + (long long)q * NU * 16 + o1);
+    w[q].hs = sb[(long long)q * NU * 8 + os];
+  }
+  const int nc = NU - j * KT_KL < KT_KL ? NU - j * KT_KL : KT_KL;
+  const int o = lane * 16, oc = o < nc * UW ? o : 0;                /* the lane's 16 bytes of the step's row */
+  for(int t0 = 0; t0 < M; t0 += MT){                               /* uniform */
+    const int nt = min(MT, M - t0);
+    uint4 stg[MT];
+    uint32_t sa[2][MT];                                             /* unit scale (f32 bits), unit sum */
+#pragma unroll
+    for(int t = 0; t < MT; ++t){
+      const int n = t0 + (t < nt ? t : 0);
+      stg[t] = *(const uint4*)(xq + (long long)n * a.ldq + (long long)j * KT_KL * UW + oc);
+      sa[0][t] = __float_as_uint(xs[(long long)n * a.ldxs + uu]);
+      sa[1][t] = (uint32_t)xa[(long long)n * a.ldxs + uu];
+    }
+    kt_pin<MT>(&stg[0], &sa[0][0]);
+#pragma unroll
+    for(int t = 0; t < MT; ++t) *(uint4*)(xw + t * KT_KL * UP + (o / UW) * UP + o % UW) = stg[t];
+    kt_wave_sync();
+#pragma unroll
+    for(int t = 0; t < MT; ++t){
+      if(t < nt){                                                   /* uniform */
+        int vv[2];
+        const uint8_t* xrow = xw + (t * KT_KL + (uok ? c : 0)) * UP;
+        if(RG == 2) kt_unit2_lds(w[0].c0, w[0].c1, w[1].c0, w[1].c1, xrow, vv);
+        else vv[0] = kt_unit_lds<KT_FMT_TERN>(w[0].c0, w[0].c1, xrow);
+#pragma unroll
+        for(int q = 0; q < RG; ++q){
+          const float d = uok ? kt_h2f(w[q].hs) : 0.0f;
+          const int v = uok ? vv[q] - (int)sa[1][t] : 0;
+          fv[((q * S + j) * MT + t) * 64 + lane] = (float)v;
+          mv[((q * S + j) * MT + t) * 64 + lane] = __uint_as_float(sa[0][t]) * d;
+          const int row = (rg0 + q) * KT_RG + r;
+          if(DBG && uok && row < R) dbg[((long long)(t0 + t) * R + row) * NU + u] = v;
+        }
+      }
+    }
+    __syncthreads();
+    if(j == 0){
+#pragma unroll
+      for(int q = 0; q < RG; ++q){
+        float tot[MT];
+#pragma unroll
+        for(int t = 0; t < MT; ++t){
+          tot[t] = 0.0f;
+          for(int k = 0; k < KS; ++k){                              /* uniform */
+            const int s_lo = k * S / KS, ns = (k + 1) * S / KS - s_lo;
+            const int i0 = ((q * S + s_lo) * MT + t) * 64 + lane;
+            float acc = fmaf(fv[i0], mv[i0], 0.0f);
+            if(ns > 1) acc = fmaf(fv[i0 + MT * 64], mv[i0 + MT * 64], acc);
+            const float y = kt_row_sum(acc);
+            tot[t] = k == 0 ? y : tot[t] + y;
+          }
+        }
+        const int row = (rg0 + q) * KT_RG + r;
+        if(c == 0 && row < R){
+#pragma unroll
+          for(int t = 0; t < MT; ++t){
+            if(a.hp){                                               /* rows 2t, 2t + 1 -> token t (MT even) */
+              if(!(t & 1) && t < nt) m.y[(long long)((t0 + t) >> 1) * m.ldy + row] = tot[t] + tot[t + 1];
+            } else if(t < nt) m.y[(long long)(t0 + t) * m.ldy + row] = tot[t];
+          }
+        }
+      }
+    }
+    if(t0 + MT < M) __syncthreads();                                /* the next chunk rewrites the LDS */
+  }
+}
+
+template __global__ void k_gemv_stepm<2, false>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
+template __global__ void k_gemv_stepm<2, true>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
+template __global__ void k_gemv_stepm<4, false>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
+template __global__ void k_gemv_stepm<4, true>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
