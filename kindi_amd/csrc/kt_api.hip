@@ -490,7 +490,8 @@ int kt_plan_build(const kt_stage* st, int n, void* plan, kt_plan_info* info, voi
     e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, block, lds);
   }
   if(e != hipSuccess) return (int)e;
-  if(nb <= 0 || cus <= 0) return KT_INVALID;
+  if(nb <= 0 || cus <= 0 || cus > KT_BAR_MAXG) return KT_INVALID;
+  nb = std::min(nb, KT_BAR_MAXG / cus);                          /* the barrier's lines */
   H->nstages = n; H->G = nb * cus; H->W = W; H->MT = mt; H->exec = 0;
   /* one token: the streamed executor when its LDS fits (one 8-wave block a CU; at least one block a CU, so a
      block's tasks (row group, K slice) of a stage are at most tmax) */
@@ -501,6 +502,7 @@ int kt_plan_build(const kt_stage* st, int n, void* plan, kt_plan_info* info, voi
     slds = kt_splan_lds(smax, numax, tmax);
     if(slds <= 160 * 1024 && hipOccupancyMaxActiveBlocksPerMultiprocessor(&sb, kt_splan_kernel(), 576, slds)
        == hipSuccess && sb > 0){
+      sb = std::min(sb, KT_BAR_MAXG / cus);
       H->exec = 1; H->G = sb * cus; H->smax = smax; H->numax = numax; H->tmax = tmax; H->qtot = qtot;
     }
   }
@@ -516,7 +518,7 @@ int kt_plan_run(const void* plan, const kt_plan_info* info, void* stream){
   if(!plan || !info || info->nstages <= 0 || info->grid <= 0 || info->waves <= 0) return KT_INVALID;
   hipStream_t s = kt_stream(stream);
   unsigned* ctr = (unsigned*)((uint8_t*)plan + kt_plan_ctr_off(info->nstages));
-  hipLaunchKernelGGL(k_plan_reset, dim3(1), dim3(256), 0, s, ctr, (int)KT_BAR_WORDS);
+  hipLaunchKernelGGL(k_plan_reset, dim3(1), dim3(256), 0, s, ctr, (int)KT_BAR_LINES);
   const uint8_t* p = (const uint8_t*)plan;
   if(info->exec == 1){
     hipLaunchKernelGGL((void (*)(const uint8_t*, unsigned*))kt_splan_kernel(), dim3(info->grid), dim3(576), info->lds,
@@ -535,7 +537,7 @@ int kt_plan_run(const void* plan, const kt_plan_info* info, void* stream){
 int kt_plan_status(const void* plan, const kt_plan_info* info, int* status, void* stream){
   if(!plan || !info || !status || info->nstages <= 0) return KT_INVALID;
   unsigned v = 0;
-  const uint8_t* p = (const uint8_t*)plan + kt_plan_ctr_off(info->nstages) + (size_t)KT_BAR_STATUS * 32 * 4;
+  const uint8_t* p = (const uint8_t*)plan + kt_plan_ctr_off(info->nstages) + (size_t)KT_BAR_STATUS * KT_BAR_LINE * 4;
   hipError_t e = hipMemcpyAsync(&v, p, 4, hipMemcpyDeviceToHost, kt_stream(stream));
   if(e == hipSuccess) e = hipStreamSynchronize(kt_stream(stream));
   *status = (int)v;

@@ -140,12 +140,17 @@ struct KtPlanHdr {
 __host__ __device__ __forceinline__ size_t kt_plan_ctr_off(int nstages){
   return ((size_t)KT_PLAN_HDR + (size_t)nstages * sizeof(KtPStage) + 255) / 256 * 256;
 }
-/* barrier words (128-byte lines of 32 words): status, then KT_BAR_SHARDS arrival counters (block b arrives on
-   shard b % KT_BAR_SHARDS) */
+/* barrier lines (256 bytes, 64 words; only word 0 is used): the status line, then one arrival line per block, then
+   one line per group of KT_BAR_FAN blocks (its first block publishes there that the group has arrived). One writer a
+   line: many writers to one line (atomics, or stores into one line) queue at the memory side, about 15 ns each. */
+#define KT_BAR_LINE 64
+#define KT_BAR_FAN 16
+#define KT_BAR_MAXG 1024              /* blocks of a plan launch */
 #define KT_BAR_STATUS 0
-#define KT_BAR_SUB 1
-#define KT_BAR_SHARDS 32
-#define KT_BAR_WORDS ((KT_BAR_SUB + KT_BAR_SHARDS) * 32)
+#define KT_BAR_ARR 1                  /* line of block b: KT_BAR_ARR + b */
+#define KT_BAR_GRP (KT_BAR_ARR + KT_BAR_MAXG)
+#define KT_BAR_LINES (KT_BAR_GRP + KT_BAR_MAXG / KT_BAR_FAN)
+#define KT_BAR_WORDS (KT_BAR_LINES * KT_BAR_LINE)
 __host__ __device__ __forceinline__ size_t kt_plan_size(int nstages){
   return kt_plan_ctr_off(nstages) + ((size_t)KT_BAR_WORDS * 4 + 255) / 256 * 256;
 }

@@ -263,8 +263,9 @@ __global__ void __launch_bounds__(1024) k_plan(const uint8_t* __restrict__ plan,
   while(s_done < nS - 1){ kt_block_sync(); ++s_done; }              /* the remaining stages' B1 */
 }
 
+/* the barrier's used words (word 0 of each of its n lines) to zero before a run */
 extern "C" __global__ void k_plan_reset(unsigned* ctr, int n){
-  for(int i = threadIdx.x; i < n; i += blockDim.x) ctr[i] = 0u;
+  for(int i = threadIdx.x; i < n; i += blockDim.x) ctr[i * KT_BAR_LINE] = 0u;
 }
 
 template __global__ void k_plan<1>(const uint8_t*, unsigned*);

@@ -413,7 +413,7 @@ __global__ void __launch_bounds__(64 * (KS_WB + 1)) k_splan(const uint8_t* __res
       }
       if(s + 1 < nS) tc = ks_stage_info(plan, s + 1, nS, G, qtot, b);   /* off the stage-end path */
     }
-    if(L.ctl[2] && lane == 0) __hip_atomic_fetch_or(ctr + KT_BAR_STATUS * 32, 2u, __ATOMIC_RELAXED,
+    if(L.ctl[2] && lane == 0) __hip_atomic_fetch_or(ctr + KT_BAR_STATUS * KT_BAR_LINE, 2u, __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
