@@ -44,7 +44,7 @@ def parse():
     ap.add_argument("--plan", action="store_true",
                     help="headline over the decode plan (kt_plan_run: one persistent launch per step) instead of one "
                          "launch per product")
-    ap.add_argument("--only", choices=("c0", "c1", "c2", "c4", "producers"),
+    ap.add_argument("--only", choices=("c0", "c1", "c2", "c3m16", "c4", "producers"),
                     help="run one secondary config alone and print its figures (for profiler runs)")
     ap.add_argument("--cpu-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--cpu-runs", type=int, default=5, help=argparse.SUPPRESS)
@@ -157,6 +157,24 @@ def sweep_step(torch, linear, layers, M, seed=7):
 
     stages = [([Lin.w[n] for n in names], act, o) for _, names, act, o in calls]
     return step, nbytes, calls, launches, stages
+
+
+def config3_kinds(torch, linear, layers, M, timer, steps, use_graph):
+    """config 3's step at M tokens and its four launch kinds, each timed alone: the kind's launches of every layer back
+    to back in one graph (so a launch's weights are not in cache from the one before)"""
+    step, nbytes, calls, launches, _ = sweep_step(torch, linear, layers, M)
+    ms = timer.run(graphed(torch, step, use_graph), steps, 2)
+    out = {"ms_per_step": round(ms, 4), "GB/s": round(nbytes / ms / 1e6, 1),
+           "frac_hbm": round(nbytes / ms / 1e6 / HBM_PEAK, 4), "us_per_launch": {}}
+    for k, kind in enumerate(("q/k/v", "o", "gate/up", "down")):
+        sel = calls[k::4]
+
+        def fn(sel=sel):
+            for f, names, act, o in sel:
+                f(names, act, o)
+        us = timer.run(graphed(torch, fn, use_graph), steps, 2) * 1e3 / len(sel)
+        out["us_per_launch"][kind] = round(us, 2)
+    return out
 
 
 def step_with_producers(torch, linear, layers, M=1):
@@ -559,6 +577,8 @@ def main():
     use_graph = not a.no_graph
     if a.only:
         fn = {"c0": lambda: config0(torch, linear, synth, timer, a.steps, use_graph),
+              "c3m16": lambda: config3_kinds(torch, linear, build_27b(torch, linear, synth, (16,)), 16, timer,
+                                             a.steps, use_graph),
               "c1": lambda: config1(torch, linear, synth, timer, a.steps, use_graph),
               "c2": lambda: config2(torch, linear, synth, timer, a.steps),
               "c4": lambda: config4(torch, moe, synth, timer, a.steps, use_graph),
@@ -621,11 +641,8 @@ def main():
                     "smfold) in the launch before it; products_GB/s counts only the products' bytes"}
         del stepP
         log("config 3, M=16")
-        step16, nb16, calls16, _, _ = sweep_step(torch, linear, layers, 16)
-        ms16 = timer.run(graphed(torch, step16, use_graph), max(a.steps // 2, 3), 2)
-        cfgs["c3 M=16"] = {"ms_per_step": round(ms16, 4), "GB/s": round(nb16 / ms16 / 1e6, 1),
-                           "frac_hbm": round(nb16 / ms16 / 1e6 / HBM_PEAK, 4)}
-        del layers, step16, calls16, step, calls, stages, plan
+        cfgs["c3 M=16"] = config3_kinds(torch, linear, layers, 16, timer, max(a.steps // 2, 3), use_graph)
+        del layers, step, calls, stages, plan
         torch.cuda.empty_cache()
         log("configs 0, 1, 2, 4")
         cfgs["c0"] = config0(torch, linear, synth, timer, a.steps, use_graph)
