@@ -25,7 +25,7 @@ __global__ void k_gemv_pair(const KtGemvArgs, const int8_t*, const float*, const
 template <int NT, bool DBG, int LB>
 __global__ void k_gemv_mma(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
 template <bool DBG>
-__global__ void k_gemv_m16(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
+__global__ void k_gemv_m16(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
 template <bool GRP, bool DBG, bool MS>
 __global__ void k_q8_mma(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
 template <int MT> __global__ void k_plan(const uint8_t*, unsigned*);
@@ -96,17 +96,21 @@ static bool kt_use_mma(const KtGemvArgs& a){
   for(int i = 0; i < a.nmat; ++i) w += (long long)a.mat[i].R * a.NU * 128;
   return a.M >= KT_MMA_ANY || w >= (1ll << 24);
 }
-static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, int32_t* dbg, hipStream_t s){
+static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, const int* xa, int32_t* dbg,
+                         hipStream_t s){
   const int ks = kt_kslices(a.NU);
   int tiles = 0;
   for(int i = 0; i < a.nmat; ++i){ a.mat[i].pad = tiles; tiles += (kt_r8(a.mat[i].R) + 3) / 4; }
   const dim3 grid(tiles, (a.M + 15) / 16), block(64 * ks);
   const size_t lds = (size_t)ks * 16 * 32 * 4 + (size_t)ks * 256 * 4;        /* slice sums, XS */
-  if(a.M > 8 && ks <= 10){
+  bool off32 = (long long)a.M * a.ldxs * 4 < (1ll << 31);      /* k_gemv_m16 reads through 32-bit buffer offsets */
+  for(int i = 0; i < a.nmat; ++i) off32 = off32 && kt_code_bytes(a.mat[i].R, a.NU) < (1ull << 31);
+  if(a.M > 8 && ks <= 10 && off32){
     /* 16x16x64 tiles from 9 tokens (measured on MI355X: 27B-class step at 16 tokens 4.10 -> 3.99 ms; at 8 tokens
        the 32x32x32 kernel is faster, 2B-class layer 26.8 against 30.5 us) */
-    if(dbg) hipLaunchKernelGGL((k_gemv_m16<true>), grid, block, lds, s, a, xq, xs, dbg, ks);
-    else hipLaunchKernelGGL((k_gemv_m16<false>), grid, block, lds, s, a, xq, xs, dbg, ks);
+    const size_t lds16 = lds + (size_t)ks * 256 * 4;                        /* + XA */
+    if(dbg) hipLaunchKernelGGL((k_gemv_m16<true>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);
+    else hipLaunchKernelGGL((k_gemv_m16<false>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);
   } else if(ks <= 10){
     /* the 640-thread bound (159 VGPRs: 3 waves a SIMD, activations 2 units ahead) up to 10 slices, also for the
        narrow products (measured on MI355X: 27B-class step at 16 tokens 4.25 -> 4.10 ms, 2B-class layer at 8 tokens
@@ -125,7 +129,7 @@ static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, int32_
 template <int FMT>
 static int kt_launch_gemv(const KtGemvArgs& a, int ngroups, const int8_t* xq, const float* xs, const int* xa,
                           int32_t* dbg, hipStream_t s){
-  if(FMT == KT_FMT_TERN && kt_use_mma(a)) return kt_launch_mma(a, xq, xs, dbg, s);
+  if(FMT == KT_FMT_TERN && kt_use_mma(a)) return kt_launch_mma(a, xq, xs, xa, dbg, s);
   const int ks = kt_kslices(a.NU);
   bool even = true;
   for(int i = 0; i < a.nmat; ++i) even = even && kt_r8(a.mat[i].R) % 2 == 0;

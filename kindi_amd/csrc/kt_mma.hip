@@ -213,20 +213,24 @@ __device__ __forceinline__ void km_swap32(unsigned& a, unsigned& b){
 __device__ __forceinline__ void km_swap16(unsigned& a, unsigned& b){
   const auto t = __builtin_amdgcn_permlane16_swap(a, b, false, false); a = t[0]; b = t[1];
 }
-/* one kt2 word (16 digits, byte b bits 2k.. = column 4 k + b) -> 16 signed trits in column order */
-__device__ __forceinline__ kt_v4i km_unpack16(uint32_t w){
+/* one kt2 word -> its 16 digits d = t + 1 (0 / 1 / 2) in column order, as unsigned bytes */
+__device__ __forceinline__ kt_v4i km_digits16(uint32_t w){
   kt_v4i B;
-  B[0] = km_trits(w & 0x03030303u);
-  B[1] = km_trits((w >> 2) & 0x03030303u);
-  B[2] = km_trits((w >> 4) & 0x03030303u);
-  B[3] = km_trits((w >> 6) & 0x03030303u);
+  B[0] = (int)(w & 0x03030303u);
+  B[1] = (int)((w >> 2) & 0x03030303u);
+  B[2] = (int)((w >> 4) & 0x03030303u);
+  B[3] = (int)((w >> 6) & 0x03030303u);
   return B;
 }
 
-/* up to 10 K slices (640 threads, 158 VGPRs: 3 waves a SIMD, activations 4 units ahead) */
+/* up to 10 K slices (640 threads, 3 waves a SIMD, activations 4 units ahead). The B operands are the unsigned digits
+   d = t + 1 (masks and shifts of the kt2 word, no lookup): an MFMA then gives the exact integer sum d q, and the
+   unit value is v = sum d q - XA (XA = sum q, the quantizer's), the same integer as sum t q. The weights, scales,
+   XS and XA are read through buffer resources that span exactly their buffers, with 32-bit offsets. */
 template <bool DBG>
 __global__ void __launch_bounds__(640) k_gemv_m16(const KtGemvArgs a, const int8_t* __restrict__ xq,
-                                                  const float* __restrict__ xs, int32_t* __restrict__ dbg, int KS){
+                                                  const float* __restrict__ xs, const int* __restrict__ xav,
+                                                  int32_t* __restrict__ dbg, int KS){
   constexpr int NT = KM_TOK, KM_PF = 4;                          /* tokens a pass, activation units loaded ahead */
   extern __shared__ __attribute__((aligned(16))) uint8_t kt_lds[];
   float* red = (float*)kt_lds;                                   /* [KS][NT][32] slice sums */
@@ -248,18 +252,25 @@ __global__ void __launch_bounds__(640) k_gemv_m16(const KtGemvArgs a, const int8
   for(int b = 0; b < 2; ++b){ orow[b] = (rg0 + 2 * b + (n >> 3)) * KT_RG + cr; ook[b] = orow[b] < m.R; }
   const int nt = min(NT, a.M - t0);
   const int s_lo = ks * S / KS, ns = (ks + 1) * S / KS - s_lo;   /* this slice's steps (1 or 2) */
-  const uint4* __restrict__ wb = (const uint4*)m.codes;
-  const uint16_t* __restrict__ sb = m.scales;
+  const int nrg = kt_r8(m.R);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)m.codes, (short)0, nrg * NU * 256, 0x00020000);
+  const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc((void*)m.scales, (short)0, nrg * NU * 16, 0x00020000);
+  const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc((void*)xs, (short)0, a.M * a.ldxs * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc((void*)xav, (short)0, a.M * a.ldxs * 4, 0x00020000);
 
-  /* the slice's XS [16 units][16 tokens] to this wave's LDS region (after the weight loads are issued) */
-  float* xsl = (float*)(kt_lds + (size_t)KS * NT * 32 * 4) + (size_t)ks * 256;
+  /* the slice's XS and XA [16 units][16 tokens] to this wave's LDS regions (after the weight loads are issued) */
+  float* xsl = (float*)(kt_lds + (size_t)KS * NT * 32 * 4) + (size_t)ks * 512;
+  int* xal = (int*)(xsl + 256);
   float xsv[4];
+  int xav4[4];
 #pragma unroll
   for(int i = 0; i < 4; ++i){
     const int idx = lane + 64 * i, un = idx >> 4, tl = idx & 15;
     const int u = (s_lo + (un >> 3)) * KT_KL + (un & 7);
     const int t = t0 + tl < a.M ? t0 + tl : t0;
-    xsv[i] = xs[(long long)t * a.ldxs + (u < NU ? u : 0)];
+    const uint32_t o = (uint32_t)(t * a.ldxs + (u < NU ? u : 0)) * 4;
+    xsv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, o, 0, 0));
+    xav4[i] = (int)__builtin_amdgcn_raw_buffer_load_b32(ar, o, 0, 0);
   }
   float part[8], t01[8], t23[8], t45[8], pend[8];
 #pragma unroll
@@ -274,9 +285,12 @@ __global__ void __launch_bounds__(640) k_gemv_m16(const KtGemvArgs a, const int8
     for(int j = 0; j < 2; ++j){
       const int s = s_lo + j, u = s * KT_KL + c;
       const bool ok = j < ns && u < NU;
-      wq[j][c] = kt_ldnt(wb + (ok && cok ? kt_widx(NU, crg, s, ch, c, cr) : 0));
-      const uint32_t h0 = sb[ok && ook[0] ? kt_sidx(NU, rg0 + (n >> 3), u, cr) : 0];
-      const uint32_t h1 = sb[ok && ook[1] ? kt_sidx(NU, rg0 + 2 + (n >> 3), u, cr) : 0];
+      const uint32_t wo = ok && cok ? (uint32_t)kt_widx(NU, crg, s, ch, c, cr) * 16 : 0u;
+      wq[j][c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo, 0, 2));
+      const uint32_t h0 = __builtin_amdgcn_raw_buffer_load_b16(
+          hr, ok && ook[0] ? (uint32_t)kt_sidx(NU, rg0 + (n >> 3), u, cr) * 2 : 0u, 0, 0);
+      const uint32_t h1 = __builtin_amdgcn_raw_buffer_load_b16(
+          hr, ok && ook[1] ? (uint32_t)kt_sidx(NU, rg0 + 2 + (n >> 3), u, cr) * 2 : 0u, 0, 0);
       hq[j][c] = h0 | h1 << 16;
     }
   /* activations through a buffer resource over the M token rows (lanes past the pass's tokens: past the range,
@@ -293,7 +307,7 @@ __global__ void __launch_bounds__(640) k_gemv_m16(const KtGemvArgs a, const int8
 #pragma unroll
   for(int un = 0; un < KM_PF; ++un) ld_act(un, xa[un]);
 #pragma unroll
-  for(int i = 0; i < 4; ++i) xsl[lane + 64 * i] = xsv[i];
+  for(int i = 0; i < 4; ++i){ xsl[lane + 64 * i] = xsv[i]; xal[lane + 64 * i] = xav4[i]; }
   kt_wave_sync();
 #pragma unroll
   for(int c = 0; c < KT_KL; ++c){
@@ -314,10 +328,14 @@ __global__ void __launch_bounds__(640) k_gemv_m16(const KtGemvArgs a, const int8
         const kt_v4i A0 = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w};
         const kt_v4i A1 = {(int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
         kt_v4i d0 = {0, 0, 0, 0}, d1 = {0, 0, 0, 0};
-        d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, km_unpack16(w0), d0, 0, 0, 0);   /* row block 0, half 0 */
-        d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, km_unpack16(w2), d1, 0, 0, 0);   /* row block 1, half 0 */
-        d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, km_unpack16(w1), d0, 0, 0, 0);   /* row block 0, half 1 */
-        d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, km_unpack16(w3), d1, 0, 0, 0);   /* row block 1, half 1 */
+        d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, km_digits16(w0), d0, 0, 0, 0);   /* row block 0, half 0 */
+        d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, km_digits16(w2), d1, 0, 0, 0);   /* row block 1, half 0 */
+        d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, km_digits16(w1), d0, 0, 0, 0);   /* row block 0, half 1 */
+        d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, km_digits16(w3), d1, 0, 0, 0);   /* row block 1, half 1 */
+        const int4 xa4 = *(const int4*)(xal + (j * 8 + c) * 16 + 4 * g);                    /* tokens 4 g .. + 3 */
+        const int xq4[4] = {xa4.x, xa4.y, xa4.z, xa4.w};
+#pragma unroll
+        for(int e = 0; e < 4; ++e){ d0[e] -= xq4[e]; d1[e] -= xq4[e]; }                      /* v = sum d q - XA */
         const float dd0 = ook[0] ? kt_h2f((uint16_t)hq[j][c]) : 0.0f;
         const float dd1 = ook[1] ? kt_h2f((uint16_t)(hq[j][c] >> 16)) : 0.0f;
         const float4 sx = *(const float4*)(xsl + (j * 8 + c) * 16 + 4 * g);                /* tokens 4 g .. + 3 */
@@ -369,8 +387,8 @@ __global__ void __launch_bounds__(640) k_gemv_m16(const KtGemvArgs a, const int8
   }
 }
 
-template __global__ void k_gemv_m16<false>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
-template __global__ void k_gemv_m16<true>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
+template __global__ void k_gemv_m16<false>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
+template __global__ void k_gemv_m16<true>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
 
 /* ------------------------------------------------------------------ q8_0 on the matrix cores
    The q8_0 product (kq8 weights against int8 rows with per-32 scales, lt_mv_q8 lightning.cu:258-284, k_q8
