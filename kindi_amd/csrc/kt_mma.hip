@@ -200,11 +200,12 @@ template __global__ void k_gemv_mma<16, true, 640>(const KtGemvArgs, const int8_
      16 (g / 2) + n of the tile, so the wave's 64 loads are the unit's 1 KB in contiguous 128-byte runs;
    - a 4 x 4 transpose of words across the four 16-lane rows (two permlane32 swaps, two permlane16 swaps) leaves lane
      (g, n) with word g of the four chunks of its row n: for chunk m (row block m / 2, half m % 2) the four lanes of
-     row n hold its 64 columns 64 (m % 2) + 16 g .. + 15 (g = 0 .. 3); unpacked to signed trits they are the B
-     operand (column n = the weight row), and the A operand is token n's activations of the same columns
-     (V_MFMA_I32_16X16X64_I8: lane 16 g + n holds row / column n, k = 16 g .. + 15 in byte order, measured);
-   - row block b chains its two halves on one accumulator: lane (g, n) register j = v(token 4 g + j, row 16 b + n),
-     the exact int32 unit value (any pairing of columns gives the same integer).
+     row n hold its 64 columns 64 (m % 2) + 16 g .. + 15 (g = 0 .. 3); as unsigned digits (0 / 1 / 2, one a byte)
+     they are the B operand (column n = the weight row), and the A operand is token n's activations of the same
+     columns (V_MFMA_I32_16X16X64_I8: lane 16 g + n holds row / column n, k = 16 g .. + 15 in byte order, measured);
+   - row block b chains its two halves on one accumulator: lane (g, n) register j = sum d q (token 4 g + j, row
+     16 b + n); minus XA (sum q) it is the exact int32 unit value sum t q (any pairing of columns gives the same
+     integer).
    The fp32 epilogue is k_gemv_mma's (and k_gemv_flat's) order: per k-lane c the chain over the slice's units 8 s + c
    in increasing s, fmaf((float)v, XS[t][u] * d[r][u], .), the butterfly's tree over c, the slices in order. */
 __device__ __forceinline__ void km_swap32(unsigned& a, unsigned& b){
