@@ -277,6 +277,21 @@ __global__ void __launch_bounds__(640) k_gemv_m16(const KtGemvArgs a, const int8
 #pragma unroll
   for(int e = 0; e < 8; ++e){ part[e] = 0.0f; t01[e] = 0.0f; t23[e] = 0.0f; t45[e] = 0.0f; pend[e] = 0.0f; }
 
+  /* activations through a buffer resource over the M token rows (lanes past the pass's tokens: past the range,
+     zeros without a memory access) */
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, a.M * a.ldq, 0x00020000);
+  const uint32_t xoff = n < nt ? (uint32_t)((t0 + n) * a.ldq + 16 * g) : (1u << 30);
+  uint4 xa[KM_PF][2];
+  auto ld_act = [&](int un, uint4* dst){                         /* unit un = 2 c + j: both halves */
+    const int c = un >> 1, j = un & 1, u = (s_lo + j) * KT_KL + c;
+    const int uu = (j < ns && u < NU) ? u : 0;
+    dst[0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + uu * 128, 0, 0));
+    dst[1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + uu * 128 + 64, 0, 0));
+  };
+  /* the first units' activations before the weights: loads retire in order, so unit 0 can start as soon as its own
+     weights have landed rather than after the whole slice */
+#pragma unroll
+  for(int un = 0; un < KM_PF; ++un) ld_act(un, xa[un]);
   /* the slice's 16 units' chunks (k-lane-major) and both row blocks' scales (b = 0 | b = 1 << 16), unconditional */
   uint4 wq[2][KT_KL];
   uint32_t hq[2][KT_KL];
@@ -294,19 +309,6 @@ __global__ void __launch_bounds__(640) k_gemv_m16(const KtGemvArgs a, const int8
           hr, ok && ook[1] ? (uint32_t)kt_sidx(NU, rg0 + 2 + (n >> 3), u, cr) * 2 : 0u, 0, 0);
       hq[j][c] = h0 | h1 << 16;
     }
-  /* activations through a buffer resource over the M token rows (lanes past the pass's tokens: past the range,
-     zeros without a memory access) */
-  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, a.M * a.ldq, 0x00020000);
-  const uint32_t xoff = n < nt ? (uint32_t)((t0 + n) * a.ldq + 16 * g) : (1u << 30);
-  uint4 xa[KM_PF][2];
-  auto ld_act = [&](int un, uint4* dst){                         /* unit un = 2 c + j: both halves */
-    const int c = un >> 1, j = un & 1, u = (s_lo + j) * KT_KL + c;
-    const int uu = (j < ns && u < NU) ? u : 0;
-    dst[0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + uu * 128, 0, 0));
-    dst[1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + uu * 128 + 64, 0, 0));
-  };
-#pragma unroll
-  for(int un = 0; un < KM_PF; ++un) ld_act(un, xa[un]);
 #pragma unroll
   for(int i = 0; i < 4; ++i){ xsl[lane + 64 * i] = xsv[i]; xal[lane + 64 * i] = xav4[i]; }
   kt_wave_sync();
