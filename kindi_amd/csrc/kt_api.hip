@@ -61,7 +61,7 @@ size_t kt_moe1_down_lds(int k, int KS);
 #define KT_STEPM_WAVES 2048           /* multi-token grids of at most this many one-step waves take k_gemv_stepm */
 #define KT_PAIR_WAVES 6144             /* one-token grids of more waves take two row groups a block (k_gemv_pair) */
 #endif
-#define KT_RS_ROWS 8192                /* per-row prefill on small blocks below this many rows */
+#define KT_RS_BLOCKS 1024              /* per-row prefill on small blocks while the 128 x 128 grid has fewer blocks */
 #define KT_LAUNCH_CHECK() do { const hipError_t _e = hipGetLastError(); if(_e != hipSuccess) return (int)_e; } while(0)
 
 static inline hipStream_t kt_stream(void* s){ return (hipStream_t)s; }
@@ -550,8 +550,10 @@ int kt_plan_status(const void* plan, const kt_plan_info* info, int* status, void
 
 /* ------------------------------------------------------------------ prefill product */
 /* per_row = 0: the reference's per-group expression on 128 x 128 blocks. per_row = 1: the per-row order, on small
-   blocks (128 tokens x 64 rows) below KT_RS_ROWS rows so that every CU gets work, else on 128 x 128 blocks; both run
-   the same per-element chain, so the bits do not depend on the choice */
+   blocks (128 tokens x 64 rows) while a grid of 128 x 128 blocks would have fewer than KT_RS_BLOCKS blocks (4 a CU),
+   else on 128 x 128 blocks; both run the same per-element chain, so the bits do not depend on the choice (measured
+   on MI355X, config 2: gate/up [12288 x 4096] at 512 tokens 60.0 -> 56.5 us on the small blocks, at 2048 tokens
+   190.8 against 202.6 us on the large ones) */
 int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA,
                  int per_row, int M, float* Y, uint16_t* Y16, int ldy, int32_t* dbg, void* stream){
   (void)XA;                                                  /* signed trits on the matrix cores: no digit offset */
@@ -565,7 +567,7 @@ int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const f
   if((long long)M * ldq >= (1ll << 31) || (long long)M * NG * 4 >= (1ll << 31) || kt_code_bytes(R, NG) >= (1ull << 31))
     return KT_INVALID;
   hipStream_t s = kt_stream(stream);
-  if(per_row && R < KT_RS_ROWS){
+  if(per_row && (long long)((R + 127) / 128) * ((M + 127) / 128) < KT_RS_BLOCKS){
     /* one 32 x 32 tile a wave, 8 waves: 128 tokens x 64 rows */
     const dim3 grid((R + 63) / 64, (M + 127) / 128);
     if(dbg) hipLaunchKernelGGL((k_tern_gemm_rs1<4, 2, 3, true>), grid, dim3(512), 0, s, codes, scales, R, NG, XQ, ldq,
