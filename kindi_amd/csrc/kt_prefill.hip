@@ -204,7 +204,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k
     for(int e = 0; e < 16; ++e){
       const int t = n0 + wt * 64 + i * 32 + (e & 3) + 8 * (e >> 2) + 4 * (lane >> 5);
       if(t < M){
-        const float xr = RS ? XS[(long long)t * NG] : 1.0f;
+        const float xr = RS ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)t * NG * 4, 0, 0))
+                            : 1.0f;
         const float y0 = RS ? acc[i][0][e] * xr : acc[i][0][e], y1 = RS ? acc[i][1][e] * xr : acc[i][1][e];
         if(cr0 < R){
           if(Y) Y[(long long)t * ldy + cr0] = y0;
@@ -256,6 +257,7 @@ __global__ void __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)codes, (short)0, R8 * NG * 256, 0x00020000);
   const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, R8 * NG * 16, 0x00020000);
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)XQ, (short)0, M * ldq, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)XS, (short)0, M * NG * 4, 0x00020000);
   /* activations: token tid / 4 of the block, 32 bytes at (tid % 4) 32 of each group */
   const int xt = tid >> 2, xq = tid & 3;
   const uint32_t xbase = (uint32_t)(n0 + xt) * (uint32_t)ldq + xq * 32;
@@ -358,7 +360,7 @@ __global__ void __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_
   for(int e = 0; e < 16; ++e){
     const int t = n0 + 32 * wt + (e & 3) + 8 * (e >> 2) + 4 * (lane >> 5);
     if(t < M && cr < R){
-      const float y = acc[e] * XS[(long long)t * NG];
+      const float y = acc[e] * __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)t * NG * 4, 0, 0));
       if(Y) Y[(long long)t * ldy + cr] = y;
       if(Y16) Y16[(long long)t * ldy + cr] = __half_as_ushort(__float2half_rn(y));
     }

@@ -1,0 +1,112 @@
+"""Properties of the gfx950 code the library ships, checked on the assembly hipcc emits for its sources (CPU only: hipcc
+cross-compiles here).
+
+- No kernel uses scratch (private segment) apart from the listed ones: the debug instantiations (int32 unit values
+  written out for the tests) and the 2-4 token register-ring plan executor.
+- The decode product at 9-32 tokens and both prefill kernels read global memory only through buffer resources that
+  span exactly their buffers, so an out-of-range offset reads zeros and cannot fault.
+- No kernel writes through the scalar data cache.
+"""
+import os
+import re
+import shutil
+import subprocess
+from concurrent.futures import ThreadPoolExecutor
+
+import pytest
+
+from kindi_amd import build
+
+pytestmark = pytest.mark.skipif(not os.path.exists(build.HIPCC) and shutil.which("hipcc") is None,
+                                reason="hipcc is not installed")
+
+
+def _asm(src, tmp):
+    out = os.path.join(tmp, src.replace(".hip", ".s"))
+    cmd = [build.HIPCC] + build.FLAGS + ["-S", "--cuda-device-only", os.path.join(build.CSRC, src), "-o", out]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    return open(out).read()
+
+
+@pytest.fixture(scope="module")
+def asm(tmp_path_factory):
+    tmp = str(tmp_path_factory.mktemp("asm"))
+    with ThreadPoolExecutor(min(8, len(build.SOURCES))) as ex:
+        texts = list(ex.map(lambda s: _asm(s, tmp), build.SOURCES))
+    return dict(zip(build.SOURCES, texts))
+
+
+def _kernels(text):
+    """{mangled name: (body lines, metadata block)} of every kernel in one assembly file"""
+    out = {}
+    lines = text.split("\n")
+    for i, l in enumerate(lines):
+        m = re.match(r"^(_Z\S+|k_\w+):\s", l + " ")
+        if m and i + 1 < len(lines):
+            name = m.group(1)
+            body = []
+            for l2 in lines[i + 1:]:
+                if l2.strip().startswith("s_endpgm"):
+                    break
+                body.append(l2.strip())
+            out[name] = [body, None]
+    for blk in text.split("  - .agpr_count")[1:]:
+        nm = re.search(r"\.name:\s+(\S+)", blk)
+        sym = re.search(r"\.symbol:\s+(\S+)\.kd", blk)
+        if sym and sym.group(1) in out:
+            out[sym.group(1)][1] = blk
+        elif nm:
+            out.setdefault(nm.group(1), [[], None])[1] = blk
+    return out
+
+
+SCRATCH_OK = {"k_gemv_flat1<0, 1, true, false>", "k_gemv_pair<true>", "k_q8_mma<false, true, false>",
+              "k_q8_mma<true, true, false>", "k_tern_gemm<true, false>", "k_tern_gemm<true, true>",
+              "k_tern_gemm_rs1<4, 2, 3, true>", "k_plan<2>", "k_plan<4>"}
+
+
+def _demangle(names):
+    tool = shutil.which("c++filt") or shutil.which("llvm-cxxfilt")
+    if tool is None:
+        return {n: n for n in names}
+    r = subprocess.run([tool], input="\n".join(names), capture_output=True, text=True)
+    return dict(zip(names, [l.split("(")[0].replace("void ", "") for l in r.stdout.split("\n")]))
+
+
+def test_no_kernel_uses_scratch(asm):
+    seen, used = 0, set()
+    for src, text in asm.items():
+        ks = {n: m for n, (_, m) in _kernels(text).items() if m is not None}
+        dm = _demangle(list(ks))
+        for name, meta in ks.items():
+            seen += 1
+            priv = int(re.search(r"\.private_segment_fixed_size:\s+(\d+)", meta).group(1))
+            spill = int(re.search(r"\.vgpr_spill_count:\s+(\d+)", meta).group(1))
+            if priv or spill:
+                used.add(dm[name])
+    assert seen >= 20
+    assert used <= SCRATCH_OK, sorted(used - SCRATCH_OK)
+
+
+def _ops(body):
+    return [l.split()[0] for l in body if l and not l.startswith((".", ";")) and not l.endswith(":")]
+
+
+@pytest.mark.parametrize("src,pat", [("kt_mma.hip", "k_gemv_m16"), ("kt_prefill.hip", "k_tern_gemm")])
+def test_reads_through_buffer_resources(asm, src, pat):
+    ks = {n: b for n, (b, _) in _kernels(asm[src]).items() if pat in n and b}
+    assert ks, pat
+    for name, body in ks.items():
+        ops = _ops(body)
+        flat = [o for o in ops if o.startswith(("global_load", "flat_load", "global_atomic", "flat_atomic"))]
+        assert not flat, (name, flat[:5])
+        assert any(o.startswith("buffer_load") for o in ops), name
+
+
+def test_no_scalar_cache_writes(asm):
+    for src, text in asm.items():
+        for l in text.split("\n"):
+            op = l.strip().split(" ")[0] if l.strip() else ""
+            assert not op.startswith(("s_store", "s_scratch_store", "s_buffer_store", "s_atomic", "s_buffer_atomic",
+                                      "s_dcache_wb")), (src, l)
