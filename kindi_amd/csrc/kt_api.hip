@@ -105,9 +105,9 @@ static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, const 
   const size_t lds = (size_t)ks * 16 * 32 * 4 + (size_t)ks * 256 * 4;        /* slice sums, XS */
   bool off32 = (long long)a.M * a.ldxs * 4 < (1ll << 31);      /* k_gemv_m16 reads through 32-bit buffer offsets */
   for(int i = 0; i < a.nmat; ++i) off32 = off32 && kt_code_bytes(a.mat[i].R, a.NU) < (1ull << 31);
-  if(a.M > 8 && ks <= 10 && off32){
-    /* 16x16x64 tiles from 9 tokens (measured on MI355X: 27B-class step at 16 tokens 4.10 -> 3.99 ms; at 8 tokens
-       the 32x32x32 kernel is faster, 2B-class layer 26.8 against 30.5 us) */
+  if(a.M >= 8 && ks <= 10 && off32){
+    /* 16x16x64 tiles from 8 tokens (measured on MI355X: 27B-class step at 16 tokens 4.10 -> 3.99 ms; 2B-class layer
+       at 8 tokens 27.26 -> 27.03 us once its digit operands and activation-first loads were in) */
     const size_t lds16 = lds + (size_t)ks * 256 * 4;                        /* + XA */
     if(dbg) hipLaunchKernelGGL((k_gemv_m16<true>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);
     else hipLaunchKernelGGL((k_gemv_m16<false>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);

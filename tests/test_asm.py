@@ -3,7 +3,7 @@ cross-compiles here).
 
 - No kernel uses scratch (private segment) apart from the listed ones: the debug instantiations (int32 unit values
   written out for the tests) and the 2-4 token register-ring plan executor.
-- The decode product at 9-32 tokens and both prefill kernels read global memory only through buffer resources that
+- The decode product at 8-32 tokens and both prefill kernels read global memory only through buffer resources that
   span exactly their buffers, so an out-of-range offset reads zeros and cannot fault.
 - No kernel writes through the scalar data cache.
 """

@@ -147,9 +147,9 @@ def test_gemv_token_invariance(kt, R, C):
 @pytest.mark.parametrize("R,C", [(5120, 5120), (1024, 5120), (17408, 5120), (5120, 17408), (256, 24576)])
 def test_gemv_27b_tokens(kt, R, C):
     """the config 3 shapes at M = 1, 6, 8, 13, 16, 32, against the oracle: every launch kind that serves them (the
-    v_dot4 kernels below 6 / 8 tokens; the 32x32x32 matrix-core kernel at 6 - 8 tokens up to 10 K slices (the 27B
+    v_dot4 kernels below 6 / 8 tokens; the 32x32x32 matrix-core kernel at 6 - 7 tokens up to 10 K slices (the 27B
     down projection, C = 17408: 9 slices) and at any token count above 10 slices (C = 24576: 12 slices); the
-    16x16x64 one above 8 tokens up to 10 slices). int32 group values and fp32 outputs bit-exact against the oracle's
+    16x16x64 one from 8 tokens up to 10 slices). int32 group values and fp32 outputs bit-exact against the oracle's
     decode tree, with and without the dbg output"""
     lib, linear = kt
     say("gemv 27B tokens", R, C)
