@@ -50,6 +50,11 @@ int kt_tern_pack(const uint8_t* bcodes, const uint16_t* dpm, int R, int C, void*
    from a file in row chunks. The same W as kt_tern_pack of convert.py's pack of the tensor. Replaces the offline
    convert + repack path (convert.py:144-159, layout.py:32-48, spec.repack spec.py:327-383). */
 int kt_tern_pack_ptq1(const uint8_t* raw, int R, int C, int row0, int nrows, void* W, void* stream);
+/* kt_tern_pack_layout: a tensor already in Kindi's load-time GEMV layout (the output of layout.repack, layout.py:32-48,
+   as the engine holds it for k_g4 / k_deq_emb3, kindi.cu:525-536): wg4 the repacked bytes [R/16][C/512][4][32][4][4],
+   sg4 the scales16 array [R/16][C/512][32][2] (fp16 bits) -> W, the same W as kt_tern_pack of the pack those came
+   from. R % 16 == 0 and C % 512 == 0 (layout.py:38-39), else hipErrorInvalidValue. */
+int kt_tern_pack_layout(const uint8_t* wg4, const uint16_t* sg4, int R, int C, void* W, void* stream);
 
 /* ---------------------------------------------------------------- activations
    X fp32 [M][ldx] -> XQ int8 [M][ldq] (natural column order, ldq % 16 == 0), XS f32 / XA i32 [M][C/128].

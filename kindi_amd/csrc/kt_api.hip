@@ -32,7 +32,7 @@ template <int MT> __global__ void k_plan(const uint8_t*, unsigned*);
 size_t kt_splan_lds(int smax, int numax, int tmax);
 const void* kt_splan_kernel();
 extern "C" __global__ void k_plan_reset(unsigned*, int);
-extern "C" __global__ void k_tern_pack(const uint8_t*, const uint16_t*, int, int, uint32_t*, uint16_t*);
+template <int SRC> __global__ void k_tern_pack(const uint8_t*, const uint16_t*, int, int, uint32_t*, uint16_t*);
 extern "C" __global__ void k_q8_pack(const uint8_t*, int, int, uint32_t*, uint16_t*);
 extern "C" __global__ void k_tern_pack_ptq1(const uint8_t*, int, int, int, int, uint32_t*, uint16_t*);
 extern "C" __global__ void k_quant_tern(const float*, int, int, int, int8_t*, int, float*, int*);
@@ -339,6 +339,18 @@ static int kt_scratch_resolve(int dev, uint8_t** out){
   return 0;
 }
 
+template <int SRC>
+static int kt_pack_launch(const uint8_t* bcodes, const uint16_t* dpm, int R, int C, void* W, void* stream){
+  const int NG = C / 128;
+  uint32_t* codes = (uint32_t*)W;
+  uint16_t* scales = (uint16_t*)((uint8_t*)W + kt_code_bytes(R, NG));
+  const long long nw = (long long)kt_code_bytes(R, NG) / 4;
+  hipLaunchKernelGGL((k_tern_pack<SRC>), dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, kt_stream(stream),
+                     bcodes, dpm, R, C, codes, scales);
+  KT_LAUNCH_CHECK();
+  return 0;
+}
+
 extern "C" {
 
 int kt_version(void){ return KT_VERSION; }
@@ -360,14 +372,12 @@ size_t kt_tern_weight_bytes(int R, int C){
 
 int kt_tern_pack(const uint8_t* bcodes, const uint16_t* dpm, int R, int C, void* W, void* stream){
   if(!bcodes || !dpm || !W || R <= 0 || C <= 0 || C % 128 || !kt_al(W, 16)) return KT_INVALID;
-  const int NG = C / 128;
-  uint32_t* codes = (uint32_t*)W;
-  uint16_t* scales = (uint16_t*)((uint8_t*)W + kt_code_bytes(R, NG));
-  const long long nw = (long long)kt_code_bytes(R, NG) / 4;
-  hipLaunchKernelGGL(k_tern_pack, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, kt_stream(stream),
-                     bcodes, dpm, R, C, codes, scales);
-  KT_LAUNCH_CHECK();
-  return 0;
+  return kt_pack_launch<0>(bcodes, dpm, R, C, W, stream);
+}
+
+int kt_tern_pack_layout(const uint8_t* wg4, const uint16_t* sg4, int R, int C, void* W, void* stream){
+  if(!wg4 || !sg4 || !W || R <= 0 || C <= 0 || R % 16 || C % 512 || !kt_al(W, 16)) return KT_INVALID;
+  return kt_pack_launch<1>(wg4, sg4, R, C, W, stream);
 }
 
 int kt_tern_pack_ptq1(const uint8_t* raw, int R, int C, int row0, int nrows, void* W, void* stream){

@@ -1,5 +1,6 @@
 /* kt_decode.hip - gfx950 kernels of the decode side of the quantized linear layer:
-     k_tern_pack   reference pack (convert.py:144-159 bcodes [C/4][R], dpm [C/128][R]) -> kt2 device layout
+     k_tern_pack   reference pack (convert.py:144-159 bcodes [C/4][R], dpm [C/128][R]) -> kt2 device layout, or
+                   the same bytes after Kindi's load-time GEMV repack (layout.py:14-48) -> kt2
      k_tern_pack_ptq1  GGUF PTQ1_0 rows (28-byte blocks, convert.py:33-46) -> kt2, a range of row groups a launch
      k_q8_pack     GGUF Q8_0 rows (34-byte blocks) -> kq8 device layout
      k_quant_tern  fp32 rows -> int8 per 128-column group (or per row), XS, XA   (k_tc_q8, tc_hip.cu:43-74)
@@ -19,8 +20,30 @@ __device__ __forceinline__ void kt_word_pos(long long i, int NU, int& rg, int& u
   r = cr & 7;
 }
 
-extern "C" __global__ void k_tern_pack(const uint8_t* __restrict__ bc, const uint16_t* __restrict__ dpm, int R, int C,
-                                       uint32_t* __restrict__ codes, uint16_t* __restrict__ scales){
+/* where the reference's pack byte s (columns 4 s .. 4 s + 3) of a row, and its fp16 scale of group p, sit in a source
+   buffer. KT_SRC_PACK: the pack itself, bcodes [C/4][R], dpm [C/128][R] (convert.py:144-159). KT_SRC_G4: Kindi's
+   load-time GEMV layout (layout.repack, layout.py:32-48; read back the same way by k_deq_emb3, kindi.cu:525-536):
+   bytes [R/16][C/512][4 chunks of 4 rows][32 lanes][4 rows][4 bytes], scales [R/16][C/512][32 lanes][2], where lane
+   l of a 16-row group holds rows b(l), b(l) + 1 (b(l) = 8 (l & 1) + 4 (l >> 1 & 1) + 2 (l >> 2 & 1)) of group
+   4 ph + (l >> 3). R % 16 == 0 and C % 512 == 0 there (layout.py:38-39). */
+#define KT_SRC_PACK 0
+#define KT_SRC_G4 1
+template <int SRC>
+__device__ __forceinline__ long long kt_src_byte(int s, int row, int R, int C){
+  if(SRC == KT_SRC_PACK) return (long long)s * R + row;
+  return ((((long long)(row >> 4) * (C >> 9) + (s >> 7)) * 4 + ((row >> 2) & 3)) * 32 + ((s >> 2) & 31)) * 16
+         + (row & 3) * 4 + (s & 3);
+}
+template <int SRC>
+__device__ __forceinline__ long long kt_src_scale(int p, int row, int R, int C){
+  if(SRC == KT_SRC_PACK) return (long long)p * R + row;
+  const int rr = row & 15, lane = ((p & 3) << 3) | ((rr >> 3) & 1) | (((rr >> 2) & 1) << 1) | (((rr >> 1) & 1) << 2);
+  return (((long long)(row >> 4) * (C >> 9) + (p >> 2)) * 32 + lane) * 2 + (rr & 1);
+}
+
+template <int SRC>
+__global__ void k_tern_pack(const uint8_t* __restrict__ bc, const uint16_t* __restrict__ dpm, int R, int C,
+                            uint32_t* __restrict__ codes, uint16_t* __restrict__ scales){
   /* one thread per output word */
   const int NG = C >> 7, R8 = kt_r8(R);
   const long long nw = (long long)R8 * NG * 64;
@@ -35,7 +58,7 @@ extern "C" __global__ void k_tern_pack(const uint8_t* __restrict__ bc, const uin
       const int s0 = (u * 128 + h * 64 + j * 16) >> 2;        /* 4 pack bytes: columns 4k .. 4k+3 of the word */
 #pragma unroll
       for(int k = 0; k < 4; ++k){
-        unsigned int b = bc[(long long)(s0 + k) * R + row];
+        unsigned int b = bc[kt_src_byte<SRC>(s0 + k, row, R, C)];
 #pragma unroll
         for(int e = 0; e < 4; ++e){                            /* column 4k + e: byte e, bits 2k */
           w |= (b % 3u) << (8 * e + 2 * k);
@@ -48,9 +71,11 @@ extern "C" __global__ void k_tern_pack(const uint8_t* __restrict__ bc, const uin
   const long long ns = (long long)R8 * NG * 8;
   if(i < ns){
     const int r = (int)(i & 7), u = (int)((i >> 3) % NG), rg = (int)((i >> 3) / NG), row = rg * KT_RG + r;
-    scales[i] = row < R ? dpm[(long long)u * R + row] : (uint16_t)0;
+    scales[i] = row < R ? dpm[kt_src_scale<SRC>(u, row, R, C)] : (uint16_t)0;
   }
 }
+template __global__ void k_tern_pack<KT_SRC_PACK>(const uint8_t*, const uint16_t*, int, int, uint32_t*, uint16_t*);
+template __global__ void k_tern_pack<KT_SRC_G4>(const uint8_t*, const uint16_t*, int, int, uint32_t*, uint16_t*);
 
 /* digit e (0..127) of a GGUF PTQ1_0 block (convert.py:33-46): qs bytes 0..15 hold elements n 16 + j, 16..23 hold
    80 + n 8 + j, qh bytes 24..25 hold 120 + n 2 + j; digit n of byte v = ((v 3^n) mod 256) 3 / 256 */

@@ -34,6 +34,7 @@ SIGNATURES = [
     ("kt_tern_weight_bytes", S, [I, I]),
     ("kt_tern_pack", I, [P, P, I, I, P, P]),
     ("kt_tern_pack_ptq1", I, [P, I, I, I, I, P, P]),
+    ("kt_tern_pack_layout", I, [P, P, I, I, P, P]),
     ("kt_quant_q8", I, [P, I, I, I, I, P, I, P, P, P]),
     ("kt_decode_kslices", I, [I, I]),
     ("kt_tern_gemv", I, [P, I, I, P, I, P, P, I, P, I, P, P]),

@@ -5,6 +5,7 @@ Kindi's callers and what each maps to here:
   build_plan gemm / gemm3 (k_tc_q8 + k_tc_mv) spec.py:619-672        quantize + Linear.gemv_q / gemv3_q
   chunk gemm_tc (k_tc_q8 + k_tc_mm2)          chunk.py:273-296       quantize + Linear.gemm
   layout.repack / spec.repack                 layout.py:32-48, spec.py:327-383   TernaryMatrix (kt_tern_pack)
+  a tensor already in layout.repack's layout  layout.py:32-48, kindi.cu:525-536  TernaryMatrix.from_layout
 
 Torch provides device memory and the current stream only; every product runs in the HIP library. Tensors are
 CUDA (HIP) tensors on one device; activations fp32 [M, C] row-major.
@@ -90,6 +91,22 @@ class TernaryMatrix(object):
             raise ValueError("PTQ1_0 data does not match %d x %d" % (R, C))
         gpudrv.check(gpudrv.load().kt_tern_pack_ptq1(ptr(rd), self.R, self.C, 0, self.R, ptr(self.W), stream()),
                      "kt_tern_pack_ptq1")
+        return self
+
+    @classmethod
+    def from_layout(cls, wg4, sg4, R, C, device="cuda", W=None):
+        """a tensor already repacked by Kindi's layout.repack (layout.py:32-48: the weight bytes in the GEMV layout
+        and the scales16 array, as the engine holds them for k_g4), rearranged on the device into the kt2 layout (the
+        same W as the pack it came from). R % 16 == 0 and C % 512 == 0, as layout.repack requires"""
+        if R % 16 or C % 512:
+            raise ValueError("the GEMV layout takes R %% 16 == 0 and C %% 512 == 0 (got %d x %d)" % (R, C))
+        self = cls._empty(R, C, device, W)
+        wb = _dev_u8(wg4, device).reshape(-1)
+        sb = _dev_u16(sg4, device).reshape(-1)
+        if wb.numel() != self.R * self.C // 4 or sb.numel() != self.R * (self.C // 128):
+            raise ValueError("GEMV-layout arrays do not match %d x %d" % (R, C))
+        gpudrv.check(gpudrv.load().kt_tern_pack_layout(ptr(wb), ptr(sb), self.R, self.C, ptr(self.W), stream()),
+                     "kt_tern_pack_layout")
         return self
 
 

@@ -12,6 +12,8 @@ Contents:
       pack_from_digits / digits_from_pack  - convert.py:49-52 (phase_bytes) and its inverse (convert.py:55-60)
       trits_from_ptq1 / ptq1_from_digits  - convert.py:33-46 (PTQ1_0 decode) and the matching encoder
       paircodes                           - cpu.py:69-88
+      layout_g4                           - layout.repack / scales16 (layout.py:14-48), the GEMV layout Kindi's
+                                            engine holds on the card for k_g4 / k_deq_emb3 (kindi.cu:525-536)
       q8_0_rows / q8_0_group4             - GGUF Q8_0 rows (dsv41_cpu.c:77-78) and k_q8g's 4-row groups
                                             (dsv41_cpu.c:781-790)
 """
@@ -138,6 +140,29 @@ def ptq1_from_digits(dig, scales):
     raw[:, 24:26] = enc([d[:, 120 + n * 2:122 + n * 2] for n in range(4)], 4)
     raw[:, 26:28] = np.asarray(scales, dtype=np.uint16).reshape(nb, 1).view(np.uint8)
     return raw
+
+
+def _g4_base_row(lane):
+    """first of the two rows of a 16-row group that lane (0..7 within its group) holds: bit 0 of the lane selects
+    8 rows, bit 1 four, bit 2 two (layout.py:14-15)"""
+    return (lane & 1) * 8 + ((lane >> 1) & 1) * 4 + ((lane >> 2) & 1) * 2
+
+
+def layout_g4(bcodes, dpm, R, C):
+    """the reference pack (bcodes [C/4, R], dpm [C/128, R]) -> Kindi's load-time GEMV layout (layout.py:1-8,32-48):
+    bytes in the order [16-row group][512-column phase][4-row chunk][lane 0..31][row in chunk][byte in word], lane l of
+    a phase holding pack bytes 4 (32 ph + l) .. + 3 (columns 16 (32 ph + l) .. + 15); scales in the order
+    [16-row group][phase][lane][2], lane l holding rows b(l), b(l) + 1 of its group for the 128-column group
+    4 ph + l / 8 (scales16, layout.py:18-28). Written here as a gather over the output positions."""
+    if R % 16 or C % 512:
+        raise ValueError("the GEMV layout takes R % 16 == 0 and C % 512 == 0")
+    bc = np.asarray(bcodes, dtype=np.uint8).reshape(C // 4, R)
+    dp = np.asarray(dpm, dtype=np.uint16).reshape(C // 128, R)
+    g16, ph, ch, ln, rl, sl = np.indices((R // 16, C // 512, 4, 32, 4, 4), sparse=True)
+    w = bc[(ph * 32 + ln) * 4 + sl, (g16 * 4 + ch) * 4 + rl]
+    g16, ph, ln, jj = np.indices((R // 16, C // 512, 32, 2), sparse=True)
+    sc = dp[ph * 4 + (ln >> 3), g16 * 16 + _g4_base_row(ln & 7) + jj]
+    return np.ascontiguousarray(w).reshape(-1), np.ascontiguousarray(sc).reshape(-1)
 
 
 _CODE = np.array([0, 1, 2, 3, 8, 4, 5, 6, 7], dtype=np.uint32)     # d0 + 3 d1 -> pair code (both zero -> 8)

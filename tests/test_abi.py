@@ -27,7 +27,7 @@ def lib():
 
 def test_exports_every_declared_symbol(lib):
     names = declared()
-    assert len(names) == 32
+    assert len(names) == 33
     for n in names:
         assert hasattr(lib, n), n
     from kindi_amd import gpudrv
@@ -145,6 +145,14 @@ def test_fold_validation(lib):
     assert lib.kt_fold_q8(f, 4000, f, 1, 4096, 4096, None, 0, f, 4096, f, f, None) == INVALID
     assert lib.kt_smfold_q8(f, 4096, f, 4096, f, 128, 4, 7, 1, 4096, 4096, None, 0, f, 4096, f, f, None) == INVALID
     assert lib.kt_smfold_q8(f, 4096, f, 4096, f, 128, 4, 0, 1, 4096, 4096, None, 0, f, 4096, f, f, None) == INVALID
+
+
+def test_layout_validation(lib):
+    f = ctypes.c_void_p(16)
+    assert lib.kt_tern_pack_layout(f, f, 100, 512, f, None) == INVALID      # R % 16 (layout.py:38)
+    assert lib.kt_tern_pack_layout(f, f, 64, 384, f, None) == INVALID       # C % 512
+    assert lib.kt_tern_pack_layout(None, f, 64, 512, f, None) == INVALID
+    assert lib.kt_tern_pack_layout(f, f, 64, 512, ctypes.c_void_p(8), None) == INVALID   # W not 16-byte aligned
 
 
 def test_ptq1_validation(lib):

@@ -466,6 +466,20 @@ def test_pack_from_ptq1(kt, R, C, tmp_path):
     assert np.array_equal(host(m.W), want)
 
 
+@pytest.mark.parametrize("R,C", [(16, 512), (6144, 2048), (1024, 17408)])
+def test_pack_from_layout(kt, R, C):
+    """a tensor in Kindi's load-time GEMV layout (the oracle's restatement of layout.repack) gives the same kt2 bytes
+    as the reference pack it came from (so every product over it has the same bits)"""
+    lib, linear = kt
+    say("layout", R, C)
+    dig, bc, dpm = tern_case(R, C, 3 * R + C)
+    wg, sg = orc.layout_g4(bc, dpm, R, C)
+    want = linear.TernaryMatrix(bc, dpm, R, C)
+    got = linear.TernaryMatrix.from_layout(wg, sg, R, C)
+    assert np.array_equal(host(got.W), host(want.W))
+    assert want.W.numel() == lib.kt_tern_weight_bytes(R, C)
+
+
 def _gguf_bytes(tensors, kv):
     """a small GGUF v3 file: kv {key: (type, value)}, tensors [(name, dims, type, data bytes)]"""
     import struct

@@ -35,6 +35,45 @@ def test_pack_known_answers(orc):
     assert b[:, 0].tolist() == [65, 40]
 
 
+def _deq_emb3_index(row, e, C):
+    """k_deq_emb3's reads of column e of a row in the GEMV layout (kindi.cu:525-536): (byte index, slot within the
+    byte, scale index) - the consumer's statement of the layout, written out per element"""
+    s, p, slot = e >> 2, e >> 7, e & 3
+    r4, rl, g16, rr = row >> 2, row & 3, row >> 4, row & 15
+    bi = ((((row >> 4) * (C >> 9) + (s >> 7)) * 4 + (r4 & 3)) * 32 + ((s >> 2) & 31)) * 16 + rl * 4 + (s & 3)
+    lane_low = ((rr >> 3) & 1) | (((rr >> 2) & 1) << 1) | (((rr >> 1) & 1) << 2)
+    lane = ((p & 3) << 3) | lane_low
+    return bi, slot, ((g16 * (C >> 9) + (p >> 2)) * 32 + lane) * 2 + (rr & 1)
+
+
+def test_layout_g4_against_deq_emb3(orc):
+    """layout_g4 (restated from layout.py) read back element by element with kindi.cu's own decode of that layout:
+    every weight digit and scale of a 32 x 1024 tensor comes back; hand-placed known answers"""
+    R, C = 32, 1024
+    dig = rand_digits(R, C, 11)
+    bc = orc.pack_from_digits(dig)
+    dpm = rand_scales((C // 128, R), 12)
+    wg, sg = orc.layout_g4(bc, dpm, R, C)
+    assert wg.size == bc.size and sg.size == dpm.size
+    for row in range(R):
+        for e in range(C):
+            bi, slot, si = _deq_emb3_index(row, e, C)
+            assert (int(wg[bi]) // 3 ** slot) % 3 == dig[row, e], (row, e)
+            if e % 128 == 0:
+                assert sg[si] == dpm[e // 128, row], (row, e)
+    # row 5, column 100 of a 16 x 512 tensor: pack byte 25 -> phase 0, lane 6, byte 1 of chunk 1's row 1:
+    # ((1 * 32 + 6) * 16) + 4 + 1 = 613; its group-2 scale: row 5 = base 4 (lane 2) + 1, lane 2 + 8 * 2 = 18 -> 37
+    bc1 = np.zeros((128, 16), np.uint8)
+    bc1[25, 5] = 77
+    dp1 = np.zeros((4, 16), np.uint16)
+    dp1[2, 5] = 0x3C00
+    w1, s1 = orc.layout_g4(bc1, dp1, 16, 512)
+    assert np.flatnonzero(w1).tolist() == [613] and w1[613] == 77
+    assert np.flatnonzero(s1).tolist() == [37] and s1[37] == 0x3C00
+    with pytest.raises(ValueError):
+        orc.layout_g4(bc1[:, :8], dp1[:, :8], 8, 512)
+
+
 def test_ptq1_round_trip_and_known_answer(orc):
     """PTQ1_0 decode (convert.py:33-46) inverts the TQ1 encoding ceil(v * 256 / 243)"""
     dig = rand_digits(300, 128, 3)
