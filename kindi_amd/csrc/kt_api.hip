@@ -78,11 +78,18 @@ static int kt_kslices(int NU){
 }
 
 /* up to 32 ternary tokens: the matrix-core product (the same numbers and tree, so the same bits), tiles of 32 rows
-   of one matrix, passes of 16 tokens. It pays from 6 tokens on launches of 2^24 weights or more and from 8 tokens
-   on any (measured on MI355X: a 27B-class step at 8 tokens 6.36 -> 3.96 ms, at 4 tokens 3.85 -> 3.80 ms; a 2B-class
-   layer even at 8 tokens, 18.8 -> 20.5 us at 4) */
+   of one matrix, passes of 16 tokens. It pays over the v_dot4 kernels from 3 tokens on launches of 2^26 weights or
+   more, 4 tokens on 2^25, 5 tokens on 2^24, and from 8 tokens on any launch. Measured on MI355X with k_gemv_m16, per
+   launch over 16 27B-class layers and per 2B-class layer: at 3 tokens gate/up (2^26.4) 21.6 -> 18.6 us and down
+   19.5 -> 13.9 us, while q/k/v (2^25.1) and o stay faster on v_dot4 (7.98 against 8.09, 7.03 against 7.70 us); at 4
+   tokens q/k/v 8.68 -> 8.31 us, while o (2^24.6) and the 2B gate/up launch (2^24.6, one K slice) stay faster on
+   v_dot4 (7.67 against 7.80 us; 2B layer 18.3 against 19.6 us); at 5 tokens the 27B layer 81.1 -> 48.9 us and the
+   2B layer 26.9 -> 26.0 us; at 2 tokens v_dot4 is faster on every launch (27B layer 43.8 against 48.1 us) */
 #ifndef KT_MMA_MIN
-#define KT_MMA_MIN 6
+#define KT_MMA_MIN 3
+#endif
+#ifndef KT_MMA_MID
+#define KT_MMA_MID 5                   /* from here 2^24 weights suffice; one token fewer doubles it */
 #endif
 #ifndef KT_MMA_ANY
 #define KT_MMA_ANY 8
@@ -92,10 +99,12 @@ static int kt_kslices(int NU){
 #define KT_Q8_MMA_KS 8                 /* q8_0 matrix-core product: K slices a block (kt_mma.hip KM_Q8_KS) */
 static bool kt_use_mma(const KtGemvArgs& a){
   if(a.M < KT_MMA_MIN || a.M > KT_MMA_MAX || (long long)a.M * a.ldq >= (1ll << 30)) return false;
+  if(a.M >= KT_MMA_ANY) return true;
   long long w = 0;
   for(int i = 0; i < a.nmat; ++i) w += (long long)a.mat[i].R * a.NU * 128;
-  return a.M >= KT_MMA_ANY || w >= (1ll << 24);
+  return w >= (1ll << (24 + (a.M >= KT_MMA_MID ? 0 : KT_MMA_MID - a.M)));
 }
+
 static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, const int* xa, int32_t* dbg,
                          hipStream_t s){
   const int ks = kt_kslices(a.NU);
@@ -105,19 +114,16 @@ static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, const 
   const size_t lds = (size_t)ks * 16 * 32 * 4 + (size_t)ks * 256 * 4;        /* slice sums, XS */
   bool off32 = (long long)a.M * a.ldxs * 4 < (1ll << 31);      /* k_gemv_m16 reads through 32-bit buffer offsets */
   for(int i = 0; i < a.nmat; ++i) off32 = off32 && kt_code_bytes(a.mat[i].R, a.NU) < (1ull << 31);
-  if(a.M >= 8 && ks <= 10 && off32){
-    /* 16x16x64 tiles from 8 tokens (measured on MI355X: 27B-class step at 16 tokens 4.10 -> 3.99 ms; 2B-class layer
-       at 8 tokens 27.26 -> 27.03 us once its digit operands and activation-first loads were in) */
+  if(ks <= 10 && off32){
+    /* 16x16x64 tiles for every matrix-core launch up to 10 slices (measured on MI355X: 27B-class step at 16 tokens
+       4.10 -> 3.99 ms; 2B-class layer at 8 tokens 27.26 -> 27.03 us, at 6 and 7 tokens even; 27B-class launches at
+       6 tokens q/k/v 8.72 -> 8.38, gate/up 22.04 -> 19.51, down 16.14 -> 14.62 us) */
     const size_t lds16 = lds + (size_t)ks * 256 * 4;                        /* + XA */
     if(dbg) hipLaunchKernelGGL((k_gemv_m16<true>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);
     else hipLaunchKernelGGL((k_gemv_m16<false>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);
-  } else if(ks <= 10){
-    /* the 640-thread bound (159 VGPRs: 3 waves a SIMD, activations 2 units ahead) up to 10 slices, also for the
-       narrow products (measured on MI355X: 27B-class step at 16 tokens 4.25 -> 4.10 ms, 2B-class layer at 8 tokens
-       28.1 -> 26.6 us against the 256-thread bound's deeper prefetch at 2 waves a SIMD) */
-    if(dbg) hipLaunchKernelGGL((k_gemv_mma<16, true, 640>), grid, block, lds, s, a, xq, xs, dbg, ks);
-    else hipLaunchKernelGGL((k_gemv_mma<16, false, 640>), grid, block, lds, s, a, xq, xs, dbg, ks);
   } else {
+    /* above 10 slices, or buffers past 32-bit offsets: 32x32x32 tiles, the 1024-thread bound (activations loaded in
+       place, 124 VGPRs) */
     if(dbg) hipLaunchKernelGGL((k_gemv_mma<16, true, 64 * KT_KSMAX>), grid, block, lds, s, a, xq, xs, dbg, ks);
     else hipLaunchKernelGGL((k_gemv_mma<16, false, 64 * KT_KSMAX>), grid, block, lds, s, a, xq, xs, dbg, ks);
   }

@@ -1,5 +1,6 @@
-/* kt_mma.hip - the decode product on the matrix cores for up to 32 tokens (passes of 16; the launcher takes it from 6 or 8 tokens) (k_tc_mv*, tc_hip.cu:180-240, at
-   the verify widths spec.py:45 takes them): ternary weights (kt2) against int8 token rows, the same numbers and the
+/* kt_mma.hip - the decode product on the matrix cores for up to 32 tokens (passes of 16; the launcher takes it from 3
+   to 8 tokens on, by launch size) (k_tc_mv*, tc_hip.cu:180-240, at the verify widths spec.py:45 takes them): ternary
+   weights (kt2) against int8 token rows, the same numbers and the
    same summation tree as k_gemv_flat, so a token's bits do not depend on which of the two kernels ran it.
 
    Block: KS waves over one tile of 32 weight rows (4 row groups of one matrix); wave ks takes the K slice ks (steps
@@ -189,8 +190,6 @@ __global__ void __launch_bounds__(LB) k_gemv_mma(const KtGemvArgs a, const int8_
 
 template __global__ void k_gemv_mma<16, false, 64 * KT_KSMAX>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
 template __global__ void k_gemv_mma<16, true, 64 * KT_KSMAX>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
-template __global__ void k_gemv_mma<16, false, 640>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
-template __global__ void k_gemv_mma<16, true, 640>(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
 
 /* ------------------------------------------------------------------ ternary, 16 tokens, V_MFMA_I32_16X16X64_I8
    k_gemv_m16: the numbers, tree and block shape of k_gemv_mma (a tile of 32 weight rows, wave ks = K slice ks,

@@ -123,8 +123,8 @@ def test_gemv_hp_pairs(kt, R, C):
 @pytest.mark.parametrize("R,C", [(640, 1024), (2048, 6144), (4096, 4096)])
 def test_gemv_token_invariance(kt, R, C):
     """a token's output does not depend on how many tokens share the pass (tc_hip.cu:14-15), for M = 1 .. 32: the
-    bandwidth kernel and the matrix-core kernels (from 6 tokens at 2^24 weights, from 8 on any; 16x16x64 tiles above 8)
-    give the same bits"""
+    bandwidth kernels and the matrix-core kernels (from 5 tokens at 2^24 weights, from 8 on any; 16x16x64 tiles up to
+    10 K slices) give the same bits"""
     lib, linear = kt
     say("gemv T-invariance", R, C)
     W, dig, bc, dpm = upload(linear, R, C, 5 + R)
@@ -135,7 +135,7 @@ def test_gemv_token_invariance(kt, R, C):
     acc = orc.tern_acc(bc, R, C, Q)
     dq = dpm.view(np.float16).astype(np.float32)
     tree = orc.out_lanes(acc, XS, dq, 8, 0, lib.kt_decode_kslices(C, 0))
-    for M in (1, 2, 3, 4, 5, 8, 9, 12, 13, 16, 17, 20, 24, 32):
+    for M in (1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 13, 16, 17, 20, 24, 32):
         act = linear.quantize(Xd[:M])
         Y = torch.empty((M, R), dtype=torch.float32, device="cuda")
         dbg = torch.empty((M, R, C // 128), dtype=torch.int32, device="cuda")
@@ -146,11 +146,11 @@ def test_gemv_token_invariance(kt, R, C):
 
 @pytest.mark.parametrize("R,C", [(5120, 5120), (1024, 5120), (17408, 5120), (5120, 17408), (256, 24576)])
 def test_gemv_27b_tokens(kt, R, C):
-    """the config 3 shapes at M = 1, 6, 8, 13, 16, 32, against the oracle: every launch kind that serves them (the
-    v_dot4 kernels below 6 / 8 tokens; the 32x32x32 matrix-core kernel at 6 - 7 tokens up to 10 K slices (the 27B
-    down projection, C = 17408: 9 slices) and at any token count above 10 slices (C = 24576: 12 slices); the
-    16x16x64 one from 8 tokens up to 10 slices). int32 group values and fp32 outputs bit-exact against the oracle's
-    decode tree, with and without the dbg output"""
+    """the config 3 shapes at M = 1, 3, 4, 5, 6, 8, 13, 16, 32, against the oracle: every launch kind that serves them
+    (the v_dot4 kernels at 1 - 2 tokens, at 3 below 2^26 weights, at 4 below 2^25 and at 5 - 7 below 2^24; the
+    16x16x64 matrix-core kernel above those up to 10 K slices; the 32x32x32 one above 10 slices, C = 24576: 12
+    slices, from 8 tokens).
+    int32 group values and fp32 outputs bit-exact against the oracle's decode tree, with and without the dbg output"""
     lib, linear = kt
     say("gemv 27B tokens", R, C)
     W, dig, bc, dpm = upload(linear, R, C, 3 * R + C)
@@ -162,7 +162,7 @@ def test_gemv_27b_tokens(kt, R, C):
     dq = dpm.view(np.float16).astype(np.float32)
     tree = orc.out_lanes(acc, XS, dq, 8, 0, lib.kt_decode_kslices(C, 0))
     assert max_rel(tree, orc.tern_out(acc, XS, dpm, R, C)) < TOL
-    for M in (1, 6, 8, 13, 16, 32):
+    for M in (1, 3, 4, 5, 6, 8, 13, 16, 32):
         say("  M", M)
         act = linear.quantize(Xd[:M])
         Y = torch.empty((M, R), dtype=torch.float32, device="cuda")
