@@ -57,8 +57,10 @@ size_t kt_moe1_up_lds(int KS);
 size_t kt_moe1_down_lds(int k, int KS);
 
 #define KT_INVALID ((int)hipErrorInvalidValue)
-#ifndef KT_PAIR_WAVES
+#ifndef KT_STEPM_WAVES
 #define KT_STEPM_WAVES 2048           /* multi-token grids of at most this many one-step waves take k_gemv_stepm */
+#endif
+#ifndef KT_PAIR_WAVES
 #define KT_PAIR_WAVES 6144             /* one-token grids of more waves take two row groups a block (k_gemv_pair) */
 #endif
 #define KT_RS_BLOCKS 1024              /* per-row prefill on small blocks while the 128 x 128 grid has fewer blocks */
