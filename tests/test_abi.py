@@ -173,3 +173,22 @@ def test_moe_decode_validation(lib):
     assert lib.kt_moe_decode(f, f, 128, 2688, 1856, 6, f, 1, f, 2688, None, f, n - 1, None) == 1   # short workspace
     assert lib.kt_moe_decode(f, f, 128, 2688, 1856, 6, f, 1, f, 2686, None, f, n, None) == 1       # ldx % 4
     assert lib.kt_moe_decode(f, f, 128, 2688, 1856, 6, f, 0, f, 2688, None, f, n, None) == 0       # nothing to do
+
+
+def test_no_fallback_without_library(tmp_path):
+    """with the library absent the product path raises KernelError (no CPU fallback): a child process with
+    KINDI_KT_LIB pointing at a missing file builds a TernaryMatrix and calls quantize"""
+    import subprocess
+    import sys
+    code = ("import numpy as np, torch\n"
+            "from kindi_amd import gpudrv, linear\n"
+            "for f in (lambda: linear.TernaryMatrix(np.zeros((32, 8), np.uint8), np.zeros((1, 8), np.uint16), 8, 128,"
+            " device='cpu'), lambda: linear.quantize(torch.zeros((1, 128)))):\n"
+            "    try:\n"
+            "        f()\n"
+            "    except gpudrv.KernelError as e:\n"
+            "        print('raised', 'not built' in str(e))\n")
+    env = dict(os.environ, KINDI_KT_LIB=str(tmp_path / "absent.so"))
+    r = subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert r.stdout.split("\n")[:2] == ["raised True", "raised True"], r.stdout
