@@ -144,13 +144,16 @@ def test_gemv_token_invariance(kt, R, C):
         assert np.array_equal(host(Y), tree[:M]), M
 
 
-@pytest.mark.parametrize("R,C", [(5120, 5120), (1024, 5120), (17408, 5120), (5120, 17408), (256, 24576)])
+@pytest.mark.parametrize("R,C", [(5120, 5120), (1024, 5120), (17408, 5120), (5120, 17408), (256, 24576), (17403, 5120),
+                                 (256, 20480), (256, 22528)])
 def test_gemv_27b_tokens(kt, R, C):
     """the config 3 shapes at M = 1, 3, 4, 5, 6, 8, 13, 16, 32, against the oracle: every launch kind that serves them
     (the v_dot4 kernels at 1 - 2 tokens, at 3 below 2^26 weights, at 4 below 2^25 and at 5 - 7 below 2^24; the
     16x16x64 matrix-core kernel above those up to 10 K slices; the 32x32x32 one above 10 slices, C = 24576: 12
-    slices, from 8 tokens).
-    int32 group values and fp32 outputs bit-exact against the oracle's decode tree, with and without the dbg output"""
+    slices, from 8 tokens). Edges: a ragged row count on a 2^26-weight launch (17403: the matrix cores from 3 tokens
+    with a partial last tile and row group), exactly 10 K slices (C = 20480, the 16x16x64 kernel's limit) and 11
+    (C = 22528, the first on the 32x32x32 kernel). int32 group values and fp32 outputs bit-exact against the
+    oracle's decode tree, with and without the dbg output"""
     lib, linear = kt
     say("gemv 27B tokens", R, C)
     W, dig, bc, dpm = upload(linear, R, C, 3 * R + C)
