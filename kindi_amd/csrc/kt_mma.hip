@@ -223,7 +223,7 @@ __device__ __forceinline__ kt_v4i km_digits16(uint32_t w){
   return B;
 }
 
-/* up to 10 K slices (640 threads, 3 waves a SIMD, activations 4 units ahead). The B operands are the unsigned digits
+/* up to 10 K slices (640 threads, 3 waves a SIMD, activations 2 units ahead). The B operands are the unsigned digits
    d = t + 1 (masks and shifts of the kt2 word, no lookup): an MFMA then gives the exact integer sum d q, and the
    unit value is v = sum d q - XA (XA = sum q, the quantizer's), the same integer as sum t q. The weights, scales,
    XS and XA are read through buffer resources that span exactly their buffers, with 32-bit offsets. */
@@ -231,7 +231,9 @@ template <bool DBG>
 __global__ void __launch_bounds__(640) k_gemv_m16(const KtGemvArgs a, const int8_t* __restrict__ xq,
                                                   const float* __restrict__ xs, const int* __restrict__ xav,
                                                   int32_t* __restrict__ dbg, int KS){
-  constexpr int NT = KM_TOK, KM_PF = 4;                          /* tokens a pass, activation units loaded ahead */
+  /* activation units loaded ahead: 2 (measured on MI355X, 27B-class step at 16 tokens: 1, 2, 3, 4, 6 units ahead
+     4.03, 3.85, 3.87, 3.92, 4.03 ms; even at 3 - 8 tokens) */
+  constexpr int NT = KM_TOK, KM_PF = 2;                          /* tokens a pass */
   extern __shared__ __attribute__((aligned(16))) uint8_t kt_lds[];
   float* red = (float*)kt_lds;                                   /* [KS][NT][32] slice sums */
   const int NU = a.NU, S = kt_steps(NU);
