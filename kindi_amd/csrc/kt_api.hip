@@ -24,7 +24,7 @@ template <bool DBG>
 __global__ void k_gemv_pair(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
 template <int NT, bool DBG, int LB>
 __global__ void k_gemv_mma(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
-template <bool DBG>
+template <bool DBG, int KQ>
 __global__ void k_gemv_m16(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
 template <bool GRP, bool DBG, bool MS>
 __global__ void k_q8_mma(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
@@ -60,6 +60,12 @@ size_t kt_moe1_down_lds(int k, int KS);
 #ifndef KT_STEPM_WAVES
 #define KT_STEPM_WAVES 2048           /* multi-token grids of at most this many one-step waves take k_gemv_stepm */
 #endif
+#ifndef KT_M16Q_WAVES
+#define KT_M16Q_WAVES 4096            /* matrix-core grids of at most this many waves split a slice over 4 waves */
+#endif
+#ifndef KT_M16Q_MAXM
+#define KT_M16Q_MAXM 8                /* ... at up to this many tokens */
+#endif
 #ifndef KT_PAIR_WAVES
 #define KT_PAIR_WAVES 6144             /* one-token grids of more waves take two row groups a block (k_gemv_pair) */
 #endif
@@ -80,31 +86,19 @@ static int kt_kslices(int NU){
 }
 
 /* up to 32 ternary tokens: the matrix-core product (the same numbers and tree, so the same bits), tiles of 32 rows
-   of one matrix, passes of 16 tokens. It pays over the v_dot4 kernels from 3 tokens on launches of 2^26 weights or
-   more, 4 tokens on 2^25, 5 tokens on 2^24, and from 8 tokens on any launch. Measured on MI355X with k_gemv_m16, per
-   launch over 16 27B-class layers and per 2B-class layer: at 3 tokens gate/up (2^26.4) 21.6 -> 18.6 us and down
-   19.5 -> 13.9 us, while q/k/v (2^25.1) and o stay faster on v_dot4 (7.98 against 8.09, 7.03 against 7.70 us); at 4
-   tokens q/k/v 8.68 -> 8.31 us, while o (2^24.6) and the 2B gate/up launch (2^24.6, one K slice) stay faster on
-   v_dot4 (7.67 against 7.80 us; 2B layer 18.3 against 19.6 us); at 5 tokens the 27B layer 81.1 -> 48.9 us and the
-   2B layer 26.9 -> 26.0 us; at 2 tokens v_dot4 is faster on every launch (27B layer 43.8 against 48.1 us) */
+   of one matrix, passes of 16 tokens, on every launch from 3 tokens (measured on MI355X with k_gemv_m16 and its
+   k-lanes split over 4 waves on small grids, per launch over 16 27B-class layers and per 2B-class layer: 27B layer
+   at 3 / 5 / 7 tokens 56.1 / 81.1 / 50.5 -> 46.6 / 47.8 / 49.6 us, 2B layer 18.8 / 26.0 / 27.4 -> 18.7 / 19.1 /
+   19.9 us against the v_dot4 kernels or the earlier size rule; at 2 tokens the v_dot4 kernels stay faster, 27B
+   layer 43.9 against 46.1 us, 2B layer 13.6 against 18.2 us) */
 #ifndef KT_MMA_MIN
 #define KT_MMA_MIN 3
-#endif
-#ifndef KT_MMA_MID
-#define KT_MMA_MID 5                   /* from here 2^24 weights suffice; one token fewer doubles it */
-#endif
-#ifndef KT_MMA_ANY
-#define KT_MMA_ANY 8
 #endif
 #define KT_Q8_MMA_MIN 12               /* q8_0 dense: the matrix-core product from 12 tokens */
 #define KT_MMA_MAX 32
 #define KT_Q8_MMA_KS 8                 /* q8_0 matrix-core product: K slices a block (kt_mma.hip KM_Q8_KS) */
 static bool kt_use_mma(const KtGemvArgs& a){
-  if(a.M < KT_MMA_MIN || a.M > KT_MMA_MAX || (long long)a.M * a.ldq >= (1ll << 30)) return false;
-  if(a.M >= KT_MMA_ANY) return true;
-  long long w = 0;
-  for(int i = 0; i < a.nmat; ++i) w += (long long)a.mat[i].R * a.NU * 128;
-  return w >= (1ll << (24 + (a.M >= KT_MMA_MID ? 0 : KT_MMA_MID - a.M)));
+  return a.M >= KT_MMA_MIN && a.M <= KT_MMA_MAX && (long long)a.M * a.ldq < (1ll << 30);
 }
 
 static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, const int* xa, int32_t* dbg,
@@ -120,9 +114,20 @@ static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, const 
     /* 16x16x64 tiles for every matrix-core launch up to 10 slices (measured on MI355X: 27B-class step at 16 tokens
        4.10 -> 3.99 ms; 2B-class layer at 8 tokens 27.26 -> 27.03 us, at 6 and 7 tokens even; 27B-class launches at
        6 tokens q/k/v 8.72 -> 8.38, gate/up 22.04 -> 19.51, down 16.14 -> 14.62 us) */
-    const size_t lds16 = lds + (size_t)ks * 256 * 4;                        /* + XA */
-    if(dbg) hipLaunchKernelGGL((k_gemv_m16<true>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);
-    else hipLaunchKernelGGL((k_gemv_m16<false>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);
+    const long long waves4 = (long long)tiles * grid.y * ks * 4;
+    if(ks <= 4 && a.M <= KT_M16Q_MAXM && waves4 <= KT_M16Q_WAVES){
+      /* the k-lanes of a slice over 4 waves where the grid leaves SIMDs short of waves (measured on MI355X: 2B-class
+         layer at 8 tokens 27.0 -> 20.1 us, 27B-class q/k/v at 4 - 6 tokens 8.2 -> 7.3 - 7.6 us; at 16 tokens 27B
+         q/k/v and o were slower split, 8.5 -> 9.7 us, so the split stops at 8 tokens; a cap of 8192 waves instead of
+         4096 measured even) */
+      const size_t lq = (size_t)ks * 4 * (16 * 32 * 4 + 512 * 4);             /* pair sums, XS + XA a wave */
+      if(dbg) hipLaunchKernelGGL((k_gemv_m16<true, 4>), grid, dim3(256 * ks), lq, s, a, xq, xs, xa, dbg, ks);
+      else hipLaunchKernelGGL((k_gemv_m16<false, 4>), grid, dim3(256 * ks), lq, s, a, xq, xs, xa, dbg, ks);
+    } else {
+      const size_t lds16 = lds + (size_t)ks * 256 * 4;                      /* + XA */
+      if(dbg) hipLaunchKernelGGL((k_gemv_m16<true, 1>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);
+      else hipLaunchKernelGGL((k_gemv_m16<false, 1>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);
+    }
   } else {
     /* above 10 slices, or buffers past 32-bit offsets: 32x32x32 tiles, the 1024-thread bound (activations loaded in
        place, 124 VGPRs) */

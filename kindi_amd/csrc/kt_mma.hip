@@ -1,5 +1,5 @@
 /* kt_mma.hip - the decode product on the matrix cores for up to 32 tokens (passes of 16; the launcher takes it from 3
-   to 8 tokens on, by launch size) (k_tc_mv*, tc_hip.cu:180-240, at the verify widths spec.py:45 takes them): ternary
+   tokens) (k_tc_mv*, tc_hip.cu:180-240, at the verify widths spec.py:45 takes them): ternary
    weights (kt2) against int8 token rows, the same numbers and the
    same summation tree as k_gemv_flat, so a token's bits do not depend on which of the two kernels ran it.
 
@@ -226,18 +226,24 @@ __device__ __forceinline__ kt_v4i km_digits16(uint32_t w){
 /* up to 10 K slices (640 threads, 3 waves a SIMD, activations 2 units ahead). The B operands are the unsigned digits
    d = t + 1 (masks and shifts of the kt2 word, no lookup): an MFMA then gives the exact integer sum d q, and the
    unit value is v = sum d q - XA (XA = sum q, the quantizer's), the same integer as sum t q. The weights, scales,
-   XS and XA are read through buffer resources that span exactly their buffers, with 32-bit offsets. */
-template <bool DBG>
-__global__ void __launch_bounds__(640) k_gemv_m16(const KtGemvArgs a, const int8_t* __restrict__ xq,
+   XS and XA are read through buffer resources that span exactly their buffers, with 32-bit offsets.
+   KQ = 4 (up to 4 slices, small grids): the slice's k-lanes are split over 4 waves, wave (ks, q) taking k-lanes 2 q
+   and 2 q + 1; each writes its pair sum p_q = chain(2 q) + chain(2 q + 1) to LDS and wave 0 forms the butterfly's
+   tree (p0 + p1) + (p2 + p3), which is the KQ = 1 tree ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)), then the
+   slices in order: the same bits with 4 times the waves. */
+template <bool DBG, int KQ>
+__global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvArgs a, const int8_t* __restrict__ xq,
                                                   const float* __restrict__ xs, const int* __restrict__ xav,
                                                   int32_t* __restrict__ dbg, int KS){
   /* activation units loaded ahead: 2 (measured on MI355X, 27B-class step at 16 tokens: 1, 2, 3, 4, 6 units ahead
      4.03, 3.85, 3.87, 3.92, 4.03 ms; even at 3 - 8 tokens) */
   constexpr int NT = KM_TOK, KM_PF = 2;                          /* tokens a pass */
+  constexpr int CW = KT_KL / KQ;                                 /* k-lanes a wave */
   extern __shared__ __attribute__((aligned(16))) uint8_t kt_lds[];
-  float* red = (float*)kt_lds;                                   /* [KS][NT][32] slice sums */
+  float* red = (float*)kt_lds;                                   /* [KS][KQ][NT][32] slice (pair) sums */
   const int NU = a.NU, S = kt_steps(NU);
-  const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, wvi = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ks = wvi / KQ, q = wvi % KQ, cb = q * CW;            /* slice, quarter, first k-lane */
   const int g = lane >> 4, n = lane & 15;
   const int tile = blockIdx.x, t0 = blockIdx.y * NT;
   int mi = 0;
@@ -261,7 +267,7 @@ __global__ void __launch_bounds__(640) k_gemv_m16(const KtGemvArgs a, const int8
   const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc((void*)xav, (short)0, a.M * a.ldxs * 4, 0x00020000);
 
   /* the slice's XS and XA [16 units][16 tokens] to this wave's LDS regions (after the weight loads are issued) */
-  float* xsl = (float*)(kt_lds + (size_t)KS * NT * 32 * 4) + (size_t)ks * 512;
+  float* xsl = (float*)(kt_lds + (size_t)KS * KQ * NT * 32 * 4) + (size_t)wvi * 512;
   int* xal = (int*)(xsl + 256);
   float xsv[4];
   int xav4[4];
@@ -283,8 +289,8 @@ __global__ void __launch_bounds__(640) k_gemv_m16(const KtGemvArgs a, const int8
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, a.M * a.ldq, 0x00020000);
   const uint32_t xoff = n < nt ? (uint32_t)((t0 + n) * a.ldq + 16 * g) : (1u << 30);
   uint4 xa[KM_PF][2];
-  auto ld_act = [&](int un, uint4* dst){                         /* unit un = 2 c + j: both halves */
-    const int c = un >> 1, j = un & 1, u = (s_lo + j) * KT_KL + c;
+  auto ld_act = [&](int un, uint4* dst){                         /* the wave's unit un = 2 (c - cb) + j: both halves */
+    const int c = cb + (un >> 1), j = un & 1, u = (s_lo + j) * KT_KL + c;
     const int uu = (j < ns && u < NU) ? u : 0;
     dst[0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + uu * 128, 0, 0));
     dst[1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + uu * 128 + 64, 0, 0));
@@ -294,39 +300,40 @@ __global__ void __launch_bounds__(640) k_gemv_m16(const KtGemvArgs a, const int8
 #pragma unroll
   for(int un = 0; un < KM_PF; ++un) ld_act(un, xa[un]);
   /* the slice's 16 units' chunks (k-lane-major) and both row blocks' scales (b = 0 | b = 1 << 16), unconditional */
-  uint4 wq[2][KT_KL];
-  uint32_t hq[2][KT_KL];
+  uint4 wq[2][CW];
+  uint32_t hq[2][CW];
 #pragma unroll
-  for(int c = 0; c < KT_KL; ++c)
+  for(int cc = 0; cc < CW; ++cc)
 #pragma unroll
     for(int j = 0; j < 2; ++j){
-      const int s = s_lo + j, u = s * KT_KL + c;
+      const int c = cb + cc, s = s_lo + j, u = s * KT_KL + c;
       const bool ok = j < ns && u < NU;
       const uint32_t wo = ok && cok ? (uint32_t)kt_widx(NU, crg, s, ch, c, cr) * 16 : 0u;
-      wq[j][c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo, 0, 2));
+      wq[j][cc] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo, 0, 2));
       const uint32_t h0 = __builtin_amdgcn_raw_buffer_load_b16(
           hr, ok && ook[0] ? (uint32_t)kt_sidx(NU, rg0 + (n >> 3), u, cr) * 2 : 0u, 0, 0);
       const uint32_t h1 = __builtin_amdgcn_raw_buffer_load_b16(
           hr, ok && ook[1] ? (uint32_t)kt_sidx(NU, rg0 + 2 + (n >> 3), u, cr) * 2 : 0u, 0, 0);
-      hq[j][c] = h0 | h1 << 16;
+      hq[j][cc] = h0 | h1 << 16;
     }
 #pragma unroll
   for(int i = 0; i < 4; ++i){ xsl[lane + 64 * i] = xsv[i]; xal[lane + 64 * i] = xav4[i]; }
   kt_wave_sync();
 #pragma unroll
-  for(int c = 0; c < KT_KL; ++c){
+  for(int cc = 0; cc < CW; ++cc){
+    const int c = cb + cc;
     float chain[8];                                              /* element 4 b + e: row block b, token 4 g + e */
 #pragma unroll
     for(int e = 0; e < 8; ++e) chain[e] = 0.0f;
 #pragma unroll
     for(int j = 0; j < 2; ++j){
-      const int un = 2 * c + j, u = (s_lo + j) * KT_KL + c;
+      const int un = 2 * cc + j, u = (s_lo + j) * KT_KL + c;
       const bool uok = j < ns && u < NU;                         /* wave-uniform */
       const uint4 x0 = xa[un % KM_PF][0], x1 = xa[un % KM_PF][1];
-      if(un + KM_PF < 2 * KT_KL) ld_act(un + KM_PF, xa[un % KM_PF]);
+      if(un + KM_PF < 2 * CW) ld_act(un + KM_PF, xa[un % KM_PF]);
       if(uok){
         /* word g of the four chunks of row n */
-        unsigned w0 = wq[j][c].x, w1 = wq[j][c].y, w2 = wq[j][c].z, w3 = wq[j][c].w;
+        unsigned w0 = wq[j][cc].x, w1 = wq[j][cc].y, w2 = wq[j][cc].z, w3 = wq[j][cc].w;
         km_swap32(w0, w2); km_swap32(w1, w3);
         km_swap16(w0, w1); km_swap16(w2, w3);
         const kt_v4i A0 = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w};
@@ -340,8 +347,8 @@ __global__ void __launch_bounds__(640) k_gemv_m16(const KtGemvArgs a, const int8
         const int xq4[4] = {xa4.x, xa4.y, xa4.z, xa4.w};
 #pragma unroll
         for(int e = 0; e < 4; ++e){ d0[e] -= xq4[e]; d1[e] -= xq4[e]; }                      /* v = sum d q - XA */
-        const float dd0 = ook[0] ? kt_h2f((uint16_t)hq[j][c]) : 0.0f;
-        const float dd1 = ook[1] ? kt_h2f((uint16_t)(hq[j][c] >> 16)) : 0.0f;
+        const float dd0 = ook[0] ? kt_h2f((uint16_t)hq[j][cc]) : 0.0f;
+        const float dd1 = ook[1] ? kt_h2f((uint16_t)(hq[j][cc] >> 16)) : 0.0f;
         const float4 sx = *(const float4*)(xsl + (j * 8 + c) * 16 + 4 * g);                /* tokens 4 g .. + 3 */
         const float sxv[4] = {sx.x, sx.y, sx.z, sx.w};
 #pragma unroll
@@ -356,28 +363,43 @@ __global__ void __launch_bounds__(640) k_gemv_m16(const KtGemvArgs a, const int8
         }
       }
     }
-    /* the butterfly's tree over c, as it completes */
+    /* the butterfly's tree over c, as it completes (KQ = 4: this wave's pair sum) */
 #pragma unroll
     for(int e = 0; e < 8; ++e){
-      if(c == 0 || c == 2 || c == 4 || c == 6) pend[e] = chain[e];
-      else if(c == 1) t01[e] = pend[e] + chain[e];
-      else if(c == 3) t23[e] = t01[e] + (pend[e] + chain[e]);
-      else if(c == 5) t45[e] = pend[e] + chain[e];
-      else part[e] = t23[e] + (t45[e] + (pend[e] + chain[e]));
+      if constexpr(KQ == 1){
+        if(c == 0 || c == 2 || c == 4 || c == 6) pend[e] = chain[e];
+        else if(c == 1) t01[e] = pend[e] + chain[e];
+        else if(c == 3) t23[e] = t01[e] + (pend[e] + chain[e]);
+        else if(c == 5) t45[e] = pend[e] + chain[e];
+        else part[e] = t23[e] + (t45[e] + (pend[e] + chain[e]));
+      } else {
+        if(cc == 0) pend[e] = chain[e];
+        else part[e] = pend[e] + chain[e];
+      }
     }
   }
-  /* slices in order */
+  /* slices in order (KQ = 4: the pair sums of a slice first, (p0 + p1) + (p2 + p3)) */
 #pragma unroll
-  for(int e = 0; e < 8; ++e) red[((size_t)ks * NT + 4 * g + (e & 3)) * 32 + 16 * (e >> 2) + n] = part[e];
+  for(int e = 0; e < 8; ++e) red[((size_t)(ks * KQ + q) * NT + 4 * g + (e & 3)) * 32 + 16 * (e >> 2) + n] = part[e];
   __syncthreads();
-  if(ks == 0){
-    float v[8];
+  if(wvi == 0){
+    auto slice = [&](int k, float (&w)[8]){
+      float p[KQ][8];
 #pragma unroll
-    for(int e = 0; e < 8; ++e) v[e] = red[(size_t)(4 * g + (e & 3)) * 32 + 16 * (e >> 2) + n];
+      for(int qq = 0; qq < KQ; ++qq)
+#pragma unroll
+        for(int e = 0; e < 8; ++e) p[qq][e] = red[((size_t)(k * KQ + qq) * NT + 4 * g + (e & 3)) * 32 + 16 * (e >> 2) + n];
+#pragma unroll
+      for(int e = 0; e < 8; ++e){
+        if constexpr(KQ == 1) w[e] = p[0][e];
+        else w[e] = (p[0][e] + p[1][e]) + (p[2][e] + p[3][e]);
+      }
+    };
+    float v[8];
+    slice(0, v);
     for(int k = 1; k < KS; ++k){
       float w[8];
-#pragma unroll
-      for(int e = 0; e < 8; ++e) w[e] = red[((size_t)k * NT + 4 * g + (e & 3)) * 32 + 16 * (e >> 2) + n];
+      slice(k, w);
 #pragma unroll
       for(int e = 0; e < 8; ++e) v[e] += w[e];
     }
@@ -391,8 +413,10 @@ __global__ void __launch_bounds__(640) k_gemv_m16(const KtGemvArgs a, const int8
   }
 }
 
-template __global__ void k_gemv_m16<false>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
-template __global__ void k_gemv_m16<true>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
+template __global__ void k_gemv_m16<false, 1>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
+template __global__ void k_gemv_m16<true, 1>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
+template __global__ void k_gemv_m16<false, 4>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
+template __global__ void k_gemv_m16<true, 4>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
 
 /* ------------------------------------------------------------------ q8_0 on the matrix cores
    The q8_0 product (kq8 weights against int8 rows with per-32 scales, lt_mv_q8 lightning.cu:258-284, k_q8

@@ -123,8 +123,8 @@ def test_gemv_hp_pairs(kt, R, C):
 @pytest.mark.parametrize("R,C", [(640, 1024), (2048, 6144), (4096, 4096)])
 def test_gemv_token_invariance(kt, R, C):
     """a token's output does not depend on how many tokens share the pass (tc_hip.cu:14-15), for M = 1 .. 32: the
-    bandwidth kernels and the matrix-core kernels (from 5 tokens at 2^24 weights, from 8 on any; 16x16x64 tiles up to
-    10 K slices) give the same bits"""
+    bandwidth kernels (1 - 2 tokens) and the matrix-core kernels (from 3 tokens; 16x16x64 tiles up to 10 K slices, their
+    k-lanes split over 4 waves on small grids up to 8 tokens) give the same bits"""
     lib, linear = kt
     say("gemv T-invariance", R, C)
     W, dig, bc, dpm = upload(linear, R, C, 5 + R)
@@ -148,10 +148,10 @@ def test_gemv_token_invariance(kt, R, C):
                                  (256, 20480), (256, 22528)])
 def test_gemv_27b_tokens(kt, R, C):
     """the config 3 shapes at M = 1, 3, 4, 5, 6, 8, 13, 16, 32, against the oracle: every launch kind that serves them
-    (the v_dot4 kernels at 1 - 2 tokens, at 3 below 2^26 weights, at 4 below 2^25 and at 5 - 7 below 2^24; the
-    16x16x64 matrix-core kernel above those up to 10 K slices; the 32x32x32 one above 10 slices, C = 24576: 12
-    slices, from 8 tokens). Edges: a ragged row count on a 2^26-weight launch (17403: the matrix cores from 3 tokens
-    with a partial last tile and row group), exactly 10 K slices (C = 20480, the 16x16x64 kernel's limit) and 11
+    (the v_dot4 kernels at 1 token; the 16x16x64 matrix-core kernel from 3 tokens up to 10 K slices, its k-lanes
+    split over 4 waves on grids of up to 4096 split waves at up to 8 tokens (R = 1024, 5120 at C = 5120), whole
+    otherwise; the 32x32x32 one above 10 slices, C = 24576: 12 slices). Edges: a ragged row count (17403: a partial
+    last tile and row group), exactly 10 K slices (C = 20480, the 16x16x64 kernel's limit) and 11
     (C = 22528, the first on the 32x32x32 kernel). int32 group values and fp32 outputs bit-exact against the
     oracle's decode tree, with and without the dbg output"""
     lib, linear = kt
