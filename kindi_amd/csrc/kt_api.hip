@@ -61,10 +61,7 @@ size_t kt_moe1_down_lds(int k, int KS);
 #define KT_STEPM_WAVES 2048           /* multi-token grids of at most this many one-step waves take k_gemv_stepm */
 #endif
 #ifndef KT_M16Q_WAVES
-#define KT_M16Q_WAVES 4096            /* matrix-core grids of at most this many waves split a slice over 4 waves */
-#endif
-#ifndef KT_M16Q_MAXM
-#define KT_M16Q_MAXM 8                /* ... at up to this many tokens */
+#define KT_M16Q_WAVES 16384           /* matrix-core grids of at most this many waves split a slice over 4 waves */
 #endif
 #ifndef KT_PAIR_WAVES
 #define KT_PAIR_WAVES 6144             /* one-token grids of more waves take two row groups a block (k_gemv_pair) */
@@ -115,11 +112,11 @@ static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, const 
        4.10 -> 3.99 ms; 2B-class layer at 8 tokens 27.26 -> 27.03 us, at 6 and 7 tokens even; 27B-class launches at
        6 tokens q/k/v 8.72 -> 8.38, gate/up 22.04 -> 19.51, down 16.14 -> 14.62 us) */
     const long long waves4 = (long long)tiles * grid.y * ks * 4;
-    if(ks <= 4 && a.M <= KT_M16Q_MAXM && waves4 <= KT_M16Q_WAVES){
-      /* the k-lanes of a slice over 4 waves where the grid leaves SIMDs short of waves (measured on MI355X: 2B-class
-         layer at 8 tokens 27.0 -> 20.1 us, 27B-class q/k/v at 4 - 6 tokens 8.2 -> 7.3 - 7.6 us; at 16 tokens 27B
-         q/k/v and o were slower split, 8.5 -> 9.7 us, so the split stops at 8 tokens; a cap of 8192 waves instead of
-         4096 measured even) */
+    if(ks <= 4 && waves4 <= KT_M16Q_WAVES){
+      /* the k-lanes of a slice over 4 waves (measured on MI355X against whole-slice waves: 27B-class step at 16
+         tokens 3.85 -> 3.71 ms, q/k/v 8.5 -> 7.9 us, gate/up 25.3 -> 24.7 us; 27B-class layer at 3 tokens 47.6 -> 44.1
+         us; 2B-class layer at 8 tokens 27.0 -> 18.0 us; a cap of 4096 or 8192 split waves, which left gate/up whole,
+         was slower) */
       const size_t lq = (size_t)ks * 4 * (16 * 32 * 4 + 512 * 4);             /* pair sums, XS + XA a wave */
       if(dbg) hipLaunchKernelGGL((k_gemv_m16<true, 4>), grid, dim3(256 * ks), lq, s, a, xq, xs, xa, dbg, ks);
       else hipLaunchKernelGGL((k_gemv_m16<false, 4>), grid, dim3(256 * ks), lq, s, a, xq, xs, xa, dbg, ks);

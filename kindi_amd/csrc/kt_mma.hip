@@ -227,10 +227,10 @@ __device__ __forceinline__ kt_v4i km_digits16(uint32_t w){
    d = t + 1 (masks and shifts of the kt2 word, no lookup): an MFMA then gives the exact integer sum d q, and the
    unit value is v = sum d q - XA (XA = sum q, the quantizer's), the same integer as sum t q. The weights, scales,
    XS and XA are read through buffer resources that span exactly their buffers, with 32-bit offsets.
-   KQ = 4 (up to 4 slices, small grids): the slice's k-lanes are split over 4 waves, wave (ks, q) taking k-lanes 2 q
-   and 2 q + 1; each writes its pair sum p_q = chain(2 q) + chain(2 q + 1) to LDS and wave 0 forms the butterfly's
-   tree (p0 + p1) + (p2 + p3), which is the KQ = 1 tree ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)), then the
-   slices in order: the same bits with 4 times the waves. */
+   KQ = 4 (up to 4 slices): the slice's k-lanes are split over 4 waves, wave (ks, q) taking k-lanes 2 q and 2 q + 1
+   (and staging only those units' XS and XA); each writes its pair sum p_q = chain(2 q) + chain(2 q + 1) to LDS and
+   wave 0 forms the butterfly's tree (p0 + p1) + (p2 + p3), which is the KQ = 1 tree ((c0 + c1) + (c2 + c3)) +
+   ((c4 + c5) + (c6 + c7)), then the slices in order: the same bits with 4 times the waves. */
 template <bool DBG, int KQ>
 __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvArgs a, const int8_t* __restrict__ xq,
                                                   const float* __restrict__ xs, const int* __restrict__ xav,
@@ -266,19 +266,25 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
   const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc((void*)xs, (short)0, a.M * a.ldxs * 4, 0x00020000);
   const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc((void*)xav, (short)0, a.M * a.ldxs * 4, 0x00020000);
 
-  /* the slice's XS and XA [16 units][16 tokens] to this wave's LDS regions (after the weight loads are issued) */
+  /* the units' XS and XA [16 units][16 tokens] to this wave's LDS region (after the weight loads are issued) */
   float* xsl = (float*)(kt_lds + (size_t)KS * KQ * NT * 32 * 4) + (size_t)wvi * 512;
   int* xal = (int*)(xsl + 256);
-  float xsv[4];
-  int xav4[4];
+  /* entry (j 8 + c) 16 + token of the region: KQ = 1 stages the slice's 16 units, KQ = 4 only its own 4 (k-lanes cb,
+     cb + 1 of both steps) */
+  constexpr int NI = 4 / KQ;
+  float xsv[NI];
+  int xav4[NI];
+  int xdst[NI];
 #pragma unroll
-  for(int i = 0; i < 4; ++i){
+  for(int i = 0; i < NI; ++i){
     const int idx = lane + 64 * i, un = idx >> 4, tl = idx & 15;
-    const int u = (s_lo + (un >> 3)) * KT_KL + (un & 7);
+    const int j = KQ == 1 ? un >> 3 : un >> 1, c = KQ == 1 ? un & 7 : cb + (un & 1);
+    const int u = (s_lo + j) * KT_KL + c;
     const int t = t0 + tl < a.M ? t0 + tl : t0;
     const uint32_t o = (uint32_t)(t * a.ldxs + (u < NU ? u : 0)) * 4;
     xsv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, o, 0, 0));
     xav4[i] = (int)__builtin_amdgcn_raw_buffer_load_b32(ar, o, 0, 0);
+    xdst[i] = (j * 8 + c) * 16 + tl;
   }
   float part[8], t01[8], t23[8], t45[8], pend[8];
 #pragma unroll
@@ -317,7 +323,7 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
       hq[j][cc] = h0 | h1 << 16;
     }
 #pragma unroll
-  for(int i = 0; i < 4; ++i){ xsl[lane + 64 * i] = xsv[i]; xal[lane + 64 * i] = xav4[i]; }
+  for(int i = 0; i < NI; ++i){ xsl[xdst[i]] = xsv[i]; xal[xdst[i]] = xav4[i]; }
   kt_wave_sync();
 #pragma unroll
   for(int cc = 0; cc < CW; ++cc){

@@ -124,7 +124,7 @@ def test_gemv_hp_pairs(kt, R, C):
 def test_gemv_token_invariance(kt, R, C):
     """a token's output does not depend on how many tokens share the pass (tc_hip.cu:14-15), for M = 1 .. 32: the
     bandwidth kernels (1 - 2 tokens) and the matrix-core kernels (from 3 tokens; 16x16x64 tiles up to 10 K slices, their
-    k-lanes split over 4 waves on small grids up to 8 tokens) give the same bits"""
+    k-lanes split over 4 waves up to 4 slices) give the same bits"""
     lib, linear = kt
     say("gemv T-invariance", R, C)
     W, dig, bc, dpm = upload(linear, R, C, 5 + R)
@@ -149,8 +149,8 @@ def test_gemv_token_invariance(kt, R, C):
 def test_gemv_27b_tokens(kt, R, C):
     """the config 3 shapes at M = 1, 3, 4, 5, 6, 8, 13, 16, 32, against the oracle: every launch kind that serves them
     (the v_dot4 kernels at 1 token; the 16x16x64 matrix-core kernel from 3 tokens up to 10 K slices, its k-lanes
-    split over 4 waves on grids of up to 4096 split waves at up to 8 tokens (R = 1024, 5120 at C = 5120), whole
-    otherwise; the 32x32x32 one above 10 slices, C = 24576: 12 slices). Edges: a ragged row count (17403: a partial
+    split over 4 waves up to 4 slices (C = 5120), whole above (C = 17408, 20480); the 32x32x32 one above 10 slices,
+    C = 22528, 24576). Edges: a ragged row count (17403: a partial
     last tile and row group), exactly 10 K slices (C = 20480, the 16x16x64 kernel's limit) and 11
     (C = 22528, the first on the 32x32x32 kernel). int32 group values and fp32 outputs bit-exact against the
     oracle's decode tree, with and without the dbg output"""
