@@ -24,7 +24,7 @@ template <bool DBG>
 __global__ void k_gemv_pair(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
 template <int NT, bool DBG, int LB>
 __global__ void k_gemv_mma(const KtGemvArgs, const int8_t*, const float*, int32_t*, int);
-template <bool DBG, int KQ>
+template <bool DBG, int KQ, bool MS>
 __global__ void k_gemv_m16(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
 template <bool GRP, bool DBG, bool MS>
 __global__ void k_q8_mma(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
@@ -59,6 +59,9 @@ size_t kt_moe1_down_lds(int k, int KS);
 #define KT_INVALID ((int)hipErrorInvalidValue)
 #ifndef KT_STEPM_WAVES
 #define KT_STEPM_WAVES 2048           /* multi-token grids of at most this many one-step waves take k_gemv_stepm */
+#endif
+#ifndef KT_M16Q_MSM
+#define KT_M16Q_MSM 8                 /* ... above 4 slices at up to this many tokens */
 #endif
 #ifndef KT_M16Q_WAVES
 #define KT_M16Q_WAVES 16384           /* matrix-core grids of at most this many waves split a slice over 4 waves */
@@ -111,19 +114,28 @@ static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, const 
     /* 16x16x64 tiles for every matrix-core launch up to 10 slices (measured on MI355X: 27B-class step at 16 tokens
        4.10 -> 3.99 ms; 2B-class layer at 8 tokens 27.26 -> 27.03 us, at 6 and 7 tokens even; 27B-class launches at
        6 tokens q/k/v 8.72 -> 8.38, gate/up 22.04 -> 19.51, down 16.14 -> 14.62 us) */
-    const long long waves4 = (long long)tiles * grid.y * ks * 4;
-    if(ks <= 4 && waves4 <= KT_M16Q_WAVES){
+    const bool ms = ks > 4;                                                 /* more slices than 4 groups */
+    const int G = ms ? 4 : ks;                                              /* slice groups of the split */
+    const long long waves4 = (long long)tiles * grid.y * G * 4;
+    if(waves4 <= KT_M16Q_WAVES && (!ms || a.M <= KT_M16Q_MSM)){
       /* the k-lanes of a slice over 4 waves (measured on MI355X against whole-slice waves: 27B-class step at 16
          tokens 3.85 -> 3.71 ms, q/k/v 8.5 -> 7.9 us, gate/up 25.3 -> 24.7 us; 27B-class layer at 3 tokens 47.6 -> 44.1
          us; 2B-class layer at 8 tokens 27.0 -> 18.0 us; a cap of 4096 or 8192 split waves, which left gate/up whole,
-         was slower) */
-      const size_t lq = (size_t)ks * 4 * (16 * 32 * 4 + 512 * 4);             /* pair sums, XS + XA a wave */
-      if(dbg) hipLaunchKernelGGL((k_gemv_m16<true, 4>), grid, dim3(256 * ks), lq, s, a, xq, xs, xa, dbg, ks);
-      else hipLaunchKernelGGL((k_gemv_m16<false, 4>), grid, dim3(256 * ks), lq, s, a, xq, xs, xa, dbg, ks);
+         was slower). Above 4 slices a wave takes up to ceil(KS / 4) slices (the 27B down launch at 3 / 5 / 8 tokens
+         13.8 / 14.2 / 15.0 -> 12.8 / 13.0 / 14.2 us; slower at 16 tokens, 17.35 -> 17.75 us, so up to 8 tokens) */
+      const size_t lq = (size_t)ks * 4 * 16 * 32 * 4 + (size_t)G * 4 * 512 * 4;   /* pair sums, XS + XA a wave */
+      const dim3 bq(256 * G);
+      if(ms){
+        if(dbg) hipLaunchKernelGGL((k_gemv_m16<true, 4, true>), grid, bq, lq, s, a, xq, xs, xa, dbg, ks);
+        else hipLaunchKernelGGL((k_gemv_m16<false, 4, true>), grid, bq, lq, s, a, xq, xs, xa, dbg, ks);
+      } else {
+        if(dbg) hipLaunchKernelGGL((k_gemv_m16<true, 4, false>), grid, bq, lq, s, a, xq, xs, xa, dbg, ks);
+        else hipLaunchKernelGGL((k_gemv_m16<false, 4, false>), grid, bq, lq, s, a, xq, xs, xa, dbg, ks);
+      }
     } else {
       const size_t lds16 = lds + (size_t)ks * 256 * 4;                      /* + XA */
-      if(dbg) hipLaunchKernelGGL((k_gemv_m16<true, 1>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);
-      else hipLaunchKernelGGL((k_gemv_m16<false, 1>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);
+      if(dbg) hipLaunchKernelGGL((k_gemv_m16<true, 1, false>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);
+      else hipLaunchKernelGGL((k_gemv_m16<false, 1, false>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);
     }
   } else {
     /* above 10 slices, or buffers past 32-bit offsets: 32x32x32 tiles, the 1024-thread bound (activations loaded in

@@ -227,11 +227,13 @@ __device__ __forceinline__ kt_v4i km_digits16(uint32_t w){
    d = t + 1 (masks and shifts of the kt2 word, no lookup): an MFMA then gives the exact integer sum d q, and the
    unit value is v = sum d q - XA (XA = sum q, the quantizer's), the same integer as sum t q. The weights, scales,
    XS and XA are read through buffer resources that span exactly their buffers, with 32-bit offsets.
-   KQ = 4 (up to 4 slices): the slice's k-lanes are split over 4 waves, wave (ks, q) taking k-lanes 2 q and 2 q + 1
-   (and staging only those units' XS and XA); each writes its pair sum p_q = chain(2 q) + chain(2 q + 1) to LDS and
+   KQ = 4: each slice's k-lanes are split over 4 waves, wave (sg, q) taking k-lanes 2 q and 2 q + 1 of slices sg,
+   sg + G, ... (MS: G = 4 slice groups for launches of more than 4 slices, so a block has at most 16 waves; else
+   G = KS, one slice a wave) and staging only those units' XS and
+   XA; for each of its slices it writes the pair sum p_q = chain(2 q) + chain(2 q + 1) to LDS and
    wave 0 forms the butterfly's tree (p0 + p1) + (p2 + p3), which is the KQ = 1 tree ((c0 + c1) + (c2 + c3)) +
    ((c4 + c5) + (c6 + c7)), then the slices in order: the same bits with 4 times the waves. */
-template <bool DBG, int KQ>
+template <bool DBG, int KQ, bool MS>
 __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvArgs a, const int8_t* __restrict__ xq,
                                                   const float* __restrict__ xs, const int* __restrict__ xav,
                                                   int32_t* __restrict__ dbg, int KS){
@@ -243,7 +245,10 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
   float* red = (float*)kt_lds;                                   /* [KS][KQ][NT][32] slice (pair) sums */
   const int NU = a.NU, S = kt_steps(NU);
   const int lane = threadIdx.x & 63, wvi = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int ks = wvi / KQ, q = wvi % KQ, cb = q * CW;            /* slice, quarter, first k-lane */
+  /* KQ = 1: wave ks = slice ks. KQ = 4: G slice groups, wave (sg, q) takes k-lanes 2 q, 2 q + 1 of slices sg,
+     sg + G, sg + 2 G, ... */
+  const int G = MS ? 4 : KS;                                     /* MS: more slices than groups */
+  const int sg = wvi / KQ, q = wvi % KQ, cb = q * CW;            /* slice group, quarter, first k-lane */
   const int g = lane >> 4, n = lane & 15;
   const int tile = blockIdx.x, t0 = blockIdx.y * NT;
   int mi = 0;
@@ -259,7 +264,6 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
 #pragma unroll
   for(int b = 0; b < 2; ++b){ orow[b] = (rg0 + 2 * b + (n >> 3)) * KT_RG + cr; ook[b] = orow[b] < m.R; }
   const int nt = min(NT, a.M - t0);
-  const int s_lo = ks * S / KS, ns = (ks + 1) * S / KS - s_lo;   /* this slice's steps (1 or 2) */
   const int nrg = kt_r8(m.R);
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)m.codes, (short)0, nrg * NU * 256, 0x00020000);
   const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc((void*)m.scales, (short)0, nrg * NU * 16, 0x00020000);
@@ -269,6 +273,12 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
   /* the units' XS and XA [16 units][16 tokens] to this wave's LDS region (after the weight loads are issued) */
   float* xsl = (float*)(kt_lds + (size_t)KS * KQ * NT * 32 * 4) + (size_t)wvi * 512;
   int* xal = (int*)(xsl + 256);
+  /* activations through a buffer resource over the M token rows (lanes past the pass's tokens: past the range,
+     zeros without a memory access) */
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, a.M * a.ldq, 0x00020000);
+  const uint32_t xoff = n < nt ? (uint32_t)((t0 + n) * a.ldq + 16 * g) : (1u << 30);
+  for(int it = 0, ks = sg; MS ? ks < KS : it < 1; ++it, ks += G){                /* !MS: one slice a wave */
+  const int s_lo = ks * S / KS, ns = (ks + 1) * S / KS - s_lo;   /* this slice's steps (1 or 2) */
   /* entry (j 8 + c) 16 + token of the region: KQ = 1 stages the slice's 16 units, KQ = 4 only its own 4 (k-lanes cb,
      cb + 1 of both steps) */
   constexpr int NI = 4 / KQ;
@@ -290,10 +300,6 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
 #pragma unroll
   for(int e = 0; e < 8; ++e){ part[e] = 0.0f; t01[e] = 0.0f; t23[e] = 0.0f; t45[e] = 0.0f; pend[e] = 0.0f; }
 
-  /* activations through a buffer resource over the M token rows (lanes past the pass's tokens: past the range,
-     zeros without a memory access) */
-  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)xq, (short)0, a.M * a.ldq, 0x00020000);
-  const uint32_t xoff = n < nt ? (uint32_t)((t0 + n) * a.ldq + 16 * g) : (1u << 30);
   uint4 xa[KM_PF][2];
   auto ld_act = [&](int un, uint4* dst){                         /* the wave's unit un = 2 (c - cb) + j: both halves */
     const int c = cb + (un >> 1), j = un & 1, u = (s_lo + j) * KT_KL + c;
@@ -387,6 +393,7 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
   /* slices in order (KQ = 4: the pair sums of a slice first, (p0 + p1) + (p2 + p3)) */
 #pragma unroll
   for(int e = 0; e < 8; ++e) red[((size_t)(ks * KQ + q) * NT + 4 * g + (e & 3)) * 32 + 16 * (e >> 2) + n] = part[e];
+  }                                                              /* the wave's slices */
   __syncthreads();
   if(wvi == 0){
     auto slice = [&](int k, float (&w)[8]){
@@ -419,10 +426,11 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
   }
 }
 
-template __global__ void k_gemv_m16<false, 1>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
-template __global__ void k_gemv_m16<true, 1>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
-template __global__ void k_gemv_m16<false, 4>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
-template __global__ void k_gemv_m16<true, 4>(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
+#define KM16_INST(DBG, KQ, MS) template __global__ void k_gemv_m16<DBG, KQ, MS>(const KtGemvArgs, const int8_t*, \
+    const float*, const int*, int32_t*, int);
+KM16_INST(false, 1, false) KM16_INST(true, 1, false) KM16_INST(false, 4, false) KM16_INST(true, 4, false)
+KM16_INST(false, 4, true) KM16_INST(true, 4, true)
+#undef KM16_INST
 
 /* ------------------------------------------------------------------ q8_0 on the matrix cores
    The q8_0 product (kq8 weights against int8 rows with per-32 scales, lt_mv_q8 lightning.cu:258-284, k_q8
