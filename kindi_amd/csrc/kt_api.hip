@@ -89,16 +89,25 @@ static int kt_kslices(int NU){
    of one matrix, passes of 16 tokens, on every launch from 3 tokens (measured on MI355X with k_gemv_m16 and its
    k-lanes split over 4 waves on small grids, per launch over 16 27B-class layers and per 2B-class layer: 27B layer
    at 3 / 5 / 7 tokens 56.1 / 81.1 / 50.5 -> 46.6 / 47.8 / 49.6 us, 2B layer 18.8 / 26.0 / 27.4 -> 18.7 / 19.1 /
-   19.9 us against the v_dot4 kernels or the earlier size rule; at 2 tokens the v_dot4 kernels stay faster, 27B
-   layer 43.9 against 46.1 us, 2B layer 13.6 against 18.2 us) */
+   19.9 us against the v_dot4 kernels or the earlier size rule). At 2 tokens only launches of 2^26 weights or more
+   (27B gate/up 17.7 -> 16.8 us, down 13.8 -> 12.6 us; the 27B layer 43.5 -> 41.6 us); the smaller ones stay faster
+   on v_dot4 (27B q/k/v 6.39 against 6.52 us, 2B layer 13.6 against 16.9 us) */
 #ifndef KT_MMA_MIN
 #define KT_MMA_MIN 3
 #endif
 #define KT_Q8_MMA_MIN 12               /* q8_0 dense: the matrix-core product from 12 tokens */
 #define KT_MMA_MAX 32
 #define KT_Q8_MMA_KS 8                 /* q8_0 matrix-core product: K slices a block (kt_mma.hip KM_Q8_KS) */
+#ifndef KT_MMA_W2
+#define KT_MMA_W2 (1ll << 26)          /* 2 tokens: the matrix cores from this many weights a launch */
+#endif
 static bool kt_use_mma(const KtGemvArgs& a){
-  return a.M >= KT_MMA_MIN && a.M <= KT_MMA_MAX && (long long)a.M * a.ldq < (1ll << 30);
+  if(a.M > KT_MMA_MAX || (long long)a.M * a.ldq >= (1ll << 30)) return false;
+  if(a.M >= KT_MMA_MIN) return true;
+  if(a.M < 2) return false;
+  long long w = 0;
+  for(int i = 0; i < a.nmat; ++i) w += (long long)a.mat[i].R * a.NU * 128;
+  return w >= KT_MMA_W2;
 }
 
 static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, const int* xa, int32_t* dbg,

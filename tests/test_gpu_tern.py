@@ -123,8 +123,8 @@ def test_gemv_hp_pairs(kt, R, C):
 @pytest.mark.parametrize("R,C", [(640, 1024), (2048, 6144), (4096, 4096)])
 def test_gemv_token_invariance(kt, R, C):
     """a token's output does not depend on how many tokens share the pass (tc_hip.cu:14-15), for M = 1 .. 32: the
-    bandwidth kernels (1 - 2 tokens) and the matrix-core kernels (from 3 tokens; 16x16x64 tiles up to 10 K slices, their
-    k-lanes split over 4 waves up to 4 slices) give the same bits"""
+    bandwidth kernels (1 - 2 tokens) and the matrix-core kernels (from 3 tokens; 16x16x64 tiles up to 10 K slices,
+    their k-lanes split over 4 waves) give the same bits"""
     lib, linear = kt
     say("gemv T-invariance", R, C)
     W, dig, bc, dpm = upload(linear, R, C, 5 + R)
@@ -147,13 +147,14 @@ def test_gemv_token_invariance(kt, R, C):
 @pytest.mark.parametrize("R,C", [(5120, 5120), (1024, 5120), (17408, 5120), (5120, 17408), (256, 24576), (17403, 5120),
                                  (256, 20480), (256, 22528)])
 def test_gemv_27b_tokens(kt, R, C):
-    """the config 3 shapes at M = 1, 3, 4, 5, 6, 8, 13, 16, 32, against the oracle: every launch kind that serves them
-    (the v_dot4 kernels at 1 token; the 16x16x64 matrix-core kernel from 3 tokens up to 10 K slices, its k-lanes
-    split over 4 waves up to 4 slices (C = 5120), whole above (C = 17408, 20480); the 32x32x32 one above 10 slices,
-    C = 22528, 24576). Edges: a ragged row count (17403: a partial
-    last tile and row group), exactly 10 K slices (C = 20480, the 16x16x64 kernel's limit) and 11
-    (C = 22528, the first on the 32x32x32 kernel). int32 group values and fp32 outputs bit-exact against the
-    oracle's decode tree, with and without the dbg output"""
+    """the config 3 shapes at M = 1, 2, 3, 4, 5, 6, 8, 13, 16, 32, against the oracle: every launch kind that serves
+    them. The v_dot4 kernels at 1 token, and at 2 below 2^26 weights; from 3 tokens (2 on the 2^26-weight launches)
+    the 16x16x64 matrix-core kernel up to 10 K slices, its k-lanes split over 4 waves up to 4 slices (C = 5120), a
+    wave taking its k-lane pair of several slices above 4 at up to 8 tokens (C = 17408, 20480), whole-slice waves
+    there above 8 tokens; the 32x32x32 kernel above 10 slices (C = 22528, 24576). Edges: a ragged row count (17403:
+    a partial last tile and row group), exactly 10 K slices (C = 20480, the 16x16x64 kernel's limit) and 11
+    (C = 22528). int32 group values and fp32 outputs bit-exact against the oracle's decode tree, with and without
+    the dbg output"""
     lib, linear = kt
     say("gemv 27B tokens", R, C)
     W, dig, bc, dpm = upload(linear, R, C, 3 * R + C)
@@ -165,7 +166,7 @@ def test_gemv_27b_tokens(kt, R, C):
     dq = dpm.view(np.float16).astype(np.float32)
     tree = orc.out_lanes(acc, XS, dq, 8, 0, lib.kt_decode_kslices(C, 0))
     assert max_rel(tree, orc.tern_out(acc, XS, dpm, R, C)) < TOL
-    for M in (1, 3, 4, 5, 6, 8, 13, 16, 32):
+    for M in (1, 2, 3, 4, 5, 6, 8, 13, 16, 32):
         say("  M", M)
         act = linear.quantize(Xd[:M])
         Y = torch.empty((M, R), dtype=torch.float32, device="cuda")
