@@ -223,16 +223,17 @@ __device__ __forceinline__ kt_v4i km_digits16(uint32_t w){
   return B;
 }
 
-/* up to 10 K slices (640 threads, 3 waves a SIMD, activations 2 units ahead). The B operands are the unsigned digits
-   d = t + 1 (masks and shifts of the kt2 word, no lookup): an MFMA then gives the exact integer sum d q, and the
-   unit value is v = sum d q - XA (XA = sum q, the quantizer's), the same integer as sum t q. The weights, scales,
-   XS and XA are read through buffer resources that span exactly their buffers, with 32-bit offsets.
+/* up to 10 K slices, activations 2 units ahead. The B operands are the unsigned digits d = t + 1 (masks and shifts
+   of the kt2 word, no lookup): an MFMA then gives the exact integer sum d q, and the unit value is v = sum d q - XA
+   (XA = sum q, the quantizer's), the same integer as sum t q. The weights, scales, XS and XA are read through buffer
+   resources that span exactly their buffers, with 32-bit offsets.
+   KQ = 1: wave ks takes the whole slice ks (640 threads, 3 waves a SIMD).
    KQ = 4: each slice's k-lanes are split over 4 waves, wave (sg, q) taking k-lanes 2 q and 2 q + 1 of slices sg,
    sg + G, ... (MS: G = 4 slice groups for launches of more than 4 slices, so a block has at most 16 waves; else
-   G = KS, one slice a wave) and staging only those units' XS and
-   XA; for each of its slices it writes the pair sum p_q = chain(2 q) + chain(2 q + 1) to LDS and
-   wave 0 forms the butterfly's tree (p0 + p1) + (p2 + p3), which is the KQ = 1 tree ((c0 + c1) + (c2 + c3)) +
-   ((c4 + c5) + (c6 + c7)), then the slices in order: the same bits with 4 times the waves. */
+   G = KS, one slice a wave), staging only those units' XS and XA. For each of its slices a wave writes the pair sum
+   p_q = chain(2 q) + chain(2 q + 1) to LDS, and wave 0 forms the butterfly's tree (p0 + p1) + (p2 + p3), which is
+   the KQ = 1 tree ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)), then the slices in order: the same bits with 4
+   times the waves. */
 template <bool DBG, int KQ, bool MS>
 __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvArgs a, const int8_t* __restrict__ xq,
                                                   const float* __restrict__ xs, const int* __restrict__ xav,
