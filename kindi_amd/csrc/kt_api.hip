@@ -60,6 +60,9 @@ size_t kt_moe1_down_lds(int k, int KS);
 #ifndef KT_STEPM_WAVES
 #define KT_STEPM_WAVES 2048           /* multi-token grids of at most this many one-step waves take k_gemv_stepm */
 #endif
+#ifndef KT_M16H_WAVES
+#define KT_M16H_WAVES 16384           /* ... and above 8 tokens, 2 waves a slice on grids of at most this many */
+#endif
 #ifndef KT_M16Q_MSM
 #define KT_M16Q_MSM 8                 /* ... above 4 slices at up to this many tokens */
 #endif
@@ -141,6 +144,12 @@ static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, const 
         if(dbg) hipLaunchKernelGGL((k_gemv_m16<true, 4, false>), grid, bq, lq, s, a, xq, xs, xa, dbg, ks);
         else hipLaunchKernelGGL((k_gemv_m16<false, 4, false>), grid, bq, lq, s, a, xq, xs, xa, dbg, ks);
       }
+    } else if(ks > 4 && a.M > KT_M16Q_MSM && (long long)tiles * grid.y * 16 <= KT_M16H_WAVES){
+      /* above 8 tokens: the k-lanes of a slice over 2 waves, 8 slice groups (16 waves a block; measured on MI355X,
+         27B-class down at 16 tokens 17.41 -> 17.19 us against whole-slice waves) */
+      const size_t lh = (size_t)ks * 2 * 16 * 32 * 4 + (size_t)16 * 512 * 4;
+      if(dbg) hipLaunchKernelGGL((k_gemv_m16<true, 2, true>), grid, dim3(1024), lh, s, a, xq, xs, xa, dbg, ks);
+      else hipLaunchKernelGGL((k_gemv_m16<false, 2, true>), grid, dim3(1024), lh, s, a, xq, xs, xa, dbg, ks);
     } else {
       const size_t lds16 = lds + (size_t)ks * 256 * 4;                      /* + XA */
       if(dbg) hipLaunchKernelGGL((k_gemv_m16<true, 1, false>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);

@@ -233,7 +233,8 @@ __device__ __forceinline__ kt_v4i km_digits16(uint32_t w){
    G = KS, one slice a wave), staging only those units' XS and XA. For each of its slices a wave writes the pair sum
    p_q = chain(2 q) + chain(2 q + 1) to LDS, and wave 0 forms the butterfly's tree (p0 + p1) + (p2 + p3), which is
    the KQ = 1 tree ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)), then the slices in order: the same bits with 4
-   times the waves. */
+   times the waves. KQ = 2 (with MS, G = 8): k-lane quads, a wave's sum (c0 + c1) + (c2 + c3) of its four and wave 0
+   adding the two quads. */
 template <bool DBG, int KQ, bool MS>
 __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvArgs a, const int8_t* __restrict__ xq,
                                                   const float* __restrict__ xs, const int* __restrict__ xav,
@@ -248,7 +249,7 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
   const int lane = threadIdx.x & 63, wvi = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   /* KQ = 1: wave ks = slice ks. KQ = 4: G slice groups, wave (sg, q) takes k-lanes 2 q, 2 q + 1 of slices sg,
      sg + G, sg + 2 G, ... */
-  const int G = MS ? 4 : KS;                                     /* MS: more slices than groups */
+  const int G = MS ? 16 / KQ : KS;                               /* MS: more slices than groups */
   const int sg = wvi / KQ, q = wvi % KQ, cb = q * CW;            /* slice group, quarter, first k-lane */
   const int g = lane >> 4, n = lane & 15;
   const int tile = blockIdx.x, t0 = blockIdx.y * NT;
@@ -289,7 +290,7 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
 #pragma unroll
   for(int i = 0; i < NI; ++i){
     const int idx = lane + 64 * i, un = idx >> 4, tl = idx & 15;
-    const int j = KQ == 1 ? un >> 3 : un >> 1, c = KQ == 1 ? un & 7 : cb + (un & 1);
+    const int j = un / CW, c = cb + un % CW;                     /* the wave's units: CW k-lanes, 2 steps */
     const int u = (s_lo + j) * KT_KL + c;
     const int t = t0 + tl < a.M ? t0 + tl : t0;
     const uint32_t o = (uint32_t)(t * a.ldxs + (u < NU ? u : 0)) * 4;
@@ -385,6 +386,10 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
         else if(c == 3) t23[e] = t01[e] + (pend[e] + chain[e]);
         else if(c == 5) t45[e] = pend[e] + chain[e];
         else part[e] = t23[e] + (t45[e] + (pend[e] + chain[e]));
+      } else if constexpr(KQ == 2){                              /* (c0 + c1) + (c2 + c3) of the wave's four */
+        if(cc == 0 || cc == 2) pend[e] = chain[e];
+        else if(cc == 1) t01[e] = pend[e] + chain[e];
+        else part[e] = t01[e] + (pend[e] + chain[e]);
       } else {
         if(cc == 0) pend[e] = chain[e];
         else part[e] = pend[e] + chain[e];
@@ -406,6 +411,7 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
 #pragma unroll
       for(int e = 0; e < 8; ++e){
         if constexpr(KQ == 1) w[e] = p[0][e];
+        else if constexpr(KQ == 2) w[e] = p[0][e] + p[1][e];
         else w[e] = (p[0][e] + p[1][e]) + (p[2][e] + p[3][e]);
       }
     };
@@ -430,7 +436,7 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
 #define KM16_INST(DBG, KQ, MS) template __global__ void k_gemv_m16<DBG, KQ, MS>(const KtGemvArgs, const int8_t*, \
     const float*, const int*, int32_t*, int);
 KM16_INST(false, 1, false) KM16_INST(true, 1, false) KM16_INST(false, 4, false) KM16_INST(true, 4, false)
-KM16_INST(false, 4, true) KM16_INST(true, 4, true)
+KM16_INST(false, 4, true) KM16_INST(true, 4, true) KM16_INST(false, 2, true) KM16_INST(true, 2, true)
 #undef KM16_INST
 
 /* ------------------------------------------------------------------ q8_0 on the matrix cores

@@ -150,8 +150,8 @@ def test_gemv_27b_tokens(kt, R, C):
     """the config 3 shapes at M = 1, 2, 3, 4, 5, 6, 8, 13, 16, 32, against the oracle: every launch kind that serves
     them. The v_dot4 kernels at 1 token, and at 2 below 2^26 weights; from 3 tokens (2 on the 2^26-weight launches)
     the 16x16x64 matrix-core kernel up to 10 K slices, its k-lanes split over 4 waves up to 4 slices (C = 5120), a
-    wave taking its k-lane pair of several slices above 4 at up to 8 tokens (C = 17408, 20480), whole-slice waves
-    there above 8 tokens; the 32x32x32 kernel above 10 slices (C = 22528, 24576). Edges: a ragged row count (17403:
+    wave taking its k-lane pair of several slices above 4 at up to 8 tokens (C = 17408, 20480) and its k-lane quad
+    above 8 tokens; the 32x32x32 kernel above 10 slices (C = 22528, 24576). Edges: a ragged row count (17403:
     a partial last tile and row group), exactly 10 K slices (C = 20480, the 16x16x64 kernel's limit) and 11
     (C = 22528). int32 group values and fp32 outputs bit-exact against the oracle's decode tree, with and without
     the dbg output"""
