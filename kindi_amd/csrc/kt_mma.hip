@@ -331,7 +331,7 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
       hq[j][cc] = h0 | h1 << 16;
     }
 #pragma unroll
-  for(int i = 0; i < NI; ++i){ xsl[xdst[i]] = xsv[i]; xal[xdst[i]] = xav4[i]; }
+  for(int i = 0; i < NI; ++i){ xsl[xdst[i]] = xsv[i]; xal[xdst[i]] = -xav4[i]; }        /* XA negated */
   kt_wave_sync();
 #pragma unroll
   for(int cc = 0; cc < CW; ++cc){
@@ -352,15 +352,13 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
         km_swap16(w0, w1); km_swap16(w2, w3);
         const kt_v4i A0 = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w};
         const kt_v4i A1 = {(int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
-        kt_v4i d0 = {0, 0, 0, 0}, d1 = {0, 0, 0, 0};
-        d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, km_digits16(w0), d0, 0, 0, 0);   /* row block 0, half 0 */
-        d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, km_digits16(w2), d1, 0, 0, 0);   /* row block 1, half 0 */
-        d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, km_digits16(w1), d0, 0, 0, 0);   /* row block 0, half 1 */
-        d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, km_digits16(w3), d1, 0, 0, 0);   /* row block 1, half 1 */
-        const int4 xa4 = *(const int4*)(xal + (j * 8 + c) * 16 + 4 * g);                    /* tokens 4 g .. + 3 */
-        const int xq4[4] = {xa4.x, xa4.y, xa4.z, xa4.w};
-#pragma unroll
-        for(int e = 0; e < 4; ++e){ d0[e] -= xq4[e]; d1[e] -= xq4[e]; }                      /* v = sum d q - XA */
+        /* both chains start from -XA of tokens 4 g .. + 3 (staged negated), so they end at v = sum d q - XA */
+        const int4 xa4 = *(const int4*)(xal + (j * 8 + c) * 16 + 4 * g);
+        const kt_v4i cx = {xa4.x, xa4.y, xa4.z, xa4.w};
+        kt_v4i d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, km_digits16(w0), cx, 0, 0, 0);   /* row block 0, half 0 */
+        kt_v4i d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, km_digits16(w2), cx, 0, 0, 0);   /* row block 1, half 0 */
+        d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, km_digits16(w1), d0, 0, 0, 0);          /* row block 0, half 1 */
+        d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, km_digits16(w3), d1, 0, 0, 0);          /* row block 1, half 1 */
         const float dd0 = ook[0] ? kt_h2f((uint16_t)hq[j][cc]) : 0.0f;
         const float dd1 = ook[1] ? kt_h2f((uint16_t)(hq[j][cc] >> 16)) : 0.0f;
         const float4 sx = *(const float4*)(xsl + (j * 8 + c) * 16 + 4 * g);                /* tokens 4 g .. + 3 */
