@@ -324,10 +324,11 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
       const bool ok = j < ns && u < NU;
       const uint32_t wo = ok && cok ? (uint32_t)kt_widx(NU, crg, s, ch, c, cr) * 16 : 0u;
       wq[j][cc] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo, 0, 2));
+      /* rows past R read past the resource: a zero scale, so their chains stay zero without a select */
       const uint32_t h0 = __builtin_amdgcn_raw_buffer_load_b16(
-          hr, ok && ook[0] ? (uint32_t)kt_sidx(NU, rg0 + (n >> 3), u, cr) * 2 : 0u, 0, 0);
+          hr, ok && ook[0] ? (uint32_t)kt_sidx(NU, rg0 + (n >> 3), u, cr) * 2 : (1u << 31), 0, 0);
       const uint32_t h1 = __builtin_amdgcn_raw_buffer_load_b16(
-          hr, ok && ook[1] ? (uint32_t)kt_sidx(NU, rg0 + 2 + (n >> 3), u, cr) * 2 : 0u, 0, 0);
+          hr, ok && ook[1] ? (uint32_t)kt_sidx(NU, rg0 + 2 + (n >> 3), u, cr) * 2 : (1u << 31), 0, 0);
       hq[j][cc] = h0 | h1 << 16;
     }
 #pragma unroll
@@ -359,8 +360,7 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
         kt_v4i d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, km_digits16(w2), cx, 0, 0, 0);   /* row block 1, half 0 */
         d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, km_digits16(w1), d0, 0, 0, 0);          /* row block 0, half 1 */
         d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, km_digits16(w3), d1, 0, 0, 0);          /* row block 1, half 1 */
-        const float dd0 = ook[0] ? kt_h2f((uint16_t)hq[j][cc]) : 0.0f;
-        const float dd1 = ook[1] ? kt_h2f((uint16_t)(hq[j][cc] >> 16)) : 0.0f;
+        const float dd0 = kt_h2f((uint16_t)hq[j][cc]), dd1 = kt_h2f((uint16_t)(hq[j][cc] >> 16));
         const float4 sx = *(const float4*)(xsl + (j * 8 + c) * 16 + 4 * g);                /* tokens 4 g .. + 3 */
         const float sxv[4] = {sx.x, sx.y, sx.z, sx.w};
 #pragma unroll
