@@ -191,10 +191,10 @@ static int kt_launch_gemv(const KtGemvArgs& a, int ngroups, const int8_t* xq, co
     return 0;
   }
   if(FMT == KT_FMT_TERN && a.M > 1 && kt_steps(a.NU) <= 8 && (long long)ngroups * kt_steps(a.NU) <= KT_STEPM_WAVES){
-    /* 2-5 tokens (the two-row form included), one step a wave, on grids that leave the CUs short of waves: 8 a CU
-       or fewer once split (measured on MI355X, 2B-class launches at 4 tokens against k_gemv_flat: q/k/v 5.40 ->
-       4.90 us, o 5.21 -> 4.66 us; the larger gate/up grid was slower split, 5.93 -> 6.25 us, and stays on
-       k_gemv_flat) */
+    /* the tokens below the matrix-core kernels (2, and 3 - 5 where a pass's activation span reaches 2^30 bytes; the
+       two-row form included), one step a wave, on grids that leave the CUs short of waves: 8 a CU or fewer once
+       split (measured on MI355X, 2B-class launches at 4 tokens against k_gemv_flat: q/k/v 5.40 -> 4.90 us, o 5.21 ->
+       4.66 us; the larger gate/up grid was slower split, 5.93 -> 6.25 us, and stays on k_gemv_flat) */
     const int S = kt_steps(a.NU), mt = a.M <= 2 ? 2 : 4;
     const size_t lds = (size_t)S * mt * KT_KL * KtFlat<KT_FMT_TERN, 1>::UP + (size_t)S * mt * 64 * 4 * 2;
     const dim3 grid(ngroups), block(64 * S);
