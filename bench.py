@@ -42,8 +42,8 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
     ap.add_argument("--unpooled", action="store_true", help="one allocation per weight matrix instead of one pool")
     ap.add_argument("--plan", action="store_true",
-                    help="headline over the decode plan (kt_plan_run: one persistent launch per step) instead of one "
-                         "launch per product")
+                    help="also time the step as launch records replayed with hipModuleLaunchKernel from the host "
+                         "(linear.Plan: Kindi's HIP plan replay), beside the graph-captured launches")
     ap.add_argument("--only", choices=("c0", "c1", "c2", "c3m16", "c4", "producers"),
                     help="run one secondary config alone and print its figures (for profiler runs)")
     ap.add_argument("--cpu-child", action="store_true", help=argparse.SUPPRESS)
@@ -592,24 +592,20 @@ def main():
     log("config 3, M=1")
     step, nbytes, calls, launches, stages = sweep_step(torch, linear, layers, 1)
     ms_l = timer.run(graphed(torch, step, use_graph), a.steps, a.warmup)
-    plan = linear.Plan(stages) if a.plan else None
-    if plan is not None:
-        # the decode plan: one persistent launch (k_plan<1>, after a one-block counter reset) per step
-        run = graphed(torch, plan.run, use_graph)
-        ms = timer.run(run, a.steps, a.warmup)
-        torch.cuda.synchronize()
-        if plan.status() != 0:
-            raise RuntimeError("decode plan: a stage barrier timed out")
-        nlaunch, kernel = 1, "k_plan<1> (decode plan, %d stages, grid %d x %d waves)" % (
-            len(stages), plan.info.grid, plan.info.waves + 1)
-    else:
-        ms, nlaunch, kernel = ms_l, len(calls), "k_gemv_step<1> (q/k/v, o) + k_gemv_step<2> (gate/up) + k_gemv_flat1 (down)"
+    ms, nlaunch, kernel = ms_l, len(calls), "k_gemv_step<1> (q/k/v, o) + k_gemv_step<2> (gate/up) + k_gemv_flat1 (down)"
+    replay = None
+    if a.plan:
+        # the same launches as records replayed from the host (no graph): Kindi's HIP plan replay
+        plan = linear.Plan(step)
+        ms_r = timer.run(plan.launch, a.steps, a.warmup)
+        replay = {"ms_per_step": round(ms_r, 4), "GB/s": round(nbytes / ms_r / 1e6, 1), "launches": plan.n,
+                  "note": "launch records (kt_record_begin/end) replayed with hipModuleLaunchKernel, no graph"}
+        del plan
     gbs = nbytes / ms / 1e6
-    # the dominant kernel is the whole step (plan) or every launch of it (launches, back to back in the graph): its
-    # average duration is the timed region over the launch count (an upper bound: it includes the gaps)
+    # the dominant kernel is every launch of the step (back to back in the graph): its average duration is the timed region over the launch count (an upper bound: it includes the gaps)
     launch_ms = ms / nlaunch
     achieved = nbytes / nlaunch / launch_ms / 1e6
-    traffic = pmc_traffic() if plan is None else None
+    traffic = pmc_traffic()
     out = {
         "metric": "decode GEMV HBM GB/s (% of 8 TB/s) + prefill int8 TOPS, ternary 27B shapes",
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
@@ -617,7 +613,7 @@ def main():
         "dtype": "int8 x ternary (int32 accumulate, fp32 scale)", "data": "synthetic (seeded; BASELINE config 3)",
         "config": {"workload": "config 3: 27B-class decode sweep, 64 layers x {q,k,v,o,gate,up,down}, M=1",
                    "tokens": 1, "bytes_per_step": nbytes, "launches_per_step": nlaunch,
-                   "products_per_step": len(calls), "executor": "plan" if plan is not None else "launches",
+                   "products_per_step": len(calls), "executor": "launches",
                    "graph": use_graph, "frac_hbm": round(gbs / HBM_PEAK, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK, 4),
@@ -642,7 +638,9 @@ def main():
         del stepP
         log("config 3, M=16")
         cfgs["c3 M=16"] = config3_kinds(torch, linear, layers, 16, timer, max(a.steps // 2, 3), use_graph)
-        del layers, step, calls, stages, plan
+        if replay:
+            cfgs["c3 M=1 record replay"] = replay
+        del layers, step, calls, stages
         torch.cuda.empty_cache()
         log("configs 0, 1, 2, 4")
         cfgs["c0"] = config0(torch, linear, synth, timer, a.steps, use_graph)

@@ -6,12 +6,16 @@
 
    Conventions (all entry points):
    - every pointer argument is a device pointer owned by the caller (as Kindi's CuPy buffers, engine.py:193-204,
-     spec.py:523-593); the library never allocates, frees or synchronizes, and keeps no device state;
+     spec.py:523-593); the library never allocates, frees or synchronizes. Its only device state is the fixed
+     workspace array of kt_moe_decode_noalloc (4 MiB a GPU, held until the process ends); every other entry point
+     works on caller buffers alone;
    - `stream` is a hipStream_t (NULL = the null stream); launches are asynchronous and graph-capturable;
    - the return value is a hipError_t as int: 0 on success, hipErrorInvalidValue (1) for a shape, stride or
      alignment the kernels do not take (Kindi raises SystemExit / RuntimeError there: spec.py:195-196,
      layout.py:38-39, tp.py:944-945), else the launch error;
-   - M = 0 tokens is a no-op returning 0.
+   - M = 0 tokens is a no-op returning 0;
+   - between kt_record_begin and kt_record_end, the calling thread's launchers record their launches instead of
+     launching them (launch records, below).
 
    Numbers (the reference's, tc.cu:1-18, tc_hip.cu:8-15): activations are int8 per 128-column group (XS = amax/127,
    q = round-to-nearest-even(x * 127 / amax), XA = sum q); a group's value v = sum t q over its 128 columns is an
@@ -95,42 +99,35 @@ int kt_tern_gemv3(const void* W0, int R0, float* Y0, const void* W1, int R1, flo
 /* y[n R + r] = sum over parts p < sp of P[(n sp + p) R + r], in part order. k_tc_sum (tc_hip.cu:271-279). */
 int kt_tern_sum(const float* P, float* y, int R, int M, int sp, void* stream);
 
-/* ---------------------------------------------------------------- decode plan (one launch per decode step)
-   A sequence of ternary products run in order by one persistent launch: stage s starts after every earlier stage
-   has finished and its stores are visible (the ordering of separate stream-ordered launches, so a stage may read
-   what an earlier stage wrote), while the weight loads of later stages are already in flight. Each stage is what
-   kt_tern_gemv3 takes (1 .. 3 matrices with one quantized input, Y_i [M][R_i]) and gives the same bits.
-   Replaces the plan replay of a decode step (Plan.add / replay, tp.py:282-302; spec.py:250-325, 619-673).
-   kt_plan_bytes: the device bytes of a plan of n stages (caller-allocated, 256-byte aligned).
-   kt_plan_build: checks the stages, sizes the launch for the current device (every block resident at once) and
-   writes the plan (synchronous on `stream`; not for graph capture). `info` receives what kt_plan_run needs.
-   Stages take C % 128 == 0 and C <= 30720, M 1 .. 4 tokens (the same for every stage).
-   kt_plan_run: one plan execution (a small reset kernel, then the plan kernel; graph-capturable). Nothing else
-   may run on the GPU at the same time (the plan's blocks wait for each other).
-   One-token plans run on the streamed executor (exec = 1: every block streams its share of all stages' weights
-   through LDS ahead of the stage it computes); others on the register-ring executor (exec = 0).
-   kt_plan_status: after the run (synchronizes `stream`): 0, or nonzero if a stage barrier timed out (results
-   invalid). */
-typedef struct kt_stage {
-  const void* W[3];                   /* up to three kt2 matrices; R[i] <= 0 ends the list */
-  int R[3];
-  float* Y[3];                        /* [M][R_i] */
-  int C;
-  const int8_t* XQ;                   /* kt_quant_q8 output [M][ldq], XS / XA [M][C/128] */
-  int ldq;
-  const float* XS;
-  const int32_t* XA;
-  int M;
-} kt_stage;
-typedef struct kt_plan_info {
-  int nstages, grid, waves, mt;
-  int exec;                           /* 0: register-ring executor; 1: streamed executor (one-token plans) */
-  size_t lds;
-} kt_plan_info;
-size_t kt_plan_bytes(int nstages);
-int kt_plan_build(const kt_stage* stages, int nstages, void* plan, kt_plan_info* info, void* stream);
-int kt_plan_run(const void* plan, const kt_plan_info* info, void* stream);
-int kt_plan_status(const void* plan, const kt_plan_info* info, int* status, void* stream);
+/* ---------------------------------------------------------------- launch records
+   The tuple Kindi's plan holds for each launch, (function, grid, block, kernel arguments), which its HIP path replays
+   with hipModuleLaunchKernel (Plan.add tp.py:282-302, Replay.launch spec.py:303-320); it takes the place of the
+   function lookup Kindi does on its run-time compiled module (mod.get_function, spec.py:84-93, 202-210).
+   kt_record_begin(recs, max): until kt_record_end, every launcher called on this thread validates its arguments as
+   always and, instead of launching, appends each of its launches to recs (at most max; the stream argument is not
+   used). The kernel, grid and block are the ones the call would have launched for those arguments: a record
+   describes that call, with its pointers and sizes, and no other.
+   kt_record_end(n): stops recording; *n = the launches the calls made (more than max: hipErrorInvalidValue, the
+   first max are filled). A launcher's own validation error is returned by that launcher as always.
+   A record: fn is a hipFunction_t; launch it as
+     hipModuleLaunchKernel(fn, grid[0], grid[1], grid[2], block[0], block[1], block[2], shmem, stream, args, NULL)
+   args[i] points at argument i, stored in the record's own argbuf (at byte off[i]): a record that is copied elsewhere
+   must have args rebuilt from off. Records launched in order on one stream give the results of the calls.
+   Recording is per thread; calls may not nest. Records of kt_moe_decode_noalloc hold the device address of its
+   array. */
+#define KT_REC_MAXARGS 24
+#define KT_REC_ARGBYTES 512
+typedef struct kt_launch {
+  void* fn;                           /* hipFunction_t */
+  unsigned grid[3], block[3];
+  unsigned shmem;                     /* dynamic LDS bytes */
+  int nargs;
+  void* args[KT_REC_MAXARGS];         /* kernelParams */
+  unsigned off[KT_REC_MAXARGS];       /* byte offset of argument i in argbuf */
+  uint64_t argbuf[KT_REC_ARGBYTES / 8];
+} kt_launch;
+int kt_record_begin(kt_launch* recs, int max);
+int kt_record_end(int* n);
 
 /* ---------------------------------------------------------------- prefill product (any M, matrix cores)
    Y and/or Y16 [M][ldy] (fp32 / fp16 bits); dbg as kt_tern_gemv. XA is accepted for the reference's argument list
@@ -162,8 +159,14 @@ int kt_q8_gemv(const void* W, int R, int C, const int8_t* Q, int ldq, const floa
 
 /* ---------------------------------------------------------------- MoE
    kt_moe_topk: logits [M][E] -> ids / gw [M][k]: softmax, the k largest (ties to the lower index), weights
-   normalized over the chosen k (the reference's Lightning router lt_topk / lt_router_topk,
-   lightning.cu:373-468, is sigmoid + bias: same interface, other scoring). E <= 1024, k <= 16.
+   normalized over the chosen k. E <= 1024, k <= 16. A NaN logit ranks below every number (the
+   picks stay distinct; its weight is NaN).
+   kt_moe_topk_r, kt_moe_route_r, kt_moe_decode_r: the same with the scoring chosen by `score`:
+     KT_SCORE_SOFTMAX (0): as above (bias and scale not read);
+     KT_SCORE_SIGMOID (1): Kindi's Lightning router (lt_topk / lt_router_topk, lightning.cu:373-468): s_e = 1 / (1 +
+     exp(-l_e)), the k largest of s_e + bias[e] (bias [E], device; ties to the lower index), gw_j = s_j / (s_0 + ... +
+     s_{k-1}, in pick order) * scale. Exp is expf (the reference's __expf is the fast approximation: the scores'
+     last bits may differ from it). Other values, or a NULL bias with KT_SCORE_SIGMOID: hipErrorInvalidValue.
    kt_moe_sort: lt_moe_lists (lightning.cu:1318-1349): cnt / off [E], xrow / where [M k], plus act [E] (experts with
    cnt > 0, ascending) and nact [1]; entries of an expert in ascending t k + j. One block; E <= 1024.
    kt_q8_grouped: per active expert e, Y[p] = W_e x[xrow[p]] for its entries p (xrow NULL: x[p]); Wexp = device
@@ -171,7 +174,11 @@ int kt_q8_gemv(const void* W, int R, int C, const int8_t* Q, int ldq, const floa
    (bounds an expert's list); dbg int32 [entries][R][C/32].
    kt_moe_combine: x[t] += sum_j fmaf(gw[t k + j], yd[where[t k + j]], .) (+ ysh[t]) (lt_moe_combine,
    lightning.cu:1352-1361). */
+#define KT_SCORE_SOFTMAX 0
+#define KT_SCORE_SIGMOID 1
 int kt_moe_topk(const float* logits, int M, int E, int k, int* ids, float* gw, void* stream);
+int kt_moe_topk_r(const float* logits, int M, int E, int k, int score, const float* bias, float scale, int* ids,
+                  float* gw, void* stream);
 int kt_moe_sort(const int* ids, int M, int k, int E, int* cnt, int* off, int* xrow, int* where, int* act, int* nact,
                 void* stream);
 /* kt_moe_route: kt_moe_topk and kt_moe_sort in one launch (one wave; M k <= 64 entries; the same outputs) — the
@@ -180,6 +187,9 @@ int kt_moe_sort(const int* ids, int M, int k, int E, int* cnt, int* off, int* xr
 int kt_moe_route(const float* logits, int M, int E, int k, int* ids, float* gw, int* cnt, int* off, int* xrow,
                  int* where, int* act, int* nact, const float* x, int ldx, int H, int8_t* Q, int ldq, float* D, int ldd,
                  void* stream);
+int kt_moe_route_r(const float* logits, int M, int E, int k, int score, const float* bias, float scale, int* ids,
+                   float* gw, int* cnt, int* off, int* xrow, int* where, int* act, int* nact, const float* x, int ldx,
+                   int H, int8_t* Q, int ldq, float* D, int ldd, void* stream);
 int kt_q8_grouped(const void* const* Wexp, int R, int C, int E, const int* cnt, const int* off, const int* act,
                   const int* nact, const int* xrow, int nentries, int M, const int8_t* Q, int ldq, const float* D,
                   int ldd, float* Y, int ldy, int32_t* dbg, void* stream);
@@ -202,6 +212,9 @@ int kt_moe_combine(const float* yd, const float* ysh, const int* where, const fl
 size_t kt_moe_decode_workspace(int M, int k, int E, int H, int F);
 int kt_moe_decode(const void* const* Wup, const void* const* Wdown, int E, int H, int F, int k, const float* logits,
                   int M, float* x, int ldx, const float* ysh, void* work, size_t work_bytes, void* stream);
+int kt_moe_decode_r(const void* const* Wup, const void* const* Wdown, int E, int H, int F, int k, int score,
+                    const float* bias, float scale, const float* logits, int M, float* x, int ldx, const float* ysh,
+                    void* work, size_t work_bytes, void* stream);
 
 /* kt_moe_decode_noalloc: kt_moe_decode with its workspace in a device array of the library instead of a caller buffer,
    for callers that cannot allocate device memory (code under graph capture, serving loops that forbid allocation).
@@ -209,7 +222,7 @@ int kt_moe_decode(const void* const* Wup, const void* const* Wdown, int E, int H
    bytes, 4 MiB) is held on every GPU the library runs on until the process ends, and its address on a device is
    resolved by kt_init(device) or by the first call on the device. Shapes whose kt_moe_decode_workspace exceeds it
    return hipErrorInvalidValue. Calls on one GPU share the array: calls that overlap in time on one GPU (other
-   streams, other threads) race. The same results as kt_moe_decode. */
+   streams, other threads) race. The same results as kt_moe_decode (softmax scoring). */
 size_t kt_moe_decode_noalloc_max(void);
 int kt_moe_decode_noalloc(const void* const* Wup, const void* const* Wdown, int E, int H, int F, int k,
                           const float* logits, int M, float* x, int ldx, const float* ysh, void* stream);

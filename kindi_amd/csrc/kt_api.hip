@@ -8,6 +8,8 @@
 #include <mutex>
 #include "../../include/kt.h"
 #include "kt_fold.h"
+#include "kt_launch.h"
+#include "kt_topk.h"
 
 template <int FMT, int MT, bool DBG, bool GRP>
 __global__ void k_gemv_flat(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, const int*, int32_t*,
@@ -28,10 +30,6 @@ template <bool DBG, int KQ, bool MS>
 __global__ void k_gemv_m16(const KtGemvArgs, const int8_t*, const float*, const int*, int32_t*, int);
 template <bool GRP, bool DBG, bool MS>
 __global__ void k_q8_mma(const KtGemvArgs, const KtGroupedArgs, const int8_t*, const float*, int32_t*, int);
-template <int MT> __global__ void k_plan(const uint8_t*, unsigned*);
-size_t kt_splan_lds(int smax, int numax, int tmax);
-const void* kt_splan_kernel();
-extern "C" __global__ void k_plan_reset(unsigned*, int);
 template <int SRC> __global__ void k_tern_pack(const uint8_t*, const uint16_t*, int, int, uint32_t*, uint16_t*);
 extern "C" __global__ void k_q8_pack(const uint8_t*, int, int, uint32_t*, uint16_t*);
 extern "C" __global__ void k_tern_pack_ptq1(const uint8_t*, int, int, int, int, uint32_t*, uint16_t*);
@@ -44,13 +42,13 @@ __global__ void k_tern_gemm(const uint32_t*, const uint16_t*, int, int, const in
 template <int WT, int WR, int PD, bool DBG>
 __global__ void k_tern_gemm_rs1(const uint32_t*, const uint16_t*, int, int, const int8_t*, int, const float*, int,
                                 float*, uint16_t*, int, int32_t*);
-extern "C" __global__ void k_moe_topk(const float*, int, int, int*, float*);
+__global__ void k_moe_topk(const float*, int, int, const KtRouter, int*, float*);
 extern "C" __global__ void k_moe_sort(const int*, int, int, int*, int*, int*, int*, int*, int*, int);
 extern "C" __global__ void k_moe_combine(const float*, const float*, const int*, const float*, int, int, float*, int);
-extern "C" __global__ void k_moe_route(const float*, int, int, int, int*, float*, int*, int*, int*, int*, int*, int*,
-                                       const float*, int, int, int8_t*, int, float*, int);
-__global__ void k_moe1_up(const float*, int, int, const uint8_t* const*, const uint8_t* const*, int, int, const float*,
-                          float*, int*, float*, const uint8_t**, int);
+__global__ void k_moe_route(const float*, int, int, int, const KtRouter, int*, float*, int*, int*, int*, int*, int*,
+                            int*, const float*, int, int, int8_t*, int, float*, int);
+__global__ void k_moe1_up(const float*, int, int, const KtRouter, const uint8_t* const*, const uint8_t* const*, int,
+                          int, const float*, float*, int*, float*, const uint8_t**, int);
 __global__ void k_moe1_down(const uint8_t* const*, const float*, int, int, int, const float*, float*, float*,
                             const float*, int);
 size_t kt_moe1_up_lds(int KS);
@@ -73,7 +71,6 @@ size_t kt_moe1_down_lds(int k, int KS);
 #define KT_PAIR_WAVES 6144             /* one-token grids of more waves take two row groups a block (k_gemv_pair) */
 #endif
 #define KT_RS_BLOCKS 1024              /* per-row prefill on small blocks while the 128 x 128 grid has fewer blocks */
-#define KT_LAUNCH_CHECK() do { const hipError_t _e = hipGetLastError(); if(_e != hipSuccess) return (int)_e; } while(0)
 
 static inline hipStream_t kt_stream(void* s){ return (hipStream_t)s; }
 static inline bool kt_al(const void* p, size_t a){ return ((uintptr_t)p % a) == 0; }
@@ -138,30 +135,29 @@ static int kt_launch_mma(KtGemvArgs a, const int8_t* xq, const float* xs, const 
       const size_t lq = (size_t)ks * 4 * 16 * 32 * 4 + (size_t)G * 4 * 512 * 4;   /* pair sums, XS + XA a wave */
       const dim3 bq(256 * G);
       if(ms){
-        if(dbg) hipLaunchKernelGGL((k_gemv_m16<true, 4, true>), grid, bq, lq, s, a, xq, xs, xa, dbg, ks);
-        else hipLaunchKernelGGL((k_gemv_m16<false, 4, true>), grid, bq, lq, s, a, xq, xs, xa, dbg, ks);
+        if(dbg) KT_LAUNCH((k_gemv_m16<true, 4, true>), grid, bq, lq, s, a, xq, xs, xa, dbg, ks);
+        else KT_LAUNCH((k_gemv_m16<false, 4, true>), grid, bq, lq, s, a, xq, xs, xa, dbg, ks);
       } else {
-        if(dbg) hipLaunchKernelGGL((k_gemv_m16<true, 4, false>), grid, bq, lq, s, a, xq, xs, xa, dbg, ks);
-        else hipLaunchKernelGGL((k_gemv_m16<false, 4, false>), grid, bq, lq, s, a, xq, xs, xa, dbg, ks);
+        if(dbg) KT_LAUNCH((k_gemv_m16<true, 4, false>), grid, bq, lq, s, a, xq, xs, xa, dbg, ks);
+        else KT_LAUNCH((k_gemv_m16<false, 4, false>), grid, bq, lq, s, a, xq, xs, xa, dbg, ks);
       }
     } else if(ks > 4 && a.M > KT_M16Q_MSM && (long long)tiles * grid.y * 16 <= KT_M16H_WAVES){
       /* above 8 tokens: the k-lanes of a slice over 2 waves, 8 slice groups (16 waves a block; measured on MI355X,
          27B-class down at 16 tokens 17.41 -> 17.19 us against whole-slice waves) */
       const size_t lh = (size_t)ks * 2 * 16 * 32 * 4 + (size_t)16 * 512 * 4;
-      if(dbg) hipLaunchKernelGGL((k_gemv_m16<true, 2, true>), grid, dim3(1024), lh, s, a, xq, xs, xa, dbg, ks);
-      else hipLaunchKernelGGL((k_gemv_m16<false, 2, true>), grid, dim3(1024), lh, s, a, xq, xs, xa, dbg, ks);
+      if(dbg) KT_LAUNCH((k_gemv_m16<true, 2, true>), grid, dim3(1024), lh, s, a, xq, xs, xa, dbg, ks);
+      else KT_LAUNCH((k_gemv_m16<false, 2, true>), grid, dim3(1024), lh, s, a, xq, xs, xa, dbg, ks);
     } else {
       const size_t lds16 = lds + (size_t)ks * 256 * 4;                      /* + XA */
-      if(dbg) hipLaunchKernelGGL((k_gemv_m16<true, 1, false>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);
-      else hipLaunchKernelGGL((k_gemv_m16<false, 1, false>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);
+      if(dbg) KT_LAUNCH((k_gemv_m16<true, 1, false>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);
+      else KT_LAUNCH((k_gemv_m16<false, 1, false>), grid, block, lds16, s, a, xq, xs, xa, dbg, ks);
     }
   } else {
     /* above 10 slices, or buffers past 32-bit offsets: 32x32x32 tiles, the 1024-thread bound (activations loaded in
        place, 124 VGPRs) */
-    if(dbg) hipLaunchKernelGGL((k_gemv_mma<16, true, 64 * KT_KSMAX>), grid, block, lds, s, a, xq, xs, dbg, ks);
-    else hipLaunchKernelGGL((k_gemv_mma<16, false, 64 * KT_KSMAX>), grid, block, lds, s, a, xq, xs, dbg, ks);
+    if(dbg) KT_LAUNCH((k_gemv_mma<16, true, 64 * KT_KSMAX>), grid, block, lds, s, a, xq, xs, dbg, ks);
+    else KT_LAUNCH((k_gemv_mma<16, false, 64 * KT_KSMAX>), grid, block, lds, s, a, xq, xs, dbg, ks);
   }
-  KT_LAUNCH_CHECK();
   return 0;
 }
 
@@ -183,11 +179,10 @@ static int kt_launch_gemv(const KtGemvArgs& a, int ngroups, const int8_t* xq, co
     const size_t lds = (size_t)S * KT_KL * KtFlat<KT_FMT_TERN, 1>::UP + (size_t)(two ? 2 : 1) * S * 64 * 4 * 2;
     const dim3 block(64 * S);
 #define KT_ST(RG) do { const dim3 grid(ngroups / RG); \
-    if(dbg) hipLaunchKernelGGL((k_gemv_step<RG, true>), grid, block, lds, s, a, xq, xs, xa, dbg, ks); \
-    else hipLaunchKernelGGL((k_gemv_step<RG, false>), grid, block, lds, s, a, xq, xs, xa, dbg, ks); } while(0)
+    if(dbg) KT_LAUNCH((k_gemv_step<RG, true>), grid, block, lds, s, a, xq, xs, xa, dbg, ks); \
+    else KT_LAUNCH((k_gemv_step<RG, false>), grid, block, lds, s, a, xq, xs, xa, dbg, ks); } while(0)
     if(two) KT_ST(2); else KT_ST(1);
 #undef KT_ST
-    KT_LAUNCH_CHECK();
     return 0;
   }
   if(FMT == KT_FMT_TERN && a.M > 1 && kt_steps(a.NU) <= 8 && (long long)ngroups * kt_steps(a.NU) <= KT_STEPM_WAVES){
@@ -199,21 +194,19 @@ static int kt_launch_gemv(const KtGemvArgs& a, int ngroups, const int8_t* xq, co
     const size_t lds = (size_t)S * mt * KT_KL * KtFlat<KT_FMT_TERN, 1>::UP + (size_t)S * mt * 64 * 4 * 2;
     const dim3 grid(ngroups), block(64 * S);
 #define KT_STM(MT) do { \
-    if(dbg) hipLaunchKernelGGL((k_gemv_stepm<MT, true>), grid, block, lds, s, a, xq, xs, xa, dbg, ks); \
-    else hipLaunchKernelGGL((k_gemv_stepm<MT, false>), grid, block, lds, s, a, xq, xs, xa, dbg, ks); } while(0)
+    if(dbg) KT_LAUNCH((k_gemv_stepm<MT, true>), grid, block, lds, s, a, xq, xs, xa, dbg, ks); \
+    else KT_LAUNCH((k_gemv_stepm<MT, false>), grid, block, lds, s, a, xq, xs, xa, dbg, ks); } while(0)
     if(mt == 2) KT_STM(2);
     else KT_STM(4);
 #undef KT_STM
-    KT_LAUNCH_CHECK();
     return 0;
   }
   if(FMT == KT_FMT_TERN && a.M == 1 && even && (long long)ngroups * ks > KT_PAIR_WAVES && kt_steps(a.NU) <= KT_SL * ks){
     /* one token on a grid too large for the wave slots: two row groups a block, one round of blocks */
     const dim3 grid(ngroups / 2), block(64 * ks);
     const size_t lds = (size_t)ks * KtFlat<KT_FMT_TERN, 1>::XW + (size_t)ks * 2 * 8 * 4;
-    if(dbg) hipLaunchKernelGGL((k_gemv_pair<true>), grid, block, lds, s, a, xq, xs, xa, dbg, ks);
-    else hipLaunchKernelGGL((k_gemv_pair<false>), grid, block, lds, s, a, xq, xs, xa, dbg, ks);
-    KT_LAUNCH_CHECK();
+    if(dbg) KT_LAUNCH((k_gemv_pair<true>), grid, block, lds, s, a, xq, xs, xa, dbg, ks);
+    else KT_LAUNCH((k_gemv_pair<false>), grid, block, lds, s, a, xq, xs, xa, dbg, ks);
     return 0;
   }
   int mt = a.M <= 1 ? 1 : a.M <= 2 ? 2 : 4;
@@ -222,11 +215,10 @@ static int kt_launch_gemv(const KtGemvArgs& a, int ngroups, const int8_t* xq, co
   const dim3 grid(ngroups), block(64 * ks);
   const KtGroupedArgs ga = {};
 #define KT_F(K, MT) do { const size_t lds = KtFlat<FMT, MT>::lds(ks); \
-    if(dbg) hipLaunchKernelGGL((K<FMT, MT, true, false>), grid, block, lds, s, a, ga, xq, xs, xa, dbg, ks); \
-    else hipLaunchKernelGGL((K<FMT, MT, false, false>), grid, block, lds, s, a, ga, xq, xs, xa, dbg, ks); } while(0)
+    if(dbg) KT_LAUNCH((K<FMT, MT, true, false>), grid, block, lds, s, a, ga, xq, xs, xa, dbg, ks); \
+    else KT_LAUNCH((K<FMT, MT, false, false>), grid, block, lds, s, a, ga, xq, xs, xa, dbg, ks); } while(0)
   if(mt == 4) KT_F(k_gemv_flat, 4); else if(mt == 2) KT_F(k_gemv_flat, 2); else KT_F(k_gemv_flat1, 1);
 #undef KT_F
-  KT_LAUNCH_CHECK();
   return 0;
 }
 
@@ -292,17 +284,16 @@ static int kt_grouped_xf(const KtGroupedArgs& a, int E, int nentries, int M, hip
   const KtGemvArgs da = {};
   const size_t lds1 = KtFlat<FMT, 1>::lds(ks), lds2 = KtFlat<FMT, 2>::lds(ks);
   if(mt == 1)
-    hipLaunchKernelGGL((k_gemv_flat1<FMT, 1, false, true>), grid, block, lds1, s, da, a,
+    KT_LAUNCH((k_gemv_flat1<FMT, 1, false, true>), grid, block, lds1, s, da, a,
                        (const int8_t*)nullptr, (const float*)nullptr, (const int*)nullptr, (int32_t*)nullptr, ks);
   else
-    hipLaunchKernelGGL((k_gemv_flat<FMT, 2, false, true>), grid, block, lds2, s, da, a,
+    KT_LAUNCH((k_gemv_flat<FMT, 2, false, true>), grid, block, lds2, s, da, a,
                        (const int8_t*)nullptr, (const float*)nullptr, (const int*)nullptr, (int32_t*)nullptr, ks);
-  KT_LAUNCH_CHECK();
   return 0;
 }
 
 static int kt_moe_decode_run(const void* const* Wup, const void* const* Wdown, int E, int H, int F, int k,
-                             const float* logits, int M, float* x, int ldx, const float* ysh, uint8_t* work,
+                             const KtRouter& rt, const float* logits, int M, float* x, int ldx, const float* ysh, uint8_t* work,
                              size_t work_bytes, hipStream_t s){
   KtMoeWork w;
   if(!kt_moe_work(M, k, E, H, F, w) || !Wup || !Wdown || !logits || !x || !work || ldx < H || ldx % 4
@@ -318,18 +309,15 @@ static int kt_moe_decode_run(const void* const* Wup, const void* const* Wdown, i
     const uint8_t* const* wu = (const uint8_t* const*)Wup;
     const uint8_t* const* wd = (const uint8_t* const*)Wdown;
     const uint8_t** pd = (const uint8_t**)(work + w.pd);
-    hipLaunchKernelGGL(k_moe1_up, dim3(kt_r8(F), k), dim3(64 * ((ksu + 1) / 2)), kt_moe1_up_lds(ksu), s, logits, E, k,
+    KT_LAUNCH(k_moe1_up, dim3(kt_r8(F), k), dim3(64 * ((ksu + 1) / 2)), kt_moe1_up_lds(ksu), s, logits, E, k, rt,
                        wu, wd, F, H, (const float*)x, u, ids, gw, pd, ksu);
-    KT_LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_moe1_down, dim3(kt_r8(H)), dim3(64 * ksd * ((k + 1) / 2)), kt_moe1_down_lds(k, ksd), s,
+    KT_LAUNCH(k_moe1_down, dim3(kt_r8(H)), dim3(64 * ksd * ((k + 1) / 2)), kt_moe1_down_lds(k, ksd), s,
                        (const uint8_t* const*)pd, (const float*)gw, k, H, F, (const float*)u, yd, x, ysh, ksd);
-    KT_LAUNCH_CHECK();
     return 0;
   }
   /* 1: router, top-k, lists */
-  hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(256), 0, s, logits, M, E, k, ids, gw, cnt, off, xrow, where, act, nact,
+  KT_LAUNCH(k_moe_route, dim3(1), dim3(256), 0, s, logits, M, E, k, rt, ids, gw, cnt, off, xrow, where, act, nact,
                      (const float*)nullptr, 0, 0, (int8_t*)nullptr, 0, (float*)nullptr, 0);
-  KT_LAUNCH_CHECK();
   const int n = M * k;
   /* 2: up = W_e x[xrow[p]] per entry, x quantized in the staging */
   KtGroupedArgs a = {};
@@ -350,9 +338,8 @@ static int kt_moe_decode_run(const void* const* Wup, const void* const* Wdown, i
   rc = kt_grouped_xf<KT_FMT_Q8R>(b, E, n, M, s);
   if(rc) return rc;
   /* 4: x[t] += sum_j gw yd[where] (+ ysh) */
-  hipLaunchKernelGGL(k_moe_combine, dim3((H + 255) / 256, M), dim3(256), 0, s, (const float*)yd, ysh,
+  KT_LAUNCH(k_moe_combine, dim3((H + 255) / 256, M), dim3(256), 0, s, (const float*)yd, ysh,
                      (const int*)where, (const float*)gw, k, H, x, ldx);
-  KT_LAUNCH_CHECK();
   return 0;
 }
 
@@ -385,10 +372,44 @@ static int kt_pack_launch(const uint8_t* bcodes, const uint16_t* dpm, int R, int
   uint32_t* codes = (uint32_t*)W;
   uint16_t* scales = (uint16_t*)((uint8_t*)W + kt_code_bytes(R, NG));
   const long long nw = (long long)kt_code_bytes(R, NG) / 4;
-  hipLaunchKernelGGL((k_tern_pack<SRC>), dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, kt_stream(stream),
+  KT_LAUNCH((k_tern_pack<SRC>), dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, kt_stream(stream),
                      bcodes, dpm, R, C, codes, scales);
-  KT_LAUNCH_CHECK();
   return 0;
+}
+
+/* launch records (kt_record_begin / kt_record_end): the calling thread's recording state */
+static thread_local KtRecState kt_rec_tls;
+static thread_local bool kt_rec_on = false;
+KtRecState* kt_rec_state(){ return kt_rec_on ? &kt_rec_tls : nullptr; }
+
+hipError_t kt_rec_push(const void* fn, dim3 g, dim3 b, size_t lds, int n, const void* const* vals,
+                       const size_t* sizes, const size_t* aligns){
+  KtRecState& r = kt_rec_tls;
+  const int i = r.n++;
+  if(r.err) return (hipError_t)r.err;
+  if(i >= r.max) return hipSuccess;                              /* counted; kt_record_end reports the overflow */
+  kt_launch& L = r.buf[i];
+  memset(&L, 0, sizeof(L));
+  hipFunction_t f = nullptr;
+  hipError_t e = hipGetFuncBySymbol(&f, fn);
+  if(e == hipSuccess && !f) e = hipErrorInvalidDeviceFunction;
+  if(e == hipSuccess && (n > KT_REC_MAXARGS || lds > 0xFFFFFFFFu)) e = hipErrorInvalidValue;
+  size_t o = 0;
+  for(int a = 0; e == hipSuccess && a < n; ++a){
+    o = (o + aligns[a] - 1) / aligns[a] * aligns[a];
+    if(o + sizes[a] > sizeof(L.argbuf)){ e = hipErrorInvalidValue; break; }
+    memcpy((uint8_t*)L.argbuf + o, vals[a], sizes[a]);
+    L.off[a] = (unsigned)o;
+    L.args[a] = (uint8_t*)L.argbuf + o;
+    o += sizes[a];
+  }
+  if(e != hipSuccess){ r.err = (int)e; return e; }
+  L.fn = (void*)f;
+  L.grid[0] = g.x; L.grid[1] = g.y; L.grid[2] = g.z;
+  L.block[0] = b.x; L.block[1] = b.y; L.block[2] = b.z;
+  L.shmem = (unsigned)lds;
+  L.nargs = n;
+  return hipSuccess;
 }
 
 extern "C" {
@@ -403,6 +424,21 @@ int kt_init(int device){
 }
 
 const char* kt_error_string(int rc){ return hipGetErrorString((hipError_t)rc); }
+
+int kt_record_begin(kt_launch* recs, int max){
+  if(kt_rec_on || max < 0 || (max > 0 && !recs)) return KT_INVALID;
+  kt_rec_tls.buf = recs; kt_rec_tls.max = max; kt_rec_tls.n = 0; kt_rec_tls.err = 0;
+  kt_rec_on = true;
+  return 0;
+}
+
+int kt_record_end(int* n){
+  if(!kt_rec_on) return KT_INVALID;
+  kt_rec_on = false;
+  if(n) *n = kt_rec_tls.n;
+  if(kt_rec_tls.err) return kt_rec_tls.err;
+  return kt_rec_tls.n > kt_rec_tls.max ? KT_INVALID : 0;
+}
 
 /* ------------------------------------------------------------------ ternary weights */
 size_t kt_tern_weight_bytes(int R, int C){
@@ -428,9 +464,8 @@ int kt_tern_pack_ptq1(const uint8_t* raw, int R, int C, int row0, int nrows, voi
   uint32_t* codes = (uint32_t*)W;
   uint16_t* scales = (uint16_t*)((uint8_t*)W + kt_code_bytes(R, NG));
   const long long nw = (long long)nrg * NG * 64;
-  hipLaunchKernelGGL(k_tern_pack_ptq1, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, kt_stream(stream),
+  KT_LAUNCH(k_tern_pack_ptq1, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, kt_stream(stream),
                      raw, R, C, row0, nrg, codes, scales);
-  KT_LAUNCH_CHECK();
   return 0;
 }
 
@@ -439,9 +474,8 @@ int kt_quant_q8(const float* X, int ldx, int M, int C, int per_row, int8_t* XQ, 
   if(M == 0) return 0;
   if(!X || !XQ || !XS || !XA || M < 0 || C <= 0 || C % 128 || ldx < C || ldq < C || ldx % 2 || ldq % 16
      || !kt_al(X, 8) || !kt_al(XQ, 16) || per_row < 0 || per_row > 2) return KT_INVALID;
-  hipLaunchKernelGGL(k_quant_tern, dim3(M), dim3(256), 0, kt_stream(stream), X, ldx, C, per_row, XQ, ldq,
+  KT_LAUNCH(k_quant_tern, dim3(M), dim3(256), 0, kt_stream(stream), X, ldx, C, per_row, XQ, ldq,
                      XS, (int*)XA);
-  KT_LAUNCH_CHECK();
   return 0;
 }
 
@@ -472,131 +506,11 @@ int kt_tern_gemv3(const void* W0, int R0, float* Y0, const void* W1, int R1, flo
 int kt_tern_sum(const float* P, float* y, int R, int M, int sp, void* stream){
   if(M == 0) return 0;
   if(!P || !y || R <= 0 || M < 0 || M > 65535 || sp <= 0) return KT_INVALID;
-  hipLaunchKernelGGL(k_tern_sum, dim3((unsigned)((R + 255) / 256), (unsigned)M), dim3(256), 0, kt_stream(stream), P, y,
+  KT_LAUNCH(k_tern_sum, dim3((unsigned)((R + 255) / 256), (unsigned)M), dim3(256), 0, kt_stream(stream), P, y,
                      R, M, sp);
-  KT_LAUNCH_CHECK();
   return 0;
 }
 
-/* ------------------------------------------------------------------ decode plan */
-size_t kt_plan_bytes(int nstages){ return nstages > 0 ? kt_plan_size(nstages) : 0; }
-
-int kt_plan_build(const kt_stage* st, int n, void* plan, kt_plan_info* info, void* stream){
-  if(!st || n <= 0 || !plan || !info || !kt_al(plan, 256)) return KT_INVALID;
-  std::vector<uint8_t> buf(kt_plan_ctr_off(n), 0);
-  KtPlanHdr* H = (KtPlanHdr*)buf.data();
-  KtPStage* S = (KtPStage*)(buf.data() + KT_PLAN_HDR);
-  const int M = st[0].M;
-  int W = 1;
-  for(int s = 0; s < n; ++s){
-    const kt_stage& x = st[s];
-    if(x.M != M || M < 1 || M > 4 || x.C <= 0 || x.C % 128 || !x.XQ || !x.XS || !x.XA || x.ldq < x.C ||
-       x.ldq % 16 || !kt_al(x.XQ, 16)) return KT_INVALID;
-    const int NU = x.C / 128, ks = kt_kslices(NU);
-    if(ks > KT_KSMAX - 1) return KT_INVALID;                     /* C <= 30720: KS + 1 waves a block */
-    KtPStage& d = S[s];
-    int groups = 0, nmat = 0;
-    for(int i = 0; i < 3 && x.R[i] > 0; ++i){
-      if(!x.W[i] || !x.Y[i] || !kt_al(x.W[i], 16)) return KT_INVALID;
-      d.mat[i].codes = (const uint32_t*)x.W[i];
-      d.mat[i].scales = (const uint16_t*)((const uint8_t*)x.W[i] + kt_code_bytes(x.R[i], NU));
-      d.mat[i].y = x.Y[i];
-      d.mat[i].R = x.R[i];
-      d.mat[i].ldy = x.R[i];
-      d.mat[i].rg0 = groups;
-      groups += kt_r8(x.R[i]);
-      ++nmat;
-    }
-    if(!nmat) return KT_INVALID;
-    d.nmat = nmat; d.NU = NU; d.KS = ks; d.ngroups = groups;
-    d.xq = x.XQ; d.xs = x.XS; d.xa = (const int*)x.XA; d.ldq = x.ldq; d.ldxs = NU; d.M = M;
-    /* inputs that overlap an output of an earlier stage are read with coherent loads */
-    const uintptr_t in[3][2] = {{(uintptr_t)x.XQ, (uintptr_t)x.XQ + (size_t)(M - 1) * x.ldq + x.C},
-                                {(uintptr_t)x.XS, (uintptr_t)x.XS + (size_t)M * NU * 4},
-                                {(uintptr_t)x.XA, (uintptr_t)x.XA + (size_t)M * NU * 4}};
-    d.coh = 0;
-    for(int p = 0; p < s; ++p)
-      for(int i = 0; i < 3 && st[p].R[i] > 0; ++i){
-        const uintptr_t y0 = (uintptr_t)st[p].Y[i], y1 = y0 + (size_t)M * st[p].R[i] * 4;
-        for(int q = 0; q < 3; ++q) if(in[q][0] < y1 && y0 < in[q][1]){ d.coh = 1; S[p].pub = 1; }
-      }
-    if(ks > W) W = ks;
-  }
-  int qtot = 0, smax = 0, numax = 0;
-  for(int s = 0; s < n; ++s){
-    S[s].rgpi = W / S[s].KS;
-    S[s].nitems = (S[s].ngroups + S[s].rgpi - 1) / S[s].rgpi;
-    S[s].q0 = qtot;
-    qtot += S[s].ngroups;
-    smax = std::max(smax, kt_steps(S[s].NU));
-    numax = std::max(numax, S[s].NU);
-  }
-  const int mt = M <= 1 ? 1 : M <= 2 ? 2 : 4;
-  const size_t lds = (size_t)W * (mt == 1 ? KtFlat<KT_FMT_TERN, 1>::XW : mt == 2 ? KtFlat<KT_FMT_TERN, 2>::XW
-                                                                               : KtFlat<KT_FMT_TERN, 4>::XW)
-                     + (size_t)2 * W * mt * 8 * 4;
-  const int block = 64 * (W + 1);
-  int dev = 0, cus = 0, nb = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if(e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  if(e == hipSuccess){
-    const void* k = mt == 1 ? (const void*)k_plan<1> : mt == 2 ? (const void*)k_plan<2> : (const void*)k_plan<4>;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, block, lds);
-  }
-  if(e != hipSuccess) return (int)e;
-  if(nb <= 0 || cus <= 0 || cus > KT_BAR_MAXG) return KT_INVALID;
-  nb = std::min(nb, KT_BAR_MAXG / cus);                          /* the barrier's lines */
-  H->nstages = n; H->G = nb * cus; H->W = W; H->MT = mt; H->exec = 0;
-  /* one token: the streamed executor when its LDS fits (one 8-wave block a CU; at least one block a CU, so a
-     block's tasks (row group, K slice) of a stage are at most tmax) */
-  size_t slds = 0;
-  if(M == 1){
-    int tmax = 0, sb = 0;
-    for(int s = 0; s < n; ++s) tmax = std::max(tmax, ((S[s].ngroups + cus - 1) / cus + 1) * S[s].KS);
-    slds = kt_splan_lds(smax, numax, tmax);
-    if(slds <= 160 * 1024 && hipOccupancyMaxActiveBlocksPerMultiprocessor(&sb, kt_splan_kernel(), 576, slds)
-       == hipSuccess && sb > 0){
-      sb = std::min(sb, KT_BAR_MAXG / cus);
-      H->exec = 1; H->G = sb * cus; H->smax = smax; H->numax = numax; H->tmax = tmax; H->qtot = qtot;
-    }
-  }
-  e = hipMemcpyAsync(plan, buf.data(), buf.size(), hipMemcpyHostToDevice, kt_stream(stream));
-  if(e == hipSuccess) e = hipStreamSynchronize(kt_stream(stream));
-  if(e != hipSuccess) return (int)e;
-  info->nstages = n; info->grid = H->G; info->waves = W; info->mt = mt; info->lds = lds; info->exec = H->exec;
-  if(H->exec == 1){ info->waves = 8; info->lds = slds; }             /* 8 compute waves + a control wave */
-  return 0;
-}
-
-int kt_plan_run(const void* plan, const kt_plan_info* info, void* stream){
-  if(!plan || !info || info->nstages <= 0 || info->grid <= 0 || info->waves <= 0) return KT_INVALID;
-  hipStream_t s = kt_stream(stream);
-  unsigned* ctr = (unsigned*)((uint8_t*)plan + kt_plan_ctr_off(info->nstages));
-  hipLaunchKernelGGL(k_plan_reset, dim3(1), dim3(256), 0, s, ctr, (int)KT_BAR_LINES);
-  const uint8_t* p = (const uint8_t*)plan;
-  if(info->exec == 1){
-    hipLaunchKernelGGL((void (*)(const uint8_t*, unsigned*))kt_splan_kernel(), dim3(info->grid), dim3(576), info->lds,
-                       s, p, ctr);
-    KT_LAUNCH_CHECK();
-    return 0;
-  }
-  const dim3 grid(info->grid), block(64 * (info->waves + 1));
-  if(info->mt == 1) hipLaunchKernelGGL(k_plan<1>, grid, block, info->lds, s, p, ctr);
-  else if(info->mt == 2) hipLaunchKernelGGL(k_plan<2>, grid, block, info->lds, s, p, ctr);
-  else hipLaunchKernelGGL(k_plan<4>, grid, block, info->lds, s, p, ctr);
-  KT_LAUNCH_CHECK();
-  return 0;
-}
-
-int kt_plan_status(const void* plan, const kt_plan_info* info, int* status, void* stream){
-  if(!plan || !info || !status || info->nstages <= 0) return KT_INVALID;
-  unsigned v = 0;
-  const uint8_t* p = (const uint8_t*)plan + kt_plan_ctr_off(info->nstages) + (size_t)KT_BAR_STATUS * KT_BAR_LINE * 4;
-  hipError_t e = hipMemcpyAsync(&v, p, 4, hipMemcpyDeviceToHost, kt_stream(stream));
-  if(e == hipSuccess) e = hipStreamSynchronize(kt_stream(stream));
-  *status = (int)v;
-  return (int)e;
-}
 
 /* ------------------------------------------------------------------ prefill product */
 /* per_row = 0: the reference's per-group expression on 128 x 128 blocks. per_row = 1: the per-row order, on small
@@ -620,20 +534,18 @@ int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const f
   if(per_row && (long long)((R + 127) / 128) * ((M + 127) / 128) < KT_RS_BLOCKS){
     /* one 32 x 32 tile a wave, 8 waves: 128 tokens x 64 rows */
     const dim3 grid((R + 63) / 64, (M + 127) / 128);
-    if(dbg) hipLaunchKernelGGL((k_tern_gemm_rs1<4, 2, 3, true>), grid, dim3(512), 0, s, codes, scales, R, NG, XQ, ldq,
+    if(dbg) KT_LAUNCH((k_tern_gemm_rs1<4, 2, 3, true>), grid, dim3(512), 0, s, codes, scales, R, NG, XQ, ldq,
                                XS, M, Y, Y16, ldy, dbg);
-    else hipLaunchKernelGGL((k_tern_gemm_rs1<4, 2, 3, false>), grid, dim3(512), 0, s, codes, scales, R, NG, XQ, ldq,
+    else KT_LAUNCH((k_tern_gemm_rs1<4, 2, 3, false>), grid, dim3(512), 0, s, codes, scales, R, NG, XQ, ldq,
                             XS, M, Y, Y16, ldy, dbg);
-    KT_LAUNCH_CHECK();
     return 0;
   }
   const dim3 grid((R + 127) / 128, (M + 127) / 128);
-#define KT_TG(DBG, RS) hipLaunchKernelGGL((k_tern_gemm<DBG, RS>), grid, dim3(256), 0, s, codes, scales, R, NG, XQ, ldq, \
+#define KT_TG(DBG, RS) KT_LAUNCH((k_tern_gemm<DBG, RS>), grid, dim3(256), 0, s, codes, scales, R, NG, XQ, ldq, \
                                           XS, M, Y, Y16, ldy, dbg)
   if(per_row){ if(dbg) KT_TG(true, true); else KT_TG(false, true); }
   else { if(dbg) KT_TG(true, false); else KT_TG(false, false); }
 #undef KT_TG
-  KT_LAUNCH_CHECK();
   return 0;
 }
 
@@ -649,9 +561,8 @@ int kt_q8_pack(const uint8_t* rows, int R, int C, void* W, void* stream){
   uint32_t* codes = (uint32_t*)W;
   uint16_t* scales = (uint16_t*)((uint8_t*)W + kt_code_bytes(R, NB));
   const long long nw = (long long)kt_code_bytes(R, NB) / 4;
-  hipLaunchKernelGGL(k_q8_pack, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, kt_stream(stream), rows, R, C,
+  KT_LAUNCH(k_q8_pack, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, kt_stream(stream), rows, R, C,
                      codes, scales);
-  KT_LAUNCH_CHECK();
   return 0;
 }
 
@@ -660,9 +571,8 @@ int kt_q8_quant(const float* X, int ldx, int M, int C, int act, int8_t* Q, int l
   if(!X || !Q || !D || M < 0 || C <= 0 || C % 32 || ldx < C || ldq < C || ldd < C / 32 || !kt_al(X, 16) || ldx % 4
      || !kt_al(Q, 4) || ldq % 4) return KT_INVALID;
   const int NB = C / 32;
-  hipLaunchKernelGGL(k_quant_q8, dim3((NB + 31) / 32, M), dim3(256), 0, kt_stream(stream), X, ldx, C, act ? 1 : 0, Q,
+  KT_LAUNCH(k_quant_q8, dim3((NB + 31) / 32, M), dim3(256), 0, kt_stream(stream), X, ldx, C, act ? 1 : 0, Q,
                      ldq, D, ldd);
-  KT_LAUNCH_CHECK();
   return 0;
 }
 
@@ -685,42 +595,61 @@ int kt_q8_gemv(const void* W, int R, int C, const int8_t* Q, int ldq, const floa
     const dim3 grid((kt_r8(R) + 3) / 4), block(64 * ks);
     const size_t lds = (size_t)ks * 16 * 32 * 4 + (size_t)ks * 256 * 4;          /* slice sums, D */
     const KtGroupedArgs ga = {};
-    if(dbg) hipLaunchKernelGGL((k_q8_mma<false, true, false>), grid, block, lds, kt_stream(stream), a, ga, Q, D, dbg, ks);
-    else hipLaunchKernelGGL((k_q8_mma<false, false, false>), grid, block, lds, kt_stream(stream), a, ga, Q, D, dbg, ks);
-    KT_LAUNCH_CHECK();
+    if(dbg) KT_LAUNCH((k_q8_mma<false, true, false>), grid, block, lds, kt_stream(stream), a, ga, Q, D, dbg, ks);
+    else KT_LAUNCH((k_q8_mma<false, false, false>), grid, block, lds, kt_stream(stream), a, ga, Q, D, dbg, ks);
     return 0;
   }
   return kt_launch_gemv<KT_FMT_Q8>(a, kt_r8(R), Q, D, NULL, dbg, kt_stream(stream));
 }
 
 /* ------------------------------------------------------------------ MoE */
-int kt_moe_topk(const float* logits, int M, int E, int k, int* ids, float* gw, void* stream){
+/* the router of kt_moe_*_r: the scoring and its operands (include/kt.h KT_SCORE_*) */
+static bool kt_router(int score, const float* bias, float scale, KtRouter& rt){
+  rt.score = score; rt.bias = bias; rt.scale = scale;
+  if(score == KT_SCORE_SOFTMAX) return true;
+  return score == KT_SCORE_SIGMOID && bias != nullptr;
+}
+
+int kt_moe_topk_r(const float* logits, int M, int E, int k, int score, const float* bias, float scale, int* ids,
+                  float* gw, void* stream){
+  KtRouter rt;
+  if(!kt_router(score, bias, scale, rt)) return KT_INVALID;
   if(M == 0) return 0;
   if(!logits || !ids || !gw || M < 0 || E <= 0 || E > 1024 || k <= 0 || k > 16 || k > E) return KT_INVALID;
-  hipLaunchKernelGGL(k_moe_topk, dim3(M), dim3(64), 0, kt_stream(stream), logits, E, k, ids, gw);
-  KT_LAUNCH_CHECK();
+  KT_LAUNCH(k_moe_topk, dim3(M), dim3(64), 0, kt_stream(stream), logits, E, k, rt, ids, gw);
+  return 0;
+}
+
+int kt_moe_topk(const float* logits, int M, int E, int k, int* ids, float* gw, void* stream){
+  return kt_moe_topk_r(logits, M, E, k, KT_SCORE_SOFTMAX, nullptr, 1.0f, ids, gw, stream);
+}
+
+int kt_moe_route_r(const float* logits, int M, int E, int k, int score, const float* bias, float scale, int* ids,
+                   float* gw, int* cnt, int* off, int* xrow, int* where, int* act, int* nact, const float* x, int ldx,
+                   int H, int8_t* Q, int ldq, float* D, int ldd, void* stream){
+  KtRouter rt;
+  if(!kt_router(score, bias, scale, rt)) return KT_INVALID;
+  if(!logits || !ids || !gw || !cnt || !off || !xrow || !where || !act || !nact || M < 0 || E <= 0 || E > 1024 ||
+     k <= 0 || k > 16 || k > E || M > 64 || (long long)M * k > 64) return KT_INVALID;
+  if(x && (H <= 0 || H % 32 || ldx < H || !Q || ldq < H || !D || ldd < H / 32)) return KT_INVALID;
+  KT_LAUNCH(k_moe_route, dim3(1), dim3(256), 0, kt_stream(stream), logits, M, E, k, rt, ids, gw, cnt, off, xrow,
+            where, act, nact, x, ldx, H, Q, ldq, D, ldd);
   return 0;
 }
 
 int kt_moe_route(const float* logits, int M, int E, int k, int* ids, float* gw, int* cnt, int* off, int* xrow,
                  int* where, int* act, int* nact, const float* x, int ldx, int H, int8_t* Q, int ldq, float* D, int ldd,
                  void* stream){
-  if(!logits || !ids || !gw || !cnt || !off || !xrow || !where || !act || !nact || M < 0 || E <= 0 || E > 1024 ||
-     k <= 0 || k > 16 || k > E || M > 64 || (long long)M * k > 64) return KT_INVALID;
-  if(x && (H <= 0 || H % 32 || ldx < H || !Q || ldq < H || !D || ldd < H / 32)) return KT_INVALID;
-  hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(256), 0, kt_stream(stream), logits, M, E, k, ids, gw, cnt, off, xrow,
-                     where, act, nact, x, ldx, H, Q, ldq, D, ldd);
-  KT_LAUNCH_CHECK();
-  return 0;
+  return kt_moe_route_r(logits, M, E, k, KT_SCORE_SOFTMAX, nullptr, 1.0f, ids, gw, cnt, off, xrow, where, act, nact,
+                        x, ldx, H, Q, ldq, D, ldd, stream);
 }
 
 int kt_moe_sort(const int* ids, int M, int k, int E, int* cnt, int* off, int* xrow, int* where, int* act, int* nact,
                 void* stream){
   if(!ids || !cnt || !off || !xrow || !where || !act || !nact || M < 0 || k <= 0 || k > 16 || E <= 0 || E > 1024
      || (long long)M * k > (1ll << 30)) return KT_INVALID;
-  hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(1024), (size_t)16 * E * 4, kt_stream(stream), ids, M * k, E, cnt, off,
+  KT_LAUNCH(k_moe_sort, dim3(1), dim3(1024), (size_t)16 * E * 4, kt_stream(stream), ids, M * k, E, cnt, off,
                      xrow, where, act, nact, k);
-  KT_LAUNCH_CHECK();
   return 0;
 }
 
@@ -753,11 +682,10 @@ int kt_q8_grouped(const void* const* Wexp, int R, int C, int E, const int* cnt, 
          with them weight bytes in flight (measured on MI355X, config 4 M=256: up 223 -> 162 us, down 161 -> 158 us;
          one wave a block 169 / 157, three 185 / 210) */
       const dim3 blk(128);
-      if(dbg) hipLaunchKernelGGL((k_q8_mma<true, true, true>), grid, blk, lds, s, da, a, Q, D, dbg, ks);
-      else hipLaunchKernelGGL((k_q8_mma<true, false, true>), grid, blk, lds, s, da, a, Q, D, dbg, ks);
-    } else if(dbg) hipLaunchKernelGGL((k_q8_mma<true, true, false>), grid, block, lds, s, da, a, Q, D, dbg, ks);
-    else hipLaunchKernelGGL((k_q8_mma<true, false, false>), grid, block, lds, s, da, a, Q, D, dbg, ks);
-    KT_LAUNCH_CHECK();
+      if(dbg) KT_LAUNCH((k_q8_mma<true, true, true>), grid, blk, lds, s, da, a, Q, D, dbg, ks);
+      else KT_LAUNCH((k_q8_mma<true, false, true>), grid, blk, lds, s, da, a, Q, D, dbg, ks);
+    } else if(dbg) KT_LAUNCH((k_q8_mma<true, true, false>), grid, block, lds, s, da, a, Q, D, dbg, ks);
+    else KT_LAUNCH((k_q8_mma<true, false, false>), grid, block, lds, s, da, a, Q, D, dbg, ks);
     return 0;
   }
   /* the decode product per (row group, active expert), the expert's list in chunks of up to 4 tokens */
@@ -770,11 +698,10 @@ int kt_q8_grouped(const void* const* Wexp, int R, int C, int E, const int* cnt, 
   const dim3 grid(kt_r8(R), ny), block(64 * ks);
   const KtGemvArgs da = {};
 #define KT_GL(K, MT) do { const size_t lds = KtFlat<KT_FMT_Q8, MT>::lds(ks); \
-    if(dbg) hipLaunchKernelGGL((K<KT_FMT_Q8, MT, true, true>), grid, block, lds, s, da, a, Q, D, nullptr, dbg, ks); \
-    else hipLaunchKernelGGL((K<KT_FMT_Q8, MT, false, true>), grid, block, lds, s, da, a, Q, D, nullptr, dbg, ks); } while(0)
+    if(dbg) KT_LAUNCH((K<KT_FMT_Q8, MT, true, true>), grid, block, lds, s, da, a, Q, D, nullptr, dbg, ks); \
+    else KT_LAUNCH((K<KT_FMT_Q8, MT, false, true>), grid, block, lds, s, da, a, Q, D, nullptr, dbg, ks); } while(0)
   if(mt == 4) KT_GL(k_gemv_flat, 4); else if(mt == 2) KT_GL(k_gemv_flat, 2); else KT_GL(k_gemv_flat1, 1);
 #undef KT_GL
-  KT_LAUNCH_CHECK();
   return 0;
 }
 
@@ -782,9 +709,8 @@ int kt_moe_combine(const float* yd, const float* ysh, const int* where, const fl
                    float* x, void* stream){
   if(M == 0) return 0;
   if(!yd || !where || !gw || !x || M < 0 || M > 65535 || k <= 0 || k > 16 || cols <= 0) return KT_INVALID;
-  hipLaunchKernelGGL(k_moe_combine, dim3((cols + 255) / 256, M), dim3(256), 0, kt_stream(stream), yd, ysh, where, gw,
+  KT_LAUNCH(k_moe_combine, dim3((cols + 255) / 256, M), dim3(256), 0, kt_stream(stream), yd, ysh, where, gw,
                      k, cols, x, cols);
-  KT_LAUNCH_CHECK();
   return 0;
 }
 
@@ -793,11 +719,20 @@ size_t kt_moe_decode_workspace(int M, int k, int E, int H, int F){
   return kt_moe_work(M, k, E, H, F, w) ? w.total : 0;
 }
 
+int kt_moe_decode_r(const void* const* Wup, const void* const* Wdown, int E, int H, int F, int k, int score,
+                    const float* bias, float scale, const float* logits, int M, float* x, int ldx, const float* ysh,
+                    void* work, size_t work_bytes, void* stream){
+  KtRouter rt;
+  if(!kt_router(score, bias, scale, rt)) return KT_INVALID;
+  if(M == 0) return 0;
+  return kt_moe_decode_run(Wup, Wdown, E, H, F, k, rt, logits, M, x, ldx, ysh, (uint8_t*)work, work_bytes,
+                           kt_stream(stream));
+}
+
 int kt_moe_decode(const void* const* Wup, const void* const* Wdown, int E, int H, int F, int k, const float* logits,
                   int M, float* x, int ldx, const float* ysh, void* work, size_t work_bytes, void* stream){
-  if(M == 0) return 0;
-  return kt_moe_decode_run(Wup, Wdown, E, H, F, k, logits, M, x, ldx, ysh, (uint8_t*)work, work_bytes,
-                           kt_stream(stream));
+  return kt_moe_decode_r(Wup, Wdown, E, H, F, k, KT_SCORE_SOFTMAX, nullptr, 1.0f, logits, M, x, ldx, ysh, work,
+                         work_bytes, stream);
 }
 
 size_t kt_moe_decode_noalloc_max(void){ return KT_SCRATCH_BYTES; }
@@ -814,7 +749,9 @@ int kt_moe_decode_noalloc(const void* const* Wup, const void* const* Wdown, int 
   uint8_t* p = nullptr;
   const int rc = kt_scratch_resolve(dev, &p);
   if(rc) return rc;
-  return kt_moe_decode_run(Wup, Wdown, E, H, F, k, logits, M, x, ldx, ysh, p, KT_SCRATCH_BYTES, kt_stream(stream));
+  const KtRouter rt = {KT_SCORE_SOFTMAX, 1.0f, nullptr};
+  return kt_moe_decode_run(Wup, Wdown, E, H, F, k, rt, logits, M, x, ldx, ysh, p, KT_SCRATCH_BYTES,
+                           kt_stream(stream));
 }
 
 /* ------------------------------------------------------------------ fused input producers (kt_fold.hip) */

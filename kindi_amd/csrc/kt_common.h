@@ -119,41 +119,6 @@ struct KtGemvArgs {
                                          output row t = the fp32 results of rows 2t and 2t + 1 added (tc.cu:405-407) */
 };
 
-/* a decode plan in device memory: header, stages, then the stage counters and the status word */
-struct KtPStage {
-  KtMat mat[KT_MAXMAT];
-  const int8_t* xq;
-  const float* xs;
-  const int* xa;
-  int nmat, NU, KS, ngroups;          /* matrices, units along C, K slices, row groups of all matrices */
-  int rgpi, nitems;                   /* row groups an item, items */
-  int ldq, ldxs, M, coh;              /* coh: the inputs overlap an earlier stage's outputs */
-  int q0, pub, pad3[2];               /* streamed executor: row groups of the stages before this one; a later stage
-                                         reads this one's outputs */
-};
-struct KtPlanHdr {
-  int nstages, G, W, MT;              /* stages, blocks, data waves a block, tokens a pass */
-  int exec, smax, numax, tmax;        /* executor (0: k_plan, 1: k_splan); streamed: max steps, units, tasks */
-  int qtot, pad[7];                   /* streamed: row groups of all stages */
-};
-#define KT_PLAN_HDR 64
-__host__ __device__ __forceinline__ size_t kt_plan_ctr_off(int nstages){
-  return ((size_t)KT_PLAN_HDR + (size_t)nstages * sizeof(KtPStage) + 255) / 256 * 256;
-}
-/* barrier lines (256 bytes, 64 words; only word 0 is used): the status line, then one arrival line per block, then
-   one line per group of KT_BAR_FAN blocks (its first block publishes there that the group has arrived). One writer a
-   line: many writers to one line (atomics, or stores into one line) queue at the memory side, about 15 ns each. */
-#define KT_BAR_LINE 64
-#define KT_BAR_FAN 16
-#define KT_BAR_MAXG 1024              /* blocks of a plan launch */
-#define KT_BAR_STATUS 0
-#define KT_BAR_ARR 1                  /* line of block b: KT_BAR_ARR + b */
-#define KT_BAR_GRP (KT_BAR_ARR + KT_BAR_MAXG)
-#define KT_BAR_LINES (KT_BAR_GRP + KT_BAR_MAXG / KT_BAR_FAN)
-#define KT_BAR_WORDS (KT_BAR_LINES * KT_BAR_LINE)
-__host__ __device__ __forceinline__ size_t kt_plan_size(int nstages){
-  return kt_plan_ctr_off(nstages) + ((size_t)KT_BAR_WORDS * 4 + 255) / 256 * 256;
-}
 
 /* grouped (MoE) launch over the token-sorted lists */
 struct KtGroupedArgs {

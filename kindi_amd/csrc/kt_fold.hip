@@ -24,6 +24,7 @@
      stages 512 and up between the registers of one HB block. */
 #include "kt_gemv.h"
 #include "kt_fold.h"
+#include "kt_launch.h"
 
 /* one butterfly stage between lanes l and l ^ X: the lower lane keeps a + b, the upper a - b, as (-b) + a: negation
    is exact and the sum is the same rounded value. neg = the sign bit on lanes with bit X set. */
@@ -384,6 +385,5 @@ hipError_t kt_fold_launch(int mode, const KtFoldArgs& a, int M, hipStream_t s){
     case KF_KEY(2, 16, 16): k = k_fold_q8<2, 16, 16>; break;
     default: return hipErrorInvalidValue;
   }
-  hipLaunchKernelGGL(k, dim3(a.C / cw, M), dim3(512), 0, s, a);
-  return hipGetLastError();
+  return kt_go(k, dim3(a.C / cw, M), dim3(512), 0, s, a);
 }

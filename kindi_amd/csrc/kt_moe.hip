@@ -1,9 +1,8 @@
 /* kt_moe.hip - the MoE dispatch around the q8_0 expert products (lightning.cu:348-468 router / top-k,
    1318-1349 lt_moe_lists, 1352-1361 lt_moe_combine; grouped products lt_mm_* lightning.cu:958-1168).
 
-     k_moe_topk     softmax over E logits, the k largest, weights normalized over the chosen k. Selection compares
-                    logits (the softmax is monotone, ties to the lower expert index), and the weights are
-                    exp(l_j - l_max) / sum over the chosen of exp(l_i - l_max) (the full softmax denominator cancels).
+     k_moe_topk     the router's top-k of each token (kt_topk.h): softmax over E logits (BASELINE) or Kindi's sigmoid +
+                    bias scoring; the k largest, ties to the lower expert index, weights normalized over the chosen k.
      k_moe_sort     token-sorted lists: cnt / off per expert, xrow (entry -> token), where ((t, j) -> entry), and the
                     active experts in ascending order. Entries of one expert are in ascending flat index t k + j
                     (stable), so the lists are deterministic.
@@ -28,11 +27,11 @@ __device__ __forceinline__ int kt_wave_excl_scan(int v, int lane, int* total){
   return inc - v;
 }
 
-extern "C" __global__ void __launch_bounds__(64) k_moe_topk(const float* __restrict__ logits, int E, int k,
-                                                            int* __restrict__ ids, float* __restrict__ gw){
+__global__ void __launch_bounds__(64) k_moe_topk(const float* __restrict__ logits, int E, int k, const KtRouter rt,
+                                                int* __restrict__ ids, float* __restrict__ gw){
   /* one wave per token; E <= 1024, k <= 16 */
   const int t = blockIdx.x;
-  kt_topk_wave(logits + (long long)t * E, E, k, ids + t * k, gw + t * k, threadIdx.x);
+  kt_topk_wave(logits + (long long)t * E, E, k, rt, ids + t * k, gw + t * k, threadIdx.x);
 }
 
 /* an exclusive scan of v over the block's 1024 threads (in-wave shuffle scan, then the 16 wave totals) */
@@ -120,8 +119,8 @@ extern "C" __global__ void __launch_bounds__(1024) k_moe_sort(const int* __restr
    readlane); offsets and the active list by prefix sums over lanes; an entry's place is its expert's offset plus the
    entries before it with the same expert (ascending flat index, as kt_moe_sort). The same outputs as
    k_moe_topk + k_moe_sort. */
-extern "C" __global__ void __launch_bounds__(256) k_moe_route(const float* __restrict__ logits, int M, int E, int k,
-    int* __restrict__ ids, float* __restrict__ gw, int* __restrict__ cnt, int* __restrict__ off,
+__global__ void __launch_bounds__(256) k_moe_route(const float* __restrict__ logits, int M, int E, int k,
+    const KtRouter rt, int* __restrict__ ids, float* __restrict__ gw, int* __restrict__ cnt, int* __restrict__ off,
     int* __restrict__ xrow, int* __restrict__ where, int* __restrict__ act, int* __restrict__ nact,
     const float* __restrict__ x, int ldx, int H, int8_t* __restrict__ Q, int ldq, float* __restrict__ D, int ldd){
   __shared__ int o[1024];
@@ -159,7 +158,7 @@ extern "C" __global__ void __launch_bounds__(256) k_moe_route(const float* __res
   int ep = -1;                                                     /* entry lane's expert */
   for(int t = 0; t < M; ++t){
     /* entry lanes t k .. t k + k - 1 take the picks from lanes 0 .. k - 1 */
-    const int mine = kt_topk_wave(logits + (long long)t * E, E, k, ids + t * k, gw + t * k, lane);
+    const int mine = kt_topk_wave(logits + (long long)t * E, E, k, rt, ids + t * k, gw + t * k, lane);
     const int got = __builtin_amdgcn_ds_bpermute(((lane - t * k) & 63) << 2, mine);
     ep = lane >= t * k && lane < t * k + k ? got : ep;
   }

@@ -34,7 +34,8 @@ extern "C" int kt_trace_read(void* host){
 /* T tasks of one wave: task t is slice sl[t] of the row group rg of the kq8 matrix at base[t] against the fp32 input
    row xin[t] (quantized here, relu^2 first when RELU); y[t] = the slice sum of row 8 rg + (lane & 7), in every lane of
    the row (the butterfly's result). Every weight, scale and input load of all tasks is issued before the first use.
-   on[t] = false: no task (its loads read valid addresses of task 0, its result is not used). xw: T * KT_SL * 8 units
+   on[t] = false: no task (its weight loads read task 0's addresses, its input load the row's first step; its result
+   is not used). xw: T * KT_SL * 8 units
    of the wave's LDS. */
 template <int T, bool RELU>
 __device__ __forceinline__ void km1_tasks(const uint8_t* const (&base)[T], const int (&sl)[T],
@@ -61,9 +62,12 @@ __device__ __forceinline__ void km1_tasks(const uint8_t* const (&base)[T], const
       w[t][f].c0 = kt_ldnt(wb + o0);
       w[t][f].c1 = kt_ldnt(wb + o1);
       w[t][f].hs = sb[os];
-      const int nc = NU - s * KT_KL < KT_KL ? NU - s * KT_KL : KT_KL;
+      /* an off task (its slice may be KS, one past the row) reads step 0 of the input row: every load stays inside
+         the row */
+      const int sa = on[t] ? s : 0;
+      const int nc = NU - sa * KT_KL < KT_KL ? NU - sa * KT_KL : KT_KL;
       const int of = lane * 4, ofc = of < nc * 32 ? of : 0;       /* unit c = lane / 8, floats 4 r .. 4 r + 3 */
-      xv[t][f] = *(const uint4*)(xin[t] + (long long)s * KT_KL * 32 + ofc);
+      xv[t][f] = *(const uint4*)(xin[t] + (long long)sa * KT_KL * 32 + ofc);
     }
   }
   float da[T][SL];
@@ -96,7 +100,7 @@ __device__ __forceinline__ void km1_tasks(const uint8_t* const (&base)[T], const
 }
 
 __global__ void __launch_bounds__(64 * KT_KSMAX / 2) __attribute__((amdgpu_waves_per_eu(4)))
-k_moe1_up(const float* __restrict__ logits, int E, int k, const uint8_t* const* __restrict__ wup,
+k_moe1_up(const float* __restrict__ logits, int E, int k, const KtRouter rt, const uint8_t* const* __restrict__ wup,
           const uint8_t* const* __restrict__ wdown, int R, int C, const float* __restrict__ x, float* __restrict__ u,
           int* __restrict__ ids, float* __restrict__ gw, const uint8_t** __restrict__ pdown, int KS){
   __shared__ float s_gw[KM1_KMAX];
@@ -115,7 +119,7 @@ k_moe1_up(const float* __restrict__ logits, int E, int k, const uint8_t* const* 
       t0 = wup[lane < E ? lane : 0];
       t1 = wup[lane + 64 < E ? lane + 64 : 0];
     }
-    const int e = kt_topk_wave(logits, E, k, s_ids, s_gw, lane);
+    const int e = kt_topk_wave(logits, E, k, rt, s_ids, s_gw, lane);
     const int ej = __builtin_amdgcn_readlane(e, j);
     KT_TS((j * gridDim.x + rg) * 4 + 1);
     if(E <= 128){

@@ -15,15 +15,15 @@ P = ctypes.c_void_p
 I = ctypes.c_int
 S = ctypes.c_size_t
 
-class KtStage(ctypes.Structure):
-    """kt_stage (include/kt.h): one product of a decode plan"""
-    _fields_ = [("W", P * 3), ("R", I * 3), ("Y", P * 3), ("C", I), ("XQ", P), ("ldq", I), ("XS", P), ("XA", P),
-                ("M", I)]
+REC_MAXARGS = 24
+REC_ARGBYTES = 512
 
 
-class KtPlanInfo(ctypes.Structure):
-    """kt_plan_info (include/kt.h): the launch shape kt_plan_build chose"""
-    _fields_ = [("nstages", I), ("grid", I), ("waves", I), ("mt", I), ("exec", I), ("lds", S)]
+class KtLaunch(ctypes.Structure):
+    """kt_launch (include/kt.h): one launch record, the (function, grid, block, arguments) Kindi's plan holds"""
+    _fields_ = [("fn", P), ("grid", ctypes.c_uint * 3), ("block", ctypes.c_uint * 3), ("shmem", ctypes.c_uint),
+                ("nargs", I), ("args", P * REC_MAXARGS), ("off", ctypes.c_uint * REC_MAXARGS),
+                ("argbuf", ctypes.c_uint64 * (REC_ARGBYTES // 8))]
 
 
 # (name, restype, argtypes): the declarations of include/kt.h
@@ -40,25 +40,26 @@ SIGNATURES = [
     ("kt_tern_gemv", I, [P, I, I, P, I, P, P, I, P, I, P, P]),
     ("kt_tern_gemv3", I, [P, I, P, P, I, P, P, I, P, I, P, I, P, P, I, P]),
     ("kt_tern_sum", I, [P, P, I, I, I, P]),
-    ("kt_plan_bytes", S, [I]),
-    ("kt_plan_build", I, [ctypes.POINTER(KtStage), I, P, ctypes.POINTER(KtPlanInfo), P]),
-    ("kt_plan_run", I, [P, ctypes.POINTER(KtPlanInfo), P]),
-    ("kt_plan_status", I, [P, ctypes.POINTER(KtPlanInfo), ctypes.POINTER(I), P]),
+    ("kt_record_begin", I, [ctypes.POINTER(KtLaunch), I]),
+    ("kt_record_end", I, [ctypes.POINTER(I)]),
     ("kt_tern_gemm", I, [P, I, I, P, I, P, P, I, I, P, P, I, P, P]),
     ("kt_q8_weight_bytes", S, [I, I]),
     ("kt_q8_pack", I, [P, I, I, P, P]),
     ("kt_q8_quant", I, [P, I, I, I, I, P, I, P, I, P]),
     ("kt_q8_gemv", I, [P, I, I, P, I, P, I, I, P, I, P, P]),
     ("kt_moe_topk", I, [P, I, I, I, P, P, P]),
+    ("kt_moe_topk_r", I, [P, I, I, I, I, P, ctypes.c_float, P, P, P]),
     ("kt_moe_sort", I, [P, I, I, I, P, P, P, P, P, P, P]),
     ("kt_q8_grouped", I, [P, I, I, I, P, P, P, P, P, I, I, P, I, P, I, P, I, P, P]),
     ("kt_moe_combine", I, [P, P, P, P, I, I, I, P, P]),
     ("kt_moe_route", I, [P, I, I, I, P, P, P, P, P, P, P, P, P, I, I, P, I, P, I, P]),
+    ("kt_moe_route_r", I, [P, I, I, I, I, P, ctypes.c_float, P, P, P, P, P, P, P, P, P, I, I, P, I, P, I, P]),
     ("kt_rmsfold_q8", I, [P, I, P, I, I, P, P, I, I, I, P, I, P, I, P, I, P, I, P, P, P]),
     ("kt_fold_q8", I, [P, I, P, I, I, I, P, I, P, I, P, P, P]),
     ("kt_smfold_q8", I, [P, I, P, I, P, I, I, I, I, I, I, P, I, P, I, P, P, P]),
     ("kt_moe_decode_workspace", S, [I, I, I, I, I]),
     ("kt_moe_decode", I, [P, P, I, I, I, I, P, I, P, I, P, P, S, P]),
+    ("kt_moe_decode_r", I, [P, P, I, I, I, I, I, P, ctypes.c_float, P, I, P, I, P, P, S, P]),
     ("kt_moe_decode_noalloc_max", S, []),
     ("kt_moe_decode_noalloc", I, [P, P, I, I, I, I, P, I, P, I, P, P]),
 ]
@@ -87,6 +88,20 @@ def load():
 def driver():
     """the loaded kernel library (the role of Kindi's gpudrv.driver())"""
     return load()
+
+
+_hip = [None]
+
+
+def hip():
+    """the HIP runtime already in the process (the one the library and torch use), with hipModuleLaunchKernel's
+    argument types: Kindi's HIP driver stand-in (gpudrv.py:24-101) binds the same call"""
+    if _hip[0] is None:
+        h = ctypes.CDLL("libamdhip64.so.7")
+        h.hipModuleLaunchKernel.restype = I
+        h.hipModuleLaunchKernel.argtypes = [P] + [ctypes.c_uint] * 7 + [P, P, P]
+        _hip[0] = h
+    return _hip[0]
 
 
 def check(rc, what=""):

@@ -307,51 +307,35 @@ class Linear(object):
 
 
 class Plan(object):
-    """A decode step as one persistent launch (kt_plan_*): the products run in the given order, each after every
-    earlier one has finished (the ordering of separate launches), with the weight loads of later products already
-    in flight. stages: [(mats, act, outs)]: up to three TernaryMatrix with one quantized input (Act) and their fp32
-    outputs [M, R_i], as Linear.gemv_q takes them. The buffers are referenced, not copied: they must live as long
-    as the plan. Replaces Plan.add / replay of a decode step (tp.py:282-302, spec.py:250-325)."""
+    """A decode step as launch records: the launches fn() makes through the kt_* launchers, recorded once
+    (kt_record_begin / kt_record_end) and replayed in order with hipModuleLaunchKernel, as Kindi's HIP path replays
+    its plan (Plan.add tp.py:282-302, Replay.launch spec.py:303-320). The records hold fn's pointers and sizes: the
+    buffers it used must live as long as the plan. A failed recording raises KernelError."""
 
-    def __init__(self, stages, device="cuda"):
+    def __init__(self, fn, max_launches=4096):
         lib = gpudrv.load()
-        n = len(stages)
-        arr = (gpudrv.KtStage * n)()
-        self.refs = []
-        for k, (mats, act, outs) in enumerate(stages):
-            if not 1 <= len(mats) <= 3 or len(outs) != len(mats):
-                raise ValueError("stage %d: 1 to 3 matrices with one output each" % k)
-            if act.hp:
-                raise ValueError("stage %d: the decode plan takes one int8 row a token (no hp)" % k)
-            st = arr[k]
-            for i, (m, o) in enumerate(zip(mats, outs)):
-                if m.C != act.C or o.dtype != torch.float32 or not o.is_contiguous() or o.numel() < act.M * m.R:
-                    raise ValueError("stage %d: matrix %d does not match its input or output" % (k, i))
-                st.W[i] = m.W.data_ptr()
-                st.R[i] = m.R
-                st.Y[i] = o.data_ptr()
-            st.C = act.C
-            st.XQ = act.XQ.data_ptr()
-            st.ldq = act.XQ.stride(0)
-            st.XS = act.XS.data_ptr()
-            st.XA = act.XA.data_ptr()
-            st.M = act.M
-            self.refs.append((mats, act, outs))
-        self.buf = torch.empty(lib.kt_plan_bytes(n) + 256, dtype=torch.uint8, device=device)
-        off = (-self.buf.data_ptr()) % 256
-        self.ptr = VP(self.buf.data_ptr() + off)
-        self.info = gpudrv.KtPlanInfo()
-        gpudrv.check(lib.kt_plan_build(arr, n, self.ptr, ctypes.byref(self.info), stream()), "kt_plan_build")
+        recs = (gpudrv.KtLaunch * max_launches)()
+        gpudrv.check(lib.kt_record_begin(recs, max_launches), "kt_record_begin")
+        try:
+            fn()
+        finally:
+            n = ctypes.c_int(0)
+            rc = lib.kt_record_end(ctypes.byref(n))
+        gpudrv.check(rc, "kt_record_end (%d launches, room for %d)" % (n.value, max_launches))
+        self.recs = recs
+        self.n = n.value
+        # Kindi's node tuples: (fn, grid, block, kernelParams); shmem added, which Replay passes as 0
+        self.nodes = [(r.fn, tuple(r.grid), tuple(r.block), r.shmem, r.args) for r in recs[:self.n]]
 
-    def run(self):
-        gpudrv.check(gpudrv.load().kt_plan_run(self.ptr, ctypes.byref(self.info), stream()), "kt_plan_run")
+    def launch(self):
+        L = gpudrv.hip().hipModuleLaunchKernel
+        s = stream()
+        for fn, g, b, sh, args in self.nodes:
+            rc = L(fn, g[0], g[1], g[2], b[0], b[1], b[2], sh, s, ctypes.cast(args, VP), None)
+            if rc:
+                raise gpudrv.KernelError("a plan launch failed (%d)" % rc)
 
-    def status(self):
-        """0, or 1 if a stage barrier timed out in a run since the last build (results invalid)"""
-        v = ctypes.c_int(0)
-        gpudrv.check(gpudrv.load().kt_plan_status(self.ptr, ctypes.byref(self.info), ctypes.byref(v), stream()),
-                     "kt_plan_status")
-        return v.value
+    run = launch
 
 
 def tern_sum(P, R, M, sp, y=None):

@@ -1,13 +1,16 @@
 """q8_0 expert products and the MoE dispatch on MI355X (the host side over libkt_gfx950.so).
 
 Kindi's MoE layer (lightning.py:687-785) and what each step maps to here:
-  lt_router_topk / lt_router + lt_topk   lightning.cu:348-468     MoE.route        (kt_moe_topk: softmax top-k)
+  lt_router_topk / lt_router + lt_topk   lightning.cu:348-468     MoE.route        (kt_moe_topk_r: softmax top-k, or
+                                                                                    Kindi's sigmoid + bias scoring)
   lt_quant / lt_quant2 (int8 runs)       lightning.cu:70-88, 470   q8_quantize      (kt_q8_quant, act = relu^2)
   lt_moe_lists                           lightning.cu:1318-1349    MoE.lists        (kt_moe_sort)
   lt_mv_q2 slots / lt_mm_* groups        lightning.cu:154-195, 958 Q8Experts.grouped (kt_q8_grouped)
   lt_moe_combine                         lightning.cu:1352-1361    MoE.combine      (kt_moe_combine)
   lt_mv_q8 / dsv41 k_q8 (dense q8_0)     lightning.cu:258-284      Q8Matrix.gemv    (kt_q8_gemv)
 """
+import ctypes
+
 import numpy as np
 import torch
 
@@ -85,19 +88,32 @@ class Q8Experts(object):
         return Y
 
 
+SCORES = {"softmax": 0, "sigmoid": 1}          # KT_SCORE_SOFTMAX, KT_SCORE_SIGMOID (include/kt.h)
+
+
 class MoE(object):
     """A q8_0 MoE feed-forward: x += sum_j gw_j * down_e(relu^2(up_e(x))) over the k routed experts e_j of each
-    token (the Lightning expert shape: up [F, H], down [H, F]), token-sorted grouped dispatch."""
+    token (the Lightning expert shape: up [F, H], down [H, F]), token-sorted grouped dispatch.
+    score: "softmax" or "sigmoid" (Kindi's Lightning router, lightning.cu:373-468: the k largest
+    sigmoid(l) + bias, weights sigmoid(l_j) / sum * scale; bias fp32 [E] on the device)."""
 
-    def __init__(self, up, down, k, device="cuda"):
+    def __init__(self, up, down, k, device="cuda", score="softmax", bias=None, scale=1.0):
         assert up.E == down.E and up.R == down.C and down.R == up.C
         self.up, self.down, self.k, self.E, self.device = up, down, k, up.E, device
+        self.score = SCORES[score]
+        if self.score == 1 and (bias is None or bias.numel() != self.E or bias.dtype != torch.float32):
+            raise ValueError("the sigmoid router takes an fp32 bias of E = %d entries" % self.E)
+        self.bias, self.scale = bias, float(scale)
+
+    def _rt(self):
+        return self.score, ptr(self.bias), ctypes.c_float(self.scale)
 
     def route(self, logits):
         M, E = logits.shape
         ids = torch.empty((M, self.k), dtype=torch.int32, device=logits.device)
         gw = torch.empty((M, self.k), dtype=torch.float32, device=logits.device)
-        gpudrv.check(gpudrv.load().kt_moe_topk(ptr(logits), M, E, self.k, ptr(ids), ptr(gw), stream()), "kt_moe_topk")
+        gpudrv.check(gpudrv.load().kt_moe_topk_r(ptr(logits), M, E, self.k, *self._rt(), ptr(ids), ptr(gw), stream()),
+                     "kt_moe_topk_r")
         return ids, gw
 
     def route_lists(self, logits, x=None, Q=None, D=None):
@@ -114,11 +130,12 @@ class MoE(object):
         act = torch.empty(self.E, dtype=torch.int32, device=dev)
         nact = torch.empty(1, dtype=torch.int32, device=dev)
         H = x.shape[1] if x is not None else 0
-        rc = gpudrv.load().kt_moe_route(ptr(logits), M, E, self.k, ptr(ids), ptr(gw), ptr(cnt), ptr(off), ptr(xrow),
-                                        ptr(where), ptr(act), ptr(nact), ptr(x), x.stride(0) if x is not None else 0,
-                                        H, ptr(Q), Q.stride(0) if Q is not None else 0, ptr(D),
-                                        D.stride(0) if D is not None else 0, stream())
-        gpudrv.check(rc, "kt_moe_route")
+        rc = gpudrv.load().kt_moe_route_r(ptr(logits), M, E, self.k, *self._rt(), ptr(ids), ptr(gw), ptr(cnt),
+                                          ptr(off), ptr(xrow), ptr(where), ptr(act), ptr(nact), ptr(x),
+                                          x.stride(0) if x is not None else 0, H, ptr(Q),
+                                          Q.stride(0) if Q is not None else 0, ptr(D),
+                                          D.stride(0) if D is not None else 0, stream())
+        gpudrv.check(rc, "kt_moe_route_r")
         return ids, gw, (cnt, off, xrow, where, act, nact)
 
     def lists(self, ids):
@@ -166,9 +183,9 @@ class MoE(object):
         lib = gpudrv.load()
         if work is None:
             work = self.workspace(M)
-        rc = lib.kt_moe_decode(ptr(self.up.table), ptr(self.down.table), self.E, H, self.up.R, self.k, ptr(logits), M,
-                               ptr(x), x.stride(0), ptr(ysh), ptr(work), work.numel(), stream())
-        gpudrv.check(rc, "kt_moe_decode")
+        rc = lib.kt_moe_decode_r(ptr(self.up.table), ptr(self.down.table), self.E, H, self.up.R, self.k, *self._rt(),
+                                 ptr(logits), M, ptr(x), x.stride(0), ptr(ysh), ptr(work), work.numel(), stream())
+        gpudrv.check(rc, "kt_moe_decode_r")
         return x
 
     def workspace(self, M):

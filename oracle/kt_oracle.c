@@ -435,22 +435,55 @@ void or_moe_combine(const float* yd, const float* ysh, const int* where, const f
    softmax: the softmax is monotone in the logit, so the k largest logits are chosen (ties: lower expert index), and
    p_j / sum over the chosen p_i = exp(l_j - l_max) / sum over the chosen exp(l_i - l_max) (the denominator of the
    full softmax cancels). fp32 with expf, the sum in selection order. */
+/* a ranks above b: numbers by value, NaN below every number (never chosen before a number); equal values do not rank
+   above each other, so the scan keeps the lower index */
+static int or_above(float a, float b){
+  if(a != a) return 0;
+  if(b != b) return 1;
+  return a > b;
+}
+/* the k best of v[0 .. E-1] by or_above, ties to the lower index, into ids */
+static void or_pick(const float* v, int E, int k, int* ids){
+  for(int j = 0; j < k; ++j){
+    int best = -1;
+    for(int e = 0; e < E; ++e){
+      int used = 0;
+      for(int i = 0; i < j; ++i) if(ids[i] == e) used = 1;
+      if(!used && (best < 0 || or_above(v[e], v[best]))) best = e;
+    }
+    ids[j] = best;
+  }
+}
 void or_router_topk(const float* logits, int M, int E, int k, int* ids, float* gw){
   for(int t = 0; t < M; ++t){
     const float* l = logits + (size_t)t * E;
-    for(int j = 0; j < k; ++j){
-      int best = -1;
-      for(int e = 0; e < E; ++e){
-        int used = 0;
-        for(int i = 0; i < j; ++i) if(ids[t * k + i] == e) used = 1;
-        if(!used && (best < 0 || l[e] > l[best])) best = e;
-      }
-      ids[t * k + j] = best;
-    }
+    or_pick(l, E, k, ids + (size_t)t * k);
     float p[64], s = 0.0f;
     for(int j = 0; j < k; ++j){ p[j] = expf(l[ids[t * k + j]] - l[ids[t * k]]); s += p[j]; }
     for(int j = 0; j < k; ++j) gw[t * k + j] = p[j] / s;
   }
+}
+
+/* Kindi's Lightning router (lt_topk, lightning.cu:373-412; lt_router_topk 414-468): score s_e = 1 / (1 + exp(-l_e)),
+   choice s_e + bias[e], the k largest choices (ties to the lower index), weights s_j / tot * scale with tot the sum of
+   the chosen scores in pick order. fp32 with expf (the reference's __expf is its fast approximation). */
+void or_router_sig(const float* logits, const float* bias, float scale, int M, int E, int k, int* ids, float* gw){
+  float* sc = (float*)malloc(sizeof(float) * (size_t)E);
+  float* ch = (float*)malloc(sizeof(float) * (size_t)E);
+  for(int t = 0; t < M; ++t){
+    const float* l = logits + (size_t)t * E;
+    for(int e = 0; e < E; ++e){
+      sc[e] = 1.0f / (1.0f + expf(-l[e]));
+      ch[e] = sc[e] + bias[e];
+    }
+    int* id = ids + (size_t)t * k;
+    or_pick(ch, E, k, id);
+    float tot = 0.0f;
+    for(int j = 0; j < k; ++j) tot += sc[id[j]];
+    for(int j = 0; j < k; ++j) gw[(size_t)t * k + j] = sc[id[j]] / tot * scale;
+  }
+  free(sc);
+  free(ch);
 }
 
 /* ------------------------------------------------------------------ fused producers of a product's input

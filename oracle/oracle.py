@@ -63,6 +63,7 @@ def lib():
         h.or_moe_sort.argtypes = [P, I, I, I, P, P, P, P]
         h.or_moe_combine.argtypes = [P, P, P, P, I, I, I, P]
         h.or_router_topk.argtypes = [P, I, I, I, P, P]
+        h.or_router_sig.argtypes = [P, P, ctypes.c_float, I, I, I, P, P]
         h.or_sumsq.argtypes = [P, I]
         h.or_sumsq.restype = ctypes.c_double
         h.or_fwht_blocks.argtypes = [P, I, I]
@@ -369,6 +370,17 @@ def router_topk(logits, k):
     ids = np.empty((M, k), np.int32)
     gw = np.empty((M, k), np.float32)
     lib().or_router_topk(_p(logits), M, E, k, _p(ids), _p(gw))
+    return ids, gw
+
+
+def router_sig(logits, bias, scale, k):
+    """Kindi's sigmoid + bias router (lt_topk, lightning.cu:373-412)"""
+    logits = _c(logits, np.float32)
+    bias = _c(bias, np.float32)
+    M, E = logits.shape
+    ids = np.empty((M, k), np.int32)
+    gw = np.empty((M, k), np.float32)
+    lib().or_router_sig(_p(logits), _p(bias), scale, M, E, k, _p(ids), _p(gw))
     return ids, gw
 
 

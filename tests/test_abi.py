@@ -27,7 +27,7 @@ def lib():
 
 def test_exports_every_declared_symbol(lib):
     names = declared()
-    assert len(names) == 33
+    assert len(names) == 34
     for n in names:
         assert hasattr(lib, n), n
     from kindi_amd import gpudrv
@@ -94,31 +94,26 @@ def test_validation_rejects_bad_shapes(lib):
     # dbg with several matrices in one launch
 
 
-def test_plan_validation(lib):
-    """kt_plan_build rejects stages the plan kernel does not take before any GPU call"""
+def test_record_protocol(lib):
+    """kt_record_begin / kt_record_end (launch records): no nesting, no end without a begin, a launcher's own
+    validation error still returned while recording and nothing recorded for it, M = 0 records no launch"""
     from kindi_amd import gpudrv
-    assert lib.kt_plan_bytes(0) == 0 and lib.kt_plan_bytes(256) % 256 == 0
-    fake = ctypes.c_void_p(1 << 20)                       # 256-aligned, never dereferenced on these paths
-    info = gpudrv.KtPlanInfo()
-
-    def stage(C=5120, M=1, R=64, ldq=None):
-        s = gpudrv.KtStage()
-        s.W[0], s.R[0], s.Y[0] = 1 << 21, R, 1 << 22
-        s.C, s.XQ, s.ldq, s.XS, s.XA, s.M = C, 1 << 23, ldq or C, 1 << 24, 1 << 25, M
-        return s
-
-    def build(*stages):
-        arr = (gpudrv.KtStage * len(stages))(*stages)
-        return lib.kt_plan_build(arr, len(stages), fake, ctypes.byref(info), None)
-
-    assert lib.kt_plan_build(None, 1, fake, ctypes.byref(info), None) == INVALID
-    assert build(stage(C=100)) == INVALID                  # C % 128
-    assert build(stage(M=5)) == INVALID                    # one pass of at most 4 tokens
-    assert build(stage(), stage(M=2)) == INVALID           # every stage the same M
-    assert build(stage(C=32768)) == INVALID                # 16 K slices + the control wave > 16 waves
-    assert build(stage(R=0)) == INVALID                    # no matrix
-    assert build(stage(ldq=5128)) == INVALID               # ldq % 16
-    assert lib.kt_plan_run(None, ctypes.byref(info), None) == INVALID
+    recs = (gpudrv.KtLaunch * 4)()
+    n = ctypes.c_int(-1)
+    assert ctypes.sizeof(gpudrv.KtLaunch) == 8 + 4 * 7 + 4 + 8 * 24 + 4 * 24 + 512
+    assert lib.kt_record_end(ctypes.byref(n)) == INVALID
+    assert lib.kt_record_begin(None, 4) == INVALID
+    assert lib.kt_record_begin(recs, -1) == INVALID
+    assert lib.kt_record_begin(recs, 4) == 0
+    assert lib.kt_record_begin(recs, 4) == INVALID                   # no nesting
+    fake = ctypes.c_void_p(0x1000)
+    assert lib.kt_tern_gemv(fake, 64, 256, fake, 260, fake, fake, 1, fake, 64, None, None) == INVALID
+    assert lib.kt_tern_gemv(fake, 64, 256, fake, 256, fake, fake, 0, fake, 64, None, None) == 0
+    assert lib.kt_moe_topk_r(fake, 1, 128, 6, 1, None, 1.0, fake, fake, None) == INVALID   # sigmoid needs a bias
+    assert lib.kt_moe_topk_r(fake, 1, 128, 6, 2, fake, 1.0, fake, fake, None) == INVALID   # unknown scoring
+    assert lib.kt_record_end(ctypes.byref(n)) == 0 and n.value == 0
+    assert lib.kt_record_begin(None, 0) == 0                         # counting only
+    assert lib.kt_record_end(None) == 0
 
 
 def test_fold_validation(lib):

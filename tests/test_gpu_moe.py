@@ -1,5 +1,6 @@
-"""GPU parity of the q8_0 path (kt_q8_pack, kt_q8_quant, kt_q8_gemv) and the MoE dispatch (kt_moe_topk,
-kt_moe_sort, kt_q8_grouped, kt_moe_combine) against the CPU oracle."""
+"""GPU parity of the q8_0 path (kt_q8_pack, kt_q8_quant, kt_q8_gemv) and the MoE dispatch (kt_moe_topk(_r),
+kt_moe_sort, kt_q8_grouped, kt_moe_combine, kt_moe_decode(_r)) against the CPU oracle, with BASELINE's softmax router
+and Kindi's sigmoid + bias router (lightning.cu:373-468)."""
 import numpy as np
 import pytest
 import torch
@@ -271,7 +272,8 @@ def test_combine_bit_exact(kt):
 
 @pytest.mark.parametrize("E,H,F,M,k", [(128, 2688, 1856, 1, 6), (128, 2688, 1856, 4, 6), (128, 2688, 1856, 10, 6),
                                        (8, 96, 64, 10, 6), (16, 160, 96, 64, 1), (4, 64, 32, 3, 4), (8, 128, 64, 1, 3),
-                                       (16, 96, 4096, 1, 8), (16, 96, 8192, 1, 2), (4, 64, 32, 1, 4), (64, 2688, 1856, 1, 1)])
+                                       (16, 96, 4096, 1, 8), (16, 96, 8192, 1, 2), (4, 64, 32, 1, 4), (64, 2688, 1856, 1, 1),
+                                       (256, 96, 64, 1, 6), (1024, 64, 32, 1, 4), (1024, 64, 32, 3, 8)])
 def test_moe_decode_chain(kt, E, H, F, M, k):
     """kt_moe_decode (one token: two launches, the up product routing for itself and the down product combining a row
     group of every pick; more tokens: route, up and down with the quantization in their staging, combine) gives x bit
@@ -279,7 +281,8 @@ def test_moe_decode_chain(kt, E, H, F, M, k):
     without the shared-expert rows, on a workspace full of garbage (it needs no initialisation), twice in a row;
     ragged row groups (H = 96, 128: a last row group of a 32-row block), one pick a token, every expert active, k not a
     register-set size (3), the widest down input the one-token chain takes (F = 4096) and one past it (F = 8192: the
-    four-launch chain)"""
+    four-launch chain); more than 128 experts (E = 256, 1024: the up launch reads the chosen expert's pointer from the
+    table, and the top-k scans 4 / 16 logits a lane)"""
     lib, moe = kt
     say("moe decode chain", E, H, F, M, k)
     ups = moe.Q8Experts([q8_case(F, H, 3000 + e)[0] for e in range(E)], F, H)
@@ -309,3 +312,105 @@ def test_moe_decode_chain(kt, E, H, F, M, k):
         ids, gw = orc.router_topk(lg, k)
         assert np.array_equal(host(st["ids"]), ids)
 
+
+
+def sig_layer(moe, E, H, F, k, seed, scale=2.5):
+    ups = moe.Q8Experts([q8_case(F, H, seed + e)[0] for e in range(E)], F, H)
+    downs = moe.Q8Experts([q8_case(H, F, seed + 1000 + e)[0] for e in range(E)], H, F)
+    bias = rng(seed).normal(0, 0.3, E).astype(np.float32)
+    return moe.MoE(ups, downs, k, score="sigmoid", bias=dev(bias), scale=scale), bias
+
+
+@pytest.mark.parametrize("E,k", [(128, 6), (1000, 16), (256, 8)])
+def test_topk_sigmoid(kt, E, k):
+    """Kindi's router (sigmoid, bias for the choice, weights = chosen scores / their sum * scale) at config 4's token
+    counts: ids bit-exact against the oracle (pinned in tests/test_oracle.py by a float64 restatement and brute-force
+    top-k), weights within 2e-6 relative (the device expf and the host's differ in the last bit on some inputs: 58
+    of 60 weights bit-equal at 10 tokens); the one-launch route + lists gives the same ids, weights and lists"""
+    lib, moe = kt
+    say("topk sigmoid", E, k)
+    layer, bias = sig_layer(moe, E, 64, 32, k, 7000 + E)
+    for M in (1, 4, 10, 256):
+        lg = rng(M + E).normal(0, 1, (M, E)).astype(np.float32)
+        if M == 10:
+            lg[2, 5:5 + k + 3] = 0.5                                  # equal logits: the bias alone orders them
+        ids, gw = layer.route(dev(lg))
+        rid, rgw = orc.router_sig(lg, bias, 2.5, k)
+        assert np.array_equal(host(ids), rid), M
+        g = host(gw)
+        assert np.allclose(g, rgw, rtol=2e-6, atol=0), M
+        say("sigmoid weights bit-exact: %d of %d" % (int((g.view(np.uint32) == rgw.view(np.uint32)).sum()), g.size))
+        if M * k <= 64:
+            ids2, gw2, lists2 = layer.route_lists(dev(lg))
+            assert np.array_equal(host(ids2), rid) and np.array_equal(host(gw2), g), M
+            lists = layer.lists(ids)
+            for a_, b_ in zip(lists2[:4], lists[:4]):
+                assert np.array_equal(host(a_), host(b_)), M
+
+
+def test_topk_nan_distinct(kt):
+    """a token with fewer numbers than k: the numbers first (by value), then NaN entries from the lowest index, every
+    pick distinct, as the oracle ranks them (both scorings)"""
+    lib, moe = kt
+    say("topk NaN")
+    E, k, M = 128, 6, 3
+    lg = np.full((M, E), np.nan, np.float32)
+    lg[0, [9, 40, 100]] = [-3.0, 1.0, 0.5]
+    lg[1, :] = rng(3).normal(0, 1, E)
+    lg[1, ::2] = np.nan
+    lg[2, 127] = 2.0
+    layer, bias = sig_layer(moe, E, 64, 32, k, 7500)
+    soft = moe.MoE(layer.up, layer.down, k)
+    ids, gw = soft.route(dev(lg))
+    rid, _ = orc.router_topk(lg, k)
+    assert np.array_equal(host(ids), rid)
+    assert all(len(set(r)) == k for r in host(ids).tolist())
+    zb = moe.MoE(layer.up, layer.down, k, score="sigmoid", bias=torch.zeros(E, device="cuda"), scale=1.0)
+    ids, gw = zb.route(dev(lg))
+    rid, _ = orc.router_sig(lg, np.zeros(E, np.float32), 1.0, k)
+    assert np.array_equal(host(ids), rid)
+    assert all(len(set(r)) == k for r in host(ids).tolist())
+
+
+@pytest.mark.parametrize("E,H,F,M,k", [(128, 2688, 1856, 1, 6), (128, 2688, 1856, 8, 6), (256, 96, 64, 1, 6),
+                                       (32, 96, 64, 40, 4)])
+def test_moe_sigmoid_chain(kt, E, H, F, M, k):
+    """the MoE layer with Kindi's router: kt_moe_decode_r gives x bit for bit as forward() (route_r / topk_r, sort,
+    grouped up, relu^2 quantize, grouped down, combine), whose picks and weights are the oracle's"""
+    lib, moe = kt
+    say("moe sigmoid chain", E, H, F, M, k)
+    layer, bias = sig_layer(moe, E, H, F, k, 8000)
+    x = rng(M + H + 1).normal(0, 1, (M, H)).astype(np.float32)
+    lg = rng(M + E + 1).normal(0, 1, (M, E)).astype(np.float32)
+    lgd = dev(lg)
+    want, st = layer.forward(dev(x), lgd)
+    rid, rgw = orc.router_sig(lg, bias, 2.5, k)
+    assert np.array_equal(host(st["ids"]), rid)
+    assert np.allclose(host(st["gw"]), rgw, rtol=2e-6, atol=0)
+    if M * k <= 64:
+        xd = dev(x)
+        layer.decode(xd, lgd)
+        assert np.array_equal(host(xd).view(np.uint32), host(want).view(np.uint32))
+
+
+def test_moe_decode_row_at_allocation_end(kt):
+    """the one-token chain with an odd slice count (H = 96: the up launch's second task of its last wave is off) reads
+    only inside x: x and the logits sit at the very end of allocations of exactly 2 MiB"""
+    lib, moe = kt
+    say("moe decode x at allocation end")
+    E, H, F, k = 8, 96, 64, 6
+    ups = moe.Q8Experts([q8_case(F, H, 9000 + e)[0] for e in range(E)], F, H)
+    downs = moe.Q8Experts([q8_case(H, F, 9100 + e)[0] for e in range(E)], H, F)
+    layer = moe.MoE(ups, downs, k)
+    x = rng(11).normal(0, 1, (1, H)).astype(np.float32)
+    lg = rng(12).normal(0, 1, (1, E)).astype(np.float32)
+    n = (2 << 20) // 4
+    xb = torch.empty(n, dtype=torch.float32, device="cuda")
+    lb = torch.empty(n, dtype=torch.float32, device="cuda")
+    xe = xb[n - H:].view(1, H)
+    le = lb[n - E:].view(1, E)
+    xe.copy_(dev(x))
+    le.copy_(dev(lg))
+    want, _ = layer.forward(dev(x), dev(lg))
+    layer.decode(xe, le)
+    assert np.array_equal(host(xe).view(np.uint32), host(want).view(np.uint32))

@@ -473,6 +473,49 @@ def test_router_softmax_topk(orc):
     assert ids.tolist() == [[2, 5]] and np.allclose(gw, 0.5)
 
 
+def test_router_sigmoid_bias(orc):
+    """Kindi's Lightning router (lt_topk, lightning.cu:373-412) against a float64 restatement: sigmoid, bias added
+    for the choice only, the k largest choices, weights = chosen scores / their sum * scale"""
+    M, E, k, scale = 64, 128, 6, 2.5
+    lg = rng(84).normal(0, 1, (M, E)).astype(np.float32)
+    bias = rng(85).normal(0, 0.3, E).astype(np.float32)
+    ids, gw = orc.router_sig(lg, bias, scale, k)
+    s = 1.0 / (1.0 + np.exp(-lg.astype(np.float64)))
+    ch = s + bias
+    top = np.argsort(-ch, axis=1, kind="stable")[:, :k]
+    assert np.array_equal(ids, top)
+    sel = np.take_along_axis(s, top, 1)
+    assert np.allclose(gw, sel / sel.sum(1, keepdims=True) * scale, rtol=1e-6)
+    assert np.allclose(gw.sum(1), scale, rtol=1e-6)
+    # the bias moves the choice but not the weight: a large bias on expert 3 makes it the first pick of every token,
+    # weighted by its own score
+    b2 = np.zeros(E, np.float32)
+    b2[3] = 10.0
+    ids, gw = orc.router_sig(lg, b2, 1.0, k)
+    assert (ids[:, 0] == 3).all()
+    s3 = 1.0 / (1.0 + np.exp(-lg[:, 3].astype(np.float64)))
+    assert np.allclose(gw[:, 0], s3 / np.take_along_axis(s, ids, 1).sum(1), rtol=1e-6)
+    # ties (equal logits, zero bias) go to the lower index; softmax and sigmoid agree on the choice with zero bias
+    t = np.zeros((1, 8), np.float32)
+    t[0, [5, 2, 6]] = 1.0
+    ids, gw = orc.router_sig(t, np.zeros(8, np.float32), 1.0, 2)
+    assert ids.tolist() == [[2, 5]] and np.allclose(gw, 0.5)
+    ids2, _ = orc.router_topk(lg, k)
+    ids3, _ = orc.router_sig(lg, np.zeros(E, np.float32), 1.0, k)
+    assert np.array_equal(ids2, ids3)
+
+
+def test_router_nan_ranks_last(orc):
+    """a NaN logit ranks below every number; with fewer numbers than k the NaN entries follow, lowest index first, so
+    the picks stay distinct"""
+    lg = np.full((1, 16), np.nan, np.float32)
+    lg[0, [9, 4]] = [-3.0, 1.0]
+    ids, gw = orc.router_topk(lg, 4)
+    assert ids.tolist() == [[4, 9, 0, 1]]
+    ids, gw = orc.router_sig(lg, np.zeros(16, np.float32), 1.0, 4)
+    assert ids.tolist() == [[4, 9, 0, 1]]
+
+
 # ------------------------------------------------------------------------------------------- fused producers
 def hadamard(n):
     """Sylvester's Hadamard matrix H[i, j] = (-1)^popcount(i & j) (float64)"""
