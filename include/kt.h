@@ -140,6 +140,19 @@ int kt_record_end(int* n);
 int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const float* XS, const int32_t* XA,
                  int per_row, int M, float* Y, uint16_t* Y16, int ldy, int32_t* dbg, void* stream);
 
+/* kt_tern_expand: the signed trits t = d - 1 of W as int8 in natural order, W8 [8 ceil(R/8)][C] (kt_tern_expand_bytes
+   bytes, 16-byte aligned; rows past R are padding), the form k_mm_g5q unpacks its tiles into (chunk.cu:836, tq(d) =
+   d - 1). Made per call or kept with the weights (4.25 times their bytes).
+   kt_tern_gemm8: kt_tern_gemm with per_row = 1 over W8 and W's scales, with the same bits: Y = XS[t][0] *
+   sum_g fmaf(v, d[r][g], .) in group order. The product reads both operands into LDS by DMA and unpacks nothing.
+   Grids of fewer 128-token x 256-row blocks than the GPU has CUs run kt_tern_gemm's packed-trit product instead
+   (the same bits). M ldq and the W8 bytes stay below 2^31. Replaces k_tc_mm2 (tc_hip.cu:243-269) and k_mm_g5q (chunk.cu:858-918) like
+   kt_tern_gemm. */
+size_t kt_tern_expand_bytes(int R, int C);
+int kt_tern_expand(const void* W, int R, int C, int8_t* W8, void* stream);
+int kt_tern_gemm8(const int8_t* W8, const void* W, int R, int C, const int8_t* XQ, int ldq, const float* XS, int M,
+                  float* Y, uint16_t* Y16, int ldy, int32_t* dbg, void* stream);
+
 /* ---------------------------------------------------------------- q8_0
    Device layout "kq8": int8 codes + fp16 scale per 32 columns (1.0625 B/w, as GGUF Q8_0).
    kt_q8_pack: GGUF Q8_0 rows (34-byte blocks: fp16 d, 32 int8; dsv41_cpu.c:77-78) -> W. Replaces dg_mat_q8

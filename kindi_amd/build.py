@@ -9,7 +9,7 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libkt_gfx950.so")
-SOURCES = ["kt_decode.hip", "kt_gemv.hip", "kt_gemv2.hip", "kt_mma.hip", "kt_prefill.hip",
+SOURCES = ["kt_decode.hip", "kt_gemv.hip", "kt_gemv2.hip", "kt_mma.hip", "kt_prefill.hip", "kt_prefill8.hip",
            "kt_moe.hip", "kt_moe1.hip", "kt_fold.hip", "kt_api.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",

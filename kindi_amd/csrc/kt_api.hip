@@ -39,6 +39,11 @@ extern "C" __global__ void k_tern_sum(const float*, float*, int, int, int);
 template <bool DBG, bool RS>
 __global__ void k_tern_gemm(const uint32_t*, const uint16_t*, int, int, const int8_t*, int, const float*, int, float*,
                             uint16_t*, int, int32_t*);
+extern "C" __global__ void k_tern_expand(const uint4*, int, long long, int, int8_t*);
+template <bool DBG>
+__global__ void k_tern_gemm8(const int8_t*, const uint16_t*, int, int, const int8_t*, int, const float*, int, float*,
+                             uint16_t*, int, int32_t*, int, int);
+size_t kt_gemm8_lds();
 template <int WT, int WR, int PD, bool DBG>
 __global__ void k_tern_gemm_rs1(const uint32_t*, const uint16_t*, int, int, const int8_t*, int, const float*, int,
                                 float*, uint16_t*, int, int32_t*);
@@ -546,6 +551,73 @@ int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const f
   if(per_row){ if(dbg) KT_TG(true, true); else KT_TG(false, true); }
   else { if(dbg) KT_TG(true, false); else KT_TG(false, false); }
 #undef KT_TG
+  return 0;
+}
+
+/* the current device's CU count, queried once per device */
+static int kt_cu_count(int* cus){
+  static int cache[64];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if(e != hipSuccess) return (int)e;
+  if(dev < 0 || dev >= 64) return KT_INVALID;
+  if(!cache[dev]){
+    int n = 0;
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if(e != hipSuccess) return (int)e;
+    cache[dev] = n;
+  }
+  *cus = cache[dev];
+  return 0;
+}
+
+size_t kt_tern_expand_bytes(int R, int C){
+  if(R <= 0 || C <= 0 || C % 128) return 0;
+  return (size_t)kt_r8(R) * KT_RG * C;
+}
+
+int kt_tern_expand(const void* W, int R, int C, int8_t* W8, void* stream){
+  if(!W || !W8 || R <= 0 || C <= 0 || C % 128 || !kt_al(W, 16) || !kt_al(W8, 16)) return KT_INVALID;
+  const int NU = C / 128;
+  const long long nq = (long long)kt_r8(R) * NU * 16;                     /* kt2 chunks */
+  KT_LAUNCH(k_tern_expand, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, kt_stream(stream), (const uint4*)W, NU,
+            nq, C, W8);
+  return 0;
+}
+
+int kt_tern_gemm8(const int8_t* W8, const void* W, int R, int C, const int8_t* XQ, int ldq, const float* XS, int M,
+                  float* Y, uint16_t* Y16, int ldy, int32_t* dbg, void* stream){
+  if(M == 0) return 0;
+  if(!W8 || !W || !XQ || !XS || (!Y && !Y16) || R <= 0 || M < 0 || C <= 0 || C % 128 || ldq < C || ldq % 16
+     || ldy < R || !kt_al(W, 16) || !kt_al(W8, 16) || !kt_al(XQ, 16)) return KT_INVALID;
+  const int NG = C / 128;
+  /* 32-bit buffer offsets, an out-of-range offset at 2^31 */
+  if((long long)M * ldq >= (1ll << 31) || (long long)kt_r8(R) * KT_RG * C >= (1ll << 31)) return KT_INVALID;
+  const uint16_t* scales = (const uint16_t*)((const uint8_t*)W + kt_code_bytes(R, NG));
+  /* a grid short of one 128 x 256 block a CU runs the packed-trit product instead (the same per-row numbers and
+     order, so the same bits) */
+  int cus = 0;
+  const int ec = kt_cu_count(&cus);
+  if(ec) return ec;
+  if((long long)((kt_r8(R) * KT_RG + 255) / 256) * ((M + 127) / 128) < cus)
+    return kt_tern_gemm(W, R, C, XQ, ldq, XS, nullptr, 1, M, Y, Y16, ldy, dbg, stream);
+  const size_t lds = kt_gemm8_lds();
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  std::call_once(once, []{
+    const size_t n = kt_gemm8_lds();
+    attr = hipFuncSetAttribute((const void*)k_tern_gemm8<false>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)n);
+    if(attr == hipSuccess)
+      attr = hipFuncSetAttribute((const void*)k_tern_gemm8<true>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)n);
+  });
+  if(attr != hipSuccess) return (int)attr;
+  /* one block a CU (its LDS), each taking tiles blockIdx.x, + grid, ... */
+  const int gx = (kt_r8(R) * KT_RG + 255) / 256, gy = (M + 127) / 128;
+  const dim3 grid(gx * gy < cus ? gx * gy : cus);
+  if(dbg) KT_LAUNCH(k_tern_gemm8<true>, grid, dim3(512), lds, kt_stream(stream), W8, scales, R, C, XQ, ldq, XS, M, Y,
+                    Y16, ldy, dbg, gx, gy);
+  else KT_LAUNCH(k_tern_gemm8<false>, grid, dim3(512), lds, kt_stream(stream), W8, scales, R, C, XQ, ldq, XS, M, Y,
+                 Y16, ldy, dbg, gx, gy);
   return 0;
 }
 

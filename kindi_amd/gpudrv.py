@@ -43,6 +43,9 @@ SIGNATURES = [
     ("kt_record_begin", I, [ctypes.POINTER(KtLaunch), I]),
     ("kt_record_end", I, [ctypes.POINTER(I)]),
     ("kt_tern_gemm", I, [P, I, I, P, I, P, P, I, I, P, P, I, P, P]),
+    ("kt_tern_expand_bytes", S, [I, I]),
+    ("kt_tern_expand", I, [P, I, I, P, P]),
+    ("kt_tern_gemm8", I, [P, P, I, I, P, I, P, I, P, P, I, P, P]),
     ("kt_q8_weight_bytes", S, [I, I]),
     ("kt_q8_pack", I, [P, I, I, P, P]),
     ("kt_q8_quant", I, [P, I, I, I, I, P, I, P, I, P]),

@@ -68,6 +68,18 @@ class TernaryMatrix(object):
     def nbytes(self):
         return self.W.numel()
 
+    def expand(self, out=None):
+        """the signed trits as int8 [8 ceil(R/8), C] (kt_tern_expand): the operand of kt_tern_gemm8. With out=None a
+        new tensor; pass a buffer of kt_tern_expand_bytes to reuse one"""
+        lib = gpudrv.load()
+        n = lib.kt_tern_expand_bytes(self.R, self.C)
+        if out is None:
+            out = torch.empty(n, dtype=torch.int8, device=self.W.device)
+        if out.numel() < n or out.dtype != torch.int8 or out.data_ptr() % 16:
+            raise ValueError("int8 trit buffer: %d bytes, 16-byte aligned" % n)
+        gpudrv.check(lib.kt_tern_expand(ptr(self.W), self.R, self.C, ptr(out), stream()), "kt_tern_expand")
+        return out
+
     @classmethod
     def _empty(cls, R, C, device, W):
         lib = gpudrv.load()
@@ -292,6 +304,22 @@ class Linear(object):
         rc = lib.kt_tern_gemm(ptr(m.W), m.R, m.C, ptr(act.XQ), act.XQ.stride(0), ptr(act.XS), ptr(act.XA),
                               1 if act.per_row else 0, act.M, ptr(Y), ptr(y16), ldy, ptr(dbg), stream())
         gpudrv.check(rc, "kt_tern_gemm")
+        return Y if Y is not None else Y16
+
+    def gemm8(self, name, act, W8, Y=None, Y16=None, dbg=None):
+        """the prefill product over the int8 trits W8 (TernaryMatrix.expand) with per-token activation scales: the bits
+        of gemm() with per_row activations"""
+        lib = gpudrv.load()
+        m = self.w[name]
+        if act.C != m.C or not act.per_row or act.hp:
+            raise ValueError("gemm8 takes per-token int8 activations of width %d" % m.C)
+        if Y is None and Y16 is None:
+            Y = torch.empty((act.M, m.R), dtype=torch.float32, device=act.XQ.device)
+        ldy = (Y if Y is not None else Y16).stride(0)
+        y16 = Y16.view(torch.int16) if Y16 is not None else None
+        rc = lib.kt_tern_gemm8(ptr(W8), ptr(m.W), m.R, m.C, ptr(act.XQ), act.XQ.stride(0), ptr(act.XS), act.M,
+                               ptr(Y), ptr(y16), ldy, ptr(dbg), stream())
+        gpudrv.check(rc, "kt_tern_gemm8")
         return Y if Y is not None else Y16
 
     # ------------------------------------------------------------------ either

@@ -529,3 +529,37 @@ def test_gguf_ptq1_by_name(kt, tmp_path):
     for name, want in wants.items():
         m = gguf.load_ternary(str(f), name, chunk_rows=8, g=g)
         assert np.array_equal(host(m.W), want), name
+
+
+@pytest.mark.parametrize("R,C,M", [(64, 128, 1), (100, 256, 7), (300, 384, 130), (2048, 2048, 512),
+                                   (8200, 128, 1000), (8200, 256, 1000), (8200, 384, 1000), (8200, 640, 1000),
+                                   (12288, 4096, 700), (4096, 12288, 2048)])
+def test_gemm8(kt, R, C, M):
+    """the int8-trit prefill product (kt_tern_expand + kt_tern_gemm8): the expanded trits equal the pack's digits - 1,
+    the int32 group values equal the oracle's, and Y / Y16 carry the bits of kt_tern_gemm with per-row activations.
+    Grids of 256 blocks and more run the DMA kernel (ragged rows and tokens; 1, 2, 3 and 5 groups: every turn of its
+    two-group loop and both tails); smaller ones the packed-trit kernel"""
+    lib, linear = kt
+    say("gemm8", R, C, M)
+    W, dig, bc, dpm = upload(linear, R, C, R * 5 + M)
+    W8 = W.expand()
+    w8 = host(W8).reshape(-1, C)
+    assert w8.shape[0] == (R + 7) // 8 * 8
+    assert np.array_equal(w8[:R], dig.astype(np.int16) - 1)
+    L = linear.Linear({"w": W})
+    X = rng(M + 9).normal(0, 1, (M, C)).astype(np.float32)
+    act = linear.quantize(dev(X), per_row=True)
+    Y = torch.empty((M, R), dtype=torch.float32, device="cuda")
+    Y16 = torch.empty((M, R), dtype=torch.float16, device="cuda")
+    L.gemm("w", act, Y=Y, Y16=Y16)
+    Y8 = torch.full((M, R), np.nan, dtype=torch.float32, device="cuda")
+    Y8h = torch.empty((M, R), dtype=torch.float16, device="cuda")
+    L.gemm8("w", act, W8, Y=Y8, Y16=Y8h)
+    assert np.array_equal(host(Y8).view(np.uint32), host(Y).view(np.uint32))
+    assert np.array_equal(host(Y8h).view(np.uint16), host(Y16).view(np.uint16))
+    if R * M * (C // 128) <= (1 << 24):
+        dbg = torch.empty((M, R, C // 128), dtype=torch.int32, device="cuda")
+        Y2 = L.gemm8("w", act, W8, dbg=dbg)
+        Q, XS, XA = orc.quant_q8(X, per_row=True)
+        assert np.array_equal(host(dbg), orc.tern_acc(bc, R, C, Q))
+        assert np.array_equal(host(Y2).view(np.uint32), host(Y).view(np.uint32))
