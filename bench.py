@@ -265,18 +265,27 @@ def config2(torch, linear, synth, timer, steps):
     res = {}
     for i, (n, R, C) in enumerate(synth.CFG["c2"]["mats"]):
         bc, dpm = synth.tern_pack(R, C, 20 + i, device="cuda")
-        L = linear.Linear({"w": linear.TernaryMatrix(bc, dpm, R, C)})
+        W = linear.TernaryMatrix(bc, dpm, R, C)
+        L = linear.Linear({"w": W})
+        W8 = W.expand()
+        ms_x = timer.run(lambda: W.expand(out=W8), max(steps // 2, 3), 2)
         for M in (512, 2048):
             act = linear.quantize(synth.activations(M, C, 22 + i, device="cuda"), per_row=True)
             Y16 = torch.empty((M, R), dtype=torch.float16, device="cuda")
             ms = timer.run(lambda: L.gemm("w", act, Y16=Y16), max(steps // 2, 3), 2)
             tops = 2.0 * M * R * C / ms / 1e9
             # every MFMA the kernels issue is useful work (2 M R C operations exactly, counted by
-            # SQ_INSTS_VALU_MFMA_MOPS_I8 in profiles/prefill_pmc.md), so the MFMA utilisation against the int8 peak is
-            # the achieved rate over the peak; the counters put the clock under this load at 2.08-2.16 GHz
+            # SQ_INSTS_VALU_MFMA_MOPS_I8), so the achieved rate over the int8 peak is the fraction of peak; the
+            # counters put the clock under this load at 2.08-2.17 GHz
+            # the same product over the int8 trit copy (kt_tern_expand once, kept with the weights: 4.25 times their
+            # bytes; kt_tern_gemm8, the same bits); expand_us is the copy's cost per matrix
+            ms8 = timer.run(lambda: L.gemm8("w", act, W8, Y16=Y16), max(steps // 2, 3), 2)
+            tops8 = 2.0 * M * R * C / ms8 / 1e9
             res["%s M=%d" % (n, M)] = {"shape": [R, C], "us": round(ms * 1e3, 1), "TOPS": round(tops, 1),
                                        "frac_int8_peak": round(tops / INT8_PEAK, 4),
-                                       "mfma_util": round(tops / INT8_PEAK, 4)}
+                                       "int8_copy_us": round(ms8 * 1e3, 1), "int8_copy_TOPS": round(tops8, 1),
+                                       "int8_copy_frac_int8_peak": round(tops8 / INT8_PEAK, 4),
+                                       "expand_us": round(ms_x * 1e3, 1)}
             # the vendor's plain int8 GEMM (hipBLASLt through torch._int_mm: int32 out, no scales, no trit unpack)
             # on the same shapes and box, as the practical ceiling of an int8 product here
             try:
@@ -288,6 +297,7 @@ def config2(torch, linear, synth, timer, steps):
                 del qb
             except Exception as e:                                   # not every build routes int8 mm
                 res["%s M=%d" % (n, M)]["vendor_int8"] = repr(e)[:80]
+        del W8
     return res
 
 
