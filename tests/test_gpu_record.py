@@ -132,3 +132,46 @@ def test_step_plan_chained(kt):
         plan.launch()
         for n, t in y.items():
             assert np.array_equal(host(t), want[n]), (it, n)
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_moe_and_producer_records(kt, M):
+    """the MoE decode chain (two launches at one token, four above; Kindi's sigmoid router) and a fused producer
+    (rmsfold) recorded and replayed: the same x and int8 rows as the direct calls"""
+    gpudrv, linear = kt
+    from kindi_amd import moe
+    from kt_cases import q8_case
+    say("records moe + rmsfold", M)
+    E, H, F, k = 16, 2688, 1856, 6
+    ups = moe.Q8Experts([q8_case(F, H, 100 + e)[0] for e in range(E)], F, H)
+    downs = moe.Q8Experts([q8_case(H, F, 200 + e)[0] for e in range(E)], H, F)
+    bias = dev(rng(3).normal(0, 0.3, E).astype(np.float32))
+    layer = moe.MoE(ups, downs, k, score="sigmoid", bias=bias, scale=2.0)
+    x0 = dev(rng(M).normal(0, 1, (M, H)).astype(np.float32))
+    lg = dev(rng(M + 1).normal(0, 1, (M, E)).astype(np.float32))
+    work = layer.workspace(M)
+    x = x0.clone()
+    layer.decode(x, lg, work)
+    want = host(x).copy()
+    x.copy_(x0)
+    torch.cuda.synchronize()
+    recs, n = record(gpudrv, lambda: layer.decode(x, lg, work))
+    assert n == (2 if M == 1 else 4)
+    assert np.array_equal(host(x), host(x0))                       # recording launched nothing
+    replay_raw(gpudrv, recs, n)
+    assert np.array_equal(host(x).view(np.uint32), want.view(np.uint32))
+    # rmsfold: x + one residual part -> norm -> fold -> int8 row
+    C = 5120
+    xs = dev(rng(7 + M).normal(0, 1, (M, C)).astype(np.float32))
+    r = dev(rng(8 + M).normal(0, 1, (M, C)).astype(np.float32))
+    w = dev(rng(9).normal(1, 0.1, C).astype(np.float32))
+    sg = dev(np.where(rng(10).random(C) < 0.5, -1.0, 1.0).astype(np.float32))
+    out = linear._act_out(M, C, "cuda")
+    a1 = linear.rmsfold(xs, w, sg, 1024, r=r, nparts=1, out=out)
+    q1, s1, x1 = host(a1.XQ).copy(), host(a1.XS).copy(), host(a1.XA).copy()
+    for t in (out.XQ, out.XS, out.XA):
+        t.zero_()
+    recs, n = record(gpudrv, lambda: linear.rmsfold(xs, w, sg, 1024, r=r, nparts=1, out=out))
+    assert n == 1
+    replay_raw(gpudrv, recs, n)
+    assert np.array_equal(host(out.XQ), q1) and np.array_equal(host(out.XS), s1) and np.array_equal(host(out.XA), x1)
