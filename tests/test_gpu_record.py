@@ -77,7 +77,8 @@ def test_gemv_records(kt, R, C, M):
     assert np.array_equal(host(dbg), acc)
 
 
-@pytest.mark.parametrize("R,C,M,per_row", [(12288, 4096, 512, True), (4096, 12288, 512, True), (2048, 2048, 512, False)])
+@pytest.mark.parametrize("R,C,M,per_row", [(12288, 4096, 512, True), (4096, 12288, 512, True), (2048, 2048, 512, False),
+                                           (12288, 4096, 2048, True)])
 def test_gemm_records(kt, R, C, M, per_row):
     gpudrv, linear = kt
     say("records gemm", R, C, M, per_row)
@@ -94,6 +95,15 @@ def test_gemm_records(kt, R, C, M, per_row):
     Y16.fill_(np.nan)
     replay_raw(gpudrv, recs, n)
     assert np.array_equal(host(Y), want) and np.array_equal(host(Y16), want16)
+    if per_row:
+        # the int8-copy product (145 KB of dynamic LDS: the record carries it): the expansion and the product
+        W8 = torch.empty(gpudrv.load().kt_tern_expand_bytes(R, C), dtype=torch.int8, device="cuda")
+        recs, n = record(gpudrv, lambda: (W.expand(out=W8), L.gemm8("w", act, W8, Y=Y, Y16=Y16)))
+        assert n == 2
+        Y.fill_(np.nan)
+        Y16.fill_(np.nan)
+        replay_raw(gpudrv, recs, n)
+        assert np.array_equal(host(Y), want) and np.array_equal(host(Y16), want16)
 
 
 def test_step_plan_chained(kt):
