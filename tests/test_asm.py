@@ -2,7 +2,7 @@
 cross-compiles here).
 
 - No kernel uses scratch (private segment) apart from the listed ones: the debug instantiations (int32 unit values
-  written out for the tests) and the 2-4 token register-ring plan executor.
+  written out for the tests).
 - The decode product at 8-32 tokens and both prefill kernels read global memory only through buffer resources that
   span exactly their buffers, so an out-of-range offset reads zeros and cannot fault.
 - No kernel writes through the scalar data cache.
@@ -63,7 +63,7 @@ def _kernels(text):
 
 SCRATCH_OK = {"k_gemv_flat1<0, 1, true, false>", "k_gemv_pair<true>", "k_q8_mma<false, true, false>",
               "k_q8_mma<true, true, false>", "k_tern_gemm<true, false>", "k_tern_gemm<true, true>",
-              "k_tern_gemm_rs1<4, 2, 3, true>"}
+              "k_tern_gemm_rs1<4, 2, 3, true>", "k_tern_gemm8<true>"}
 
 
 def _demangle(names):
