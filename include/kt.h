@@ -128,6 +128,9 @@ typedef struct kt_launch {
 } kt_launch;
 int kt_record_begin(kt_launch* recs, int max);
 int kt_record_end(int* n);
+/* launch records recs[0 .. n) in order, record i on streams[i % nstreams] (1 to 16 streams), with
+   hipModuleLaunchKernel: Replay.launch (spec.py:303-320) as one C loop. */
+int kt_replay(const kt_launch* recs, int n, void* const* streams, int nstreams);
 
 /* ---------------------------------------------------------------- prefill product (any M, matrix cores)
    Y and/or Y16 [M][ldy] (fp32 / fp16 bits); dbg as kt_tern_gemv. XA is accepted for the reference's argument list

@@ -430,6 +430,18 @@ int kt_init(int device){
 
 const char* kt_error_string(int rc){ return hipGetErrorString((hipError_t)rc); }
 
+int kt_replay(const kt_launch* recs, int n, void* const* streams, int nstreams){
+  if(n < 0 || (n > 0 && !recs) || nstreams < 1 || nstreams > 16 || !streams) return KT_INVALID;
+  for(int i = 0; i < n; ++i){
+    const kt_launch& L = recs[i];
+    const hipError_t e = hipModuleLaunchKernel((hipFunction_t)L.fn, L.grid[0], L.grid[1], L.grid[2], L.block[0],
+                                               L.block[1], L.block[2], L.shmem, kt_stream(streams[i % nstreams]),
+                                               (void**)L.args, nullptr);
+    if(e != hipSuccess) return (int)e;
+  }
+  return 0;
+}
+
 int kt_record_begin(kt_launch* recs, int max){
   if(kt_rec_on || max < 0 || (max > 0 && !recs)) return KT_INVALID;
   kt_rec_tls.buf = recs; kt_rec_tls.max = max; kt_rec_tls.n = 0; kt_rec_tls.err = 0;

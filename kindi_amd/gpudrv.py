@@ -42,6 +42,7 @@ SIGNATURES = [
     ("kt_tern_sum", I, [P, P, I, I, I, P]),
     ("kt_record_begin", I, [ctypes.POINTER(KtLaunch), I]),
     ("kt_record_end", I, [ctypes.POINTER(I)]),
+    ("kt_replay", I, [ctypes.POINTER(KtLaunch), I, ctypes.POINTER(P), I]),
     ("kt_tern_gemm", I, [P, I, I, P, I, P, P, I, I, P, P, I, P, P]),
     ("kt_tern_expand_bytes", S, [I, I]),
     ("kt_tern_expand", I, [P, I, I, P, P]),

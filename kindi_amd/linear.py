@@ -356,6 +356,12 @@ class Plan(object):
         self.nodes = [(r.fn, tuple(r.grid), tuple(r.block), r.shmem, r.args) for r in recs[:self.n]]
 
     def launch(self):
+        """the records in order on the current stream, in one C loop (kt_replay)"""
+        ss = (VP * 1)(torch.cuda.current_stream().cuda_stream)
+        gpudrv.check(gpudrv.load().kt_replay(self.recs, self.n, ss, 1), "kt_replay")
+
+    def launch_nodes(self):
+        """the node tuples launched one by one from Python with hipModuleLaunchKernel, as Kindi's Replay does"""
         L = gpudrv.hip().hipModuleLaunchKernel
         s = stream()
         for fn, g, b, sh, args in self.nodes:

@@ -27,7 +27,7 @@ def lib():
 
 def test_exports_every_declared_symbol(lib):
     names = declared()
-    assert len(names) == 37
+    assert len(names) == 38
     for n in names:
         assert hasattr(lib, n), n
     from kindi_amd import gpudrv
@@ -114,6 +114,11 @@ def test_record_protocol(lib):
     assert lib.kt_record_end(ctypes.byref(n)) == 0 and n.value == 0
     assert lib.kt_record_begin(None, 0) == 0                         # counting only
     assert lib.kt_record_end(None) == 0
+    ss = (ctypes.c_void_p * 1)(None)
+    assert lib.kt_replay(recs, -1, ss, 1) == INVALID                 # kt_replay checks before launching
+    assert lib.kt_replay(None, 1, ss, 1) == INVALID
+    assert lib.kt_replay(recs, 1, ss, 0) == INVALID
+    assert lib.kt_replay(recs, 0, ss, 1) == 0
 
 
 def test_fold_validation(lib):

@@ -139,7 +139,12 @@ def test_step_plan_chained(kt):
         want = {n: host(t).copy() for n, t in y.items()}
         for t in y.values():
             t.fill_(np.nan)
-        plan.launch()
+        plan.launch()                                       # kt_replay: the records in one C loop
+        for n, t in y.items():
+            assert np.array_equal(host(t), want[n]), (it, n)
+        for t in y.values():
+            t.fill_(np.nan)
+        plan.launch_nodes()                                 # Kindi's Replay loop over the node tuples
         for n, t in y.items():
             assert np.array_equal(host(t), want[n]), (it, n)
 
