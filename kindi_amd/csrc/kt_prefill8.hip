@@ -19,10 +19,11 @@
    Two sets of int32 accumulators: group g's MFMAs run while group g - 1's epilogue is applied, written out in issue
    order (each MFMA followed by 8 epilogue VALU operations; on gfx950 a wave issues in order, and the VALU work
    overlaps an MFMA only when it sits behind it in the stream). One block a CU (its 145 KB of LDS) takes tiles
-   blockIdx.x, + gridDim.x, ...; a tile's stores go out before the next tile's first DMAs.
+   blockIdx.x, + gridDim.x, ...; a tile's outputs go out through LDS as 16-byte token rows before the next tile's
+   first DMAs.
    Measured on MI355X (config 2, M = 2048, fp16 out, against k_tern_gemm on the packed trits): gate/up [12288 x 4096]
-   174 against 199 us, down [4096 x 12288] 138 against 172 us. Below one block a CU (M = 512) the packed-trit kernels
-   are faster and kt_tern_gemm8 runs them. */
+   131 against 199 us, down [4096 x 12288] 128 against 172 us (with two-byte stores straight from the accumulators:
+   175 and 142 us). Below one block a CU (M = 512) the packed-trit kernels are faster and kt_tern_gemm8 runs them. */
 #include "kt_common.h"
 
 typedef int kt8_v4i __attribute__((ext_vector_type(4)));
@@ -300,26 +301,66 @@ k_tern_gemm8(const int8_t* __restrict__ W8, const uint16_t* __restrict__ scales,
       epi(g, cy, hy0, hy1);
     } else epi(g - 1, cx, hx0, hx1);
     __syncthreads();                    /* every wave is done with every stage of this tile */
-    /* Y = XS[t] * acc: lanes of one register write 32 consecutive rows of one token */
-    const int cr0 = r0 + br0, cr1 = cr0 + 32;
+    /* Y = XS[t] * acc, each output through LDS: a wave stages its 64 tokens x 64 rows (the stages are free until the
+       next tile's first DMAs), token rows at a 16-byte-padded pitch, then writes 16 bytes a lane, whole token rows of
+       the block in contiguous runs (fp16: 8 store instructions a wave and tile in place of 64 two-byte ones). The
+       launcher routes outputs not 16-byte aligned, or with ldy not a multiple of 8, to the packed-trit kernel. */
+    const int tw0 = n0 + wt * 64, rw0 = r0 + wr * 64;
+    auto staged = [&](auto tag, auto* Yp){
+      using T = decltype(tag);
+      /* the lane index taken through an empty asm: what is computed from it here is not hoisted out of the tile loop
+         (where it would hold registers the products need) */
+      int lane = threadIdx.x & 63;
+      asm volatile("" : "+v"(lane));
+      constexpr int ES = (int)sizeof(T), PITCH = 64 * ES + 16, CPR = 64 * ES / 16, TPI = 64 / CPR, EPC = 16 / ES;
+      uint8_t* ob = p8_lds_buf + (size_t)w * 64 * PITCH;
+      /* the wave's 64 token scales: one load a lane, through LDS (past the 8 staging blocks) to every lane */
+      float* xsw = (float*)(p8_lds_buf + (size_t)8 * 64 * PITCH) + 64 * w;
+      xsw[lane] = tw0 + lane < M ? XS[(long long)(tw0 + lane) * NG] : 0.0f;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-    for(int i = 0; i < 2; ++i)
+      for(int i = 0; i < 2; ++i)
 #pragma unroll
-      for(int e = 0; e < 16; ++e){
-        const int tk = n0 + wt * 64 + i * 32 + (e & 3) + 8 * (e >> 2) + 4 * (lane >> 5);
-        if(tk < M){
-          const float xr = XS[(long long)tk * NG];
-          const float y0 = acc[i][0][e] * xr, y1 = acc[i][1][e] * xr;
-          if(cr0 < R){
-            if(Y) Y[(long long)tk * ldy + cr0] = y0;
-            if(Y16) Y16[(long long)tk * ldy + cr0] = __half_as_ushort(__float2half_rn(y0));
+        for(int e = 0; e < 16; ++e){
+          const int lt = i * 32 + (e & 3) + 8 * (e >> 2) + 4 * (lane >> 5);
+          const float xr = xsw[lt];
+#pragma unroll
+          for(int j = 0; j < 2; ++j){
+            float y = acc[i][j][e] * xr;
+            /* the fp32 product, then fp16 (two roundings, as the other products): the empty asm keeps the compiler
+               from folding the multiply into a mixed-precision instruction that rounds once */
+            asm volatile("" : "+v"(y));
+            T* d = (T*)(ob + lt * PITCH + ((lane & 31) + 32 * j) * ES);
+            if constexpr(ES == 4) *d = y;
+            else *d = __half_as_ushort(__float2half_rn(y));
           }
-          if(cr1 < R){
-            if(Y) Y[(long long)tk * ldy + cr1] = y1;
-            if(Y16) Y16[(long long)tk * ldy + cr1] = __half_as_ushort(__float2half_rn(y1));
+        }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for(int k = 0; k < 64 / TPI; ++k){
+        const int lt = lane / CPR + TPI * k, ck = lane % CPR, tk = tw0 + lt, row = rw0 + ck * EPC;
+        if(tk < M && row < R){
+          const uint4 v = *(const uint4*)(ob + lt * PITCH + ck * 16);
+          T* dst = Yp + (long long)tk * ldy + row;
+          if(row + EPC <= R) *(uint4*)dst = v;
+          else {                                                   /* the last rows of a ragged R */
+            const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for(int q = 0; q < EPC; ++q)
+              if(row + q < R){
+                if constexpr(ES == 4) dst[q] = __uint_as_float(vw[q]);
+                else dst[q] = (uint16_t)(vw[q >> 1] >> (16 * (q & 1)));
+              }
           }
         }
       }
+    };
+    if(Y){ staged(0.0f, Y); __syncthreads(); }
+    if(Y16){ staged((uint16_t)0, Y16); __syncthreads(); }
     t += gridDim.x;
     if(t < ntiles){
       tile_at(t);
