@@ -197,7 +197,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k
 #undef KT_PF_STEP
 #undef KT_PF_LOADW
 #undef KT_PF_LOADX
-  /* store: lanes of one register write 32 consecutive rows of one token */
+  /* store. fp16 rows 16-byte aligned (ldy % 8 == 0): each wave stages its 64 tokens x 64 rows in LDS (the X stages
+     are free once every wave is past its last group), token rows at a 16-byte-padded pitch, and writes 16 bytes a
+     lane, whole token rows in contiguous runs (8 store instructions in place of 64 two-byte ones). Else, and fp32,
+     lanes of one register write 32 consecutive rows of one token. */
+  const bool v16 = Y16 && (uintptr_t)Y16 % 16 == 0 && ldy % 8 == 0;
+  if(v16) __syncthreads();
 #pragma unroll
   for(int i = 0; i < 2; ++i)
 #pragma unroll
@@ -206,17 +211,46 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k
       if(t < M){
         const float xr = RS ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)t * NG * 4, 0, 0))
                             : 1.0f;
-        const float y0 = RS ? acc[i][0][e] * xr : acc[i][0][e], y1 = RS ? acc[i][1][e] * xr : acc[i][1][e];
+        float y0 = RS ? acc[i][0][e] * xr : acc[i][0][e], y1 = RS ? acc[i][1][e] * xr : acc[i][1][e];
+        /* the fp32 values, then fp16 (two roundings): not folded into a mixed-precision instruction */
+        asm volatile("" : "+v"(y0), "+v"(y1));
         if(cr0 < R){
           if(Y) Y[(long long)t * ldy + cr0] = y0;
-          if(Y16) Y16[(long long)t * ldy + cr0] = __half_as_ushort(__float2half_rn(y0));
+          if(Y16 && !v16) Y16[(long long)t * ldy + cr0] = __half_as_ushort(__float2half_rn(y0));
         }
         if(cr1 < R){
           if(Y) Y[(long long)t * ldy + cr1] = y1;
-          if(Y16) Y16[(long long)t * ldy + cr1] = __half_as_ushort(__float2half_rn(y1));
+          if(Y16 && !v16) Y16[(long long)t * ldy + cr1] = __half_as_ushort(__float2half_rn(y1));
+        }
+        if(v16){
+          const int lt = i * 32 + (e & 3) + 8 * (e >> 2) + 4 * (lane >> 5);
+          uint16_t* o = (uint16_t*)(&Xl[0][0] + wv * 64 * PF_LD + lt * PF_LD) + (lane & 31);
+          o[0] = __half_as_ushort(__float2half_rn(y0));
+          o[32] = __half_as_ushort(__float2half_rn(y1));
         }
       }
     }
+  if(v16){
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int tw0 = n0 + wt * 64, rw0 = r0 + wr * 64;
+#pragma unroll
+    for(int k = 0; k < 8; ++k){
+      const int lt = (lane >> 3) + 8 * k, t = tw0 + lt, row = rw0 + 8 * (lane & 7);
+      if(t < M && row < R){
+        const uint4 v = *(const uint4*)(&Xl[0][0] + wv * 64 * PF_LD + lt * PF_LD + 16 * (lane & 7));
+        uint16_t* dst = Y16 + (long long)t * ldy + row;
+        if(row + 8 <= R) *(uint4*)dst = v;
+        else {                                                     /* the last rows of a ragged R */
+          const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for(int q = 0; q < 8; ++q)
+            if(row + q < R) dst[q] = (uint16_t)(vw[q >> 1] >> (16 * (q & 1)));
+        }
+      }
+    }
+  }
 }
 
 #define KT_TG(DBG, RS) template __global__ void k_tern_gemm<DBG, RS>(const uint32_t*, const uint16_t*, int, int, \
@@ -360,7 +394,8 @@ __global__ void __launch_bounds__(64 * WT * WR) __attribute__((amdgpu_waves_per_
   for(int e = 0; e < 16; ++e){
     const int t = n0 + 32 * wt + (e & 3) + 8 * (e >> 2) + 4 * (lane >> 5);
     if(t < M && cr < R){
-      const float y = acc[e] * __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)t * NG * 4, 0, 0));
+      float y = acc[e] * __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)t * NG * 4, 0, 0));
+      asm volatile("" : "+v"(y));                                /* fp32, then fp16: two roundings */
       if(Y) Y[(long long)t * ldy + cr] = y;
       if(Y16) Y16[(long long)t * ldy + cr] = __half_as_ushort(__float2half_rn(y));
     }
