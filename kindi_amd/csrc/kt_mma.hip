@@ -235,6 +235,12 @@ __device__ __forceinline__ kt_v4i km_digits16(uint32_t w){
    the KQ = 1 tree ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)), then the slices in order: the same bits with 4
    times the waves. KQ = 2 (with MS, G = 8): k-lane quads, a wave's sum (c0 + c1) + (c2 + c3) of its four and wave 0
    adding the two quads. */
+#ifdef KT_TRACE
+#define KT_M16TS(k) do { if(kt_trace_on && lane == 0 && blockIdx.x < 512 && blockIdx.y == 0) \
+    kt_trace_buf[(blockIdx.x * 16 + wvi) * 8 + (k)] = __builtin_amdgcn_s_memrealtime(); } while(0)
+#else
+#define KT_M16TS(k) do {} while(0)
+#endif
 template <bool DBG, int KQ, bool MS>
 __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvArgs a, const int8_t* __restrict__ xq,
                                                   const float* __restrict__ xs, const int* __restrict__ xav,
@@ -244,7 +250,7 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
   constexpr int NT = KM_TOK, KM_PF = 2;                          /* tokens a pass */
   constexpr int CW = KT_KL / KQ;                                 /* k-lanes a wave */
   extern __shared__ __attribute__((aligned(16))) uint8_t kt_lds[];
-  float* red = (float*)kt_lds;                                   /* [KS][KQ][NT][32] slice (pair) sums */
+  float* red = (float*)kt_lds;                                   /* [KS][KQ][2][64] float4: the slice (pair) sums */
   const int NU = a.NU, S = kt_steps(NU);
   const int lane = threadIdx.x & 63, wvi = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   /* KQ = 1: wave ks = slice ks. KQ = 4: G slice groups, wave (sg, q) takes k-lanes 2 q, 2 q + 1 of slices sg,
@@ -253,6 +259,7 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
   const int sg = wvi / KQ, q = wvi % KQ, cb = q * CW;            /* slice group, quarter, first k-lane */
   const int g = lane >> 4, n = lane & 15;
   const int tile = blockIdx.x, t0 = blockIdx.y * NT;
+  KT_M16TS(0);
   int mi = 0;
   if(a.nmat > 1 && tile >= a.mat[1].pad) mi = 1;
   if(a.nmat > 2 && tile >= a.mat[2].pad) mi = 2;
@@ -334,6 +341,7 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
 #pragma unroll
   for(int i = 0; i < NI; ++i){ xsl[xdst[i]] = xsv[i]; xal[xdst[i]] = -xav4[i]; }        /* XA negated */
   kt_wave_sync();
+  KT_M16TS(1);
 #pragma unroll
   for(int cc = 0; cc < CW; ++cc){
     const int c = cb + cc;
@@ -394,18 +402,27 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
       }
     }
   }
+  KT_M16TS(2);
   /* slices in order (KQ = 4: the pair sums of a slice first, (p0 + p1) + (p2 + p3)) */
-#pragma unroll
-  for(int e = 0; e < 8; ++e) red[((size_t)(ks * KQ + q) * NT + 4 * g + (e & 3)) * 32 + 16 * (e >> 2) + n] = part[e];
+  /* a lane's 8 sums as two float4 at [slice][quarter][half][lane]: 16-byte LDS accesses, conflict free */
+  {
+    float4* r4 = (float4*)red + (size_t)(ks * KQ + q) * 128 + lane;
+    r4[0] = make_float4(part[0], part[1], part[2], part[3]);
+    r4[64] = make_float4(part[4], part[5], part[6], part[7]);
+  }
   }                                                              /* the wave's slices */
   __syncthreads();
+  KT_M16TS(3);
   if(wvi == 0){
     auto slice = [&](int k, float (&w)[8]){
       float p[KQ][8];
 #pragma unroll
-      for(int qq = 0; qq < KQ; ++qq)
-#pragma unroll
-        for(int e = 0; e < 8; ++e) p[qq][e] = red[((size_t)(k * KQ + qq) * NT + 4 * g + (e & 3)) * 32 + 16 * (e >> 2) + n];
+      for(int qq = 0; qq < KQ; ++qq){
+        const float4* r4 = (const float4*)red + (size_t)(k * KQ + qq) * 128 + lane;
+        const float4 lo = r4[0], hi = r4[64];
+        p[qq][0] = lo.x; p[qq][1] = lo.y; p[qq][2] = lo.z; p[qq][3] = lo.w;
+        p[qq][4] = hi.x; p[qq][5] = hi.y; p[qq][6] = hi.z; p[qq][7] = hi.w;
+      }
 #pragma unroll
       for(int e = 0; e < 8; ++e){
         if constexpr(KQ == 1) w[e] = p[0][e];
@@ -428,6 +445,7 @@ __global__ void __launch_bounds__(KQ == 1 ? 640 : 1024) k_gemv_m16(const KtGemvA
         if(!(e & 1) && t < a.M && ook[e >> 2]) m.y[(long long)(t >> 1) * m.ldy + orow[e >> 2]] = v[e] + v[e + 1];
       } else if(t < a.M && ook[e >> 2]) m.y[(long long)t * m.ldy + orow[e >> 2]] = v[e];
     }
+    KT_M16TS(4);
   }
 }
 

@@ -63,7 +63,7 @@ def _kernels(text):
 
 SCRATCH_OK = {"k_gemv_flat1<0, 1, true, false>", "k_gemv_pair<true>", "k_q8_mma<false, true, false>",
               "k_q8_mma<true, true, false>", "k_tern_gemm<true, false>", "k_tern_gemm<true, true>",
-              "k_tern_gemm_rs1<4, 2, 3, true>", "k_tern_gemm8<true>"}
+              "k_tern_gemm_rs1<4, 2, 3, true>", "k_tern_gemm8<true>", "k_gemv_m16<true, 2, true>"}
 
 
 def _demangle(names):
