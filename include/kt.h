@@ -148,8 +148,9 @@ int kt_tern_gemm(const void* W, int R, int C, const int8_t* XQ, int ldq, const f
    d - 1). Made per call or kept with the weights (4.25 times their bytes).
    kt_tern_gemm8: kt_tern_gemm with per_row = 1 over W8 and W's scales, with the same bits: Y = XS[t][0] *
    sum_g fmaf(v, d[r][g], .) in group order. The product reads both operands into LDS by DMA and unpacks nothing.
-   Grids of fewer 128-token x 256-row blocks than the GPU has CUs run kt_tern_gemm's packed-trit product instead
-   (the same bits). M ldq and the W8 bytes stay below 2^31. Replaces k_tc_mm2 (tc_hip.cu:243-269) and k_mm_g5q (chunk.cu:858-918) like
+   Grids of fewer 128-token x 256-row tiles than 0.7 of the GPU's CUs, and Y / Y16 not 16-byte aligned or ldy not a
+   multiple of 8 (the kernel writes 16-byte output rows), run kt_tern_gemm's packed-trit product instead (the same
+   bits). M ldq and the W8 bytes stay below 2^31. Replaces k_tc_mm2 (tc_hip.cu:243-269) and k_mm_g5q (chunk.cu:858-918) like
    kt_tern_gemm. */
 size_t kt_tern_expand_bytes(int R, int C);
 int kt_tern_expand(const void* W, int R, int C, int8_t* W8, void* stream);

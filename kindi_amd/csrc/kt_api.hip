@@ -606,13 +606,17 @@ int kt_tern_gemm8(const int8_t* W8, const void* W, int R, int C, const int8_t* X
   /* 32-bit buffer offsets, an out-of-range offset at 2^31 */
   if((long long)M * ldq >= (1ll << 31) || (long long)kt_r8(R) * KT_RG * C >= (1ll << 31)) return KT_INVALID;
   const uint16_t* scales = (const uint16_t*)((const uint8_t*)W + kt_code_bytes(R, NG));
-  /* a grid short of one 128 x 256 block a CU, or outputs the kernel's 16-byte row stores cannot take, run the
+  /* a grid short of 0.7 of a 128 x 256 tile a CU, or outputs the kernel's 16-byte row stores cannot take, run the
      packed-trit product instead (the same per-row numbers and order, so the same bits) */
   int cus = 0;
   const int ec = kt_cu_count(&cus);
   if(ec) return ec;
   const bool aligned = ldy % 8 == 0 && (!Y || kt_al(Y, 16)) && (!Y16 || kt_al(Y16, 16));   /* 16-byte output rows */
-  if((long long)((kt_r8(R) * KT_RG + 255) / 256) * ((M + 127) / 128) < cus || !aligned)
+#ifndef KT_G8_MIN_PCT
+#define KT_G8_MIN_PCT 70              /* tiles a CU, percent (measured on MI355X: gate/up [12288 x 4096] at 512 tokens,
+                                         192 tiles on 256 CUs, 53.7 -> 41.9 us over the packed-trit kernel) */
+#endif
+  if((long long)((kt_r8(R) * KT_RG + 255) / 256) * ((M + 127) / 128) * 100 < (long long)cus * KT_G8_MIN_PCT || !aligned)
     return kt_tern_gemm(W, R, C, XQ, ldq, XS, nullptr, 1, M, Y, Y16, ldy, dbg, stream);
   const size_t lds = kt_gemm8_lds();
   static std::once_flag once;
