@@ -285,7 +285,12 @@ def config2(torch, linear, synth, timer, steps):
                                        "frac_int8_peak": round(tops / INT8_PEAK, 4),
                                        "int8_copy_us": round(ms8 * 1e3, 1), "int8_copy_TOPS": round(tops8, 1),
                                        "int8_copy_frac_int8_peak": round(tops8 / INT8_PEAK, 4),
-                                       "expand_us": round(ms_x * 1e3, 1)}
+                                       "expand_us": round(ms_x * 1e3, 1),
+                                       # the faster of the two product paths (both give the same bits)
+                                       "best_TOPS": round(max(tops, tops8), 1),
+                                       "best_frac_int8_peak": round(max(tops, tops8) / INT8_PEAK, 4),
+                                       "best_path": "int8 trit copy (kt_tern_gemm8)" if tops8 > tops
+                                                    else "packed trits (kt_tern_gemm)"}
             # the vendor's plain int8 GEMM (hipBLASLt through torch._int_mm: int32 out, no scales, no trit unpack)
             # on the same shapes and box, as the practical ceiling of an int8 product here
             try:
