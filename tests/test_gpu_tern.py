@@ -533,13 +533,14 @@ def test_gguf_ptq1_by_name(kt, tmp_path):
 
 @pytest.mark.parametrize("R,C,M", [(64, 128, 1), (100, 256, 7), (300, 384, 130), (2048, 2048, 512),
                                    (8200, 128, 1000), (8200, 256, 1000), (8200, 384, 1000), (8200, 640, 1000),
-                                   (12288, 4096, 700), (4096, 12288, 2048), (12288, 1024, 512)])
+                                   (12288, 4096, 700), (4096, 12288, 2048), (12288, 1024, 512),
+                                   (12288, 128, 1500), (12288, 256, 2048), (12288, 384, 2048)])
 def test_gemm8(kt, R, C, M):
     """the int8-trit prefill product (kt_tern_expand + kt_tern_gemm8): the expanded trits equal the pack's digits - 1,
     the int32 group values equal the oracle's, and Y / Y16 carry the bits of kt_tern_gemm with per-row activations.
     Grids of at least 0.7 of a 128 x 256 tile a CU run the DMA kernel (ragged rows and tokens; 1, 2, 3 and 5 groups:
-    every turn of its two-group loop and both tails; 192 tiles on fewer blocks than CUs); smaller ones the packed-trit
-    kernel"""
+    every turn of its two-group loop and both tails; 192 tiles on fewer blocks than CUs; 2 and 3 tiles a block, so
+    the DMAs run ahead across tile ends and the token-scale slots rotate); smaller ones the packed-trit kernel"""
     lib, linear = kt
     say("gemm8", R, C, M)
     W, dig, bc, dpm = upload(linear, R, C, R * 5 + M)
