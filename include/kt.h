@@ -129,7 +129,9 @@ typedef struct kt_launch {
 int kt_record_begin(kt_launch* recs, int max);
 int kt_record_end(int* n);
 /* launch records recs[0 .. n) in order, record i on streams[i % nstreams] (1 to 16 streams), with
-   hipModuleLaunchKernel: Replay.launch (spec.py:303-320) as one C loop. */
+   hipModuleLaunchKernel: Replay.launch (spec.py:303-320) as one C loop. Launches on different streams carry no
+   order between them: a plan whose launches depend on each other (a decode step) takes one stream, as Replay.launch
+   replays on one (the null stream); several streams are for records that are independent in turn. */
 int kt_replay(const kt_launch* recs, int n, void* const* streams, int nstreams);
 
 /* ---------------------------------------------------------------- prefill product (any M, matrix cores)
