@@ -565,3 +565,27 @@ def test_gemm8(kt, R, C, M):
         Q, XS, XA = orc.quant_q8(X, per_row=True)
         assert np.array_equal(host(dbg), orc.tern_acc(bc, R, C, Q))
         assert np.array_equal(host(Y2).view(np.uint32), host(Y).view(np.uint32))
+
+
+@pytest.mark.parametrize("pad", [8, 4])
+def test_gemm8_strided_rows(kt, pad):
+    """the int8-trit prefill product into rows of a wider buffer (ldy = R + pad): a pad that keeps the 16-byte row
+    stores aligned (8 fp16 / fp32 elements) runs the DMA kernel, one that does not the packed-trit kernel; both write
+    exactly the R columns of each row, with kt_tern_gemm's bits, and leave the pad untouched"""
+    lib, linear = kt
+    R, C, M = 12288, 1024, 512
+    say("gemm8 strided", R, C, M, pad)
+    W, dig, bc, dpm = upload(linear, R, C, 77 + pad)
+    W8 = W.expand()
+    L = linear.Linear({"w": W})
+    X = rng(pad).normal(0, 1, (M, C)).astype(np.float32)
+    act = linear.quantize(dev(X), per_row=True)
+    Y = torch.empty((M, R), dtype=torch.float32, device="cuda")
+    Y16 = torch.empty((M, R), dtype=torch.float16, device="cuda")
+    L.gemm("w", act, Y=Y, Y16=Y16)
+    B = torch.full((M, R + pad), 7.0, dtype=torch.float32, device="cuda")
+    B16 = torch.full((M, R + pad), 7.0, dtype=torch.float16, device="cuda")
+    L.gemm8("w", act, W8, Y=B[:, :R], Y16=B16[:, :R])
+    assert np.array_equal(host(B[:, :R]).view(np.uint32), host(Y).view(np.uint32))
+    assert np.array_equal(host(B16[:, :R]).view(np.uint16), host(Y16).view(np.uint16))
+    assert bool((B[:, R:] == 7.0).all()) and bool((B16[:, R:] == 7.0).all())
