@@ -571,7 +571,8 @@ def test_gemm8(kt, R, C, M):
 def test_gemm8_strided_rows(kt, pad):
     """the int8-trit prefill product into rows of a wider buffer (ldy = R + pad): a pad that keeps the 16-byte row
     stores aligned (8 fp16 / fp32 elements) runs the DMA kernel, one that does not the packed-trit kernel; both write
-    exactly the R columns of each row, with kt_tern_gemm's bits, and leave the pad untouched"""
+    exactly the R columns of each row, with kt_tern_gemm's bits, and leave the pad untouched; and kt_tern_gemm itself
+    into the same rows"""
     lib, linear = kt
     R, C, M = 12288, 1024, 512
     say("gemm8 strided", R, C, M, pad)
@@ -586,6 +587,13 @@ def test_gemm8_strided_rows(kt, pad):
     B = torch.full((M, R + pad), 7.0, dtype=torch.float32, device="cuda")
     B16 = torch.full((M, R + pad), 7.0, dtype=torch.float16, device="cuda")
     L.gemm8("w", act, W8, Y=B[:, :R], Y16=B16[:, :R])
+    assert np.array_equal(host(B[:, :R]).view(np.uint32), host(Y).view(np.uint32))
+    assert np.array_equal(host(B16[:, :R]).view(np.uint16), host(Y16).view(np.uint16))
+    assert bool((B[:, R:] == 7.0).all()) and bool((B16[:, R:] == 7.0).all())
+    # the packed-trit product itself into the same wider rows (its 16-byte fp16 row stores need the aligned pad)
+    B.fill_(7.0)
+    B16.fill_(7.0)
+    L.gemm("w", act, Y=B[:, :R], Y16=B16[:, :R])
     assert np.array_equal(host(B[:, :R]).view(np.uint32), host(Y).view(np.uint32))
     assert np.array_equal(host(B16[:, :R]).view(np.uint16), host(Y16).view(np.uint16))
     assert bool((B[:, R:] == 7.0).all()) and bool((B16[:, R:] == 7.0).all())
