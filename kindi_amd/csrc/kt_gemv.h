@@ -11,6 +11,9 @@
    Loads are unconditional (a unit past the matrix reads the first 16 bytes of the codes) and only compute is
    skipped, by wave-uniform branches, so the compiler's wait counts stay exact. */
 #pragma once
+#ifndef KT_FLAT1_ONE
+#define KT_FLAT1_ONE 1                /* one-token dense ternary k_gemv_flat1: activations first (kt_gemv_one_body) */
+#endif
 #include "kt_common.h"
 
 #ifdef KT_TRACE                        /* a timeline build: per-block s_memrealtime stamps, one buffer per source file */
@@ -313,12 +316,103 @@ __device__ __forceinline__ void kt_gemv_flat_body(const KtGemvArgs& a, const KtG
   KT_GTS(3);
 }
 
+/* one token of a dense ternary launch whose slices have at most KT_SL steps (the one-token decode): the body above
+   for M = 1 with the loads in another order. The activation rows of the slice's steps go out first, then the
+   weights (the first halves c0 of every step, then the c1 halves, then the scales): loads retire in order, so the
+   staging waits for the activations alone while the weights are still in flight, and each step's first half can be
+   taken before the last weight bytes land. The same chains, butterfly and slice order, so the same bits. */
+template <bool DBG>
+__device__ __forceinline__ void kt_gemv_one_body(const KtGemvArgs& a, const int8_t* __restrict__ xq,
+                                                 const float* __restrict__ xs, const int* __restrict__ xa,
+                                                 int32_t* __restrict__ dbg, int KS){
+  extern __shared__ __attribute__((aligned(16))) uint8_t kt_lds[];
+  using F = KtFlat<KT_FMT_TERN, 1>;
+  constexpr int UW = F::UW, UP = F::UP, SL = KT_SL;
+  const int NU = a.NU, S = kt_steps(NU);
+  const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), r = lane & 7, c = lane >> 3;
+  const int g = blockIdx.x;
+  int mi = 0;
+  if(a.nmat > 1 && g >= a.mat[1].rg0) mi = 1;
+  if(a.nmat > 2 && g >= a.mat[2].rg0) mi = 2;
+  const KtMat& m = a.mat[mi];
+  const uint4* __restrict__ wb = (const uint4*)m.codes;
+  const uint16_t* __restrict__ sb = m.scales;
+  const int R = m.R, rg = g - m.rg0, row = rg * KT_RG + r;
+  const int s_lo = ks * S / KS, ns = (ks + 1) * S / KS - s_lo;      /* this slice's steps (1 .. SL) */
+  uint8_t* xw = kt_lds + (size_t)ks * F::XW;                         /* [SL][8][UP] */
+  float* red = (float*)(kt_lds + (size_t)KS * F::XW);                /* [KS][8] */
+  /* the activation rows of the slice's steps, the lane's unit scales and sums */
+  uint32_t sa[2][SL];
+  uint4 stg[SL];
+  const int o = lane * 16;
+#pragma unroll
+  for(int j = 0; j < SL; ++j){
+    const int s = s_lo + (j < ns ? j : 0), u = s * KT_KL + c, uu = (j < ns && u < NU) ? u : 0;
+    const int nc = NU - s * KT_KL < KT_KL ? NU - s * KT_KL : KT_KL;
+    sa[0][j] = __float_as_uint(xs[uu]);
+    sa[1][j] = (uint32_t)xa[uu];
+    const int oc = o < nc * UW ? o : 0;
+    stg[j] = *(const uint4*)(xq + (long long)s * KT_KL * UW + oc);
+  }
+  /* every weight offset (an integer select: a unit past the slice or the matrix reads offset 0), then the loads */
+  unsigned o0[SL], o1[SL], os[SL];
+#pragma unroll
+  for(int j = 0; j < SL; ++j){
+    const int s = s_lo + j, u = s * KT_KL + c;
+    const bool ok = j < ns && u < NU;
+    o0[j] = ok ? (unsigned)kt_widx(NU, rg, s, 0, c, r) : 0u;
+    o1[j] = ok ? (unsigned)kt_widx(NU, rg, s, 1, c, r) : 0u;
+    os[j] = ok ? (unsigned)kt_sidx(NU, rg, u, r) : 0u;
+  }
+  KtStep w[SL];
+#pragma unroll
+  for(int j = 0; j < SL; ++j) w[j].c0 = kt_ldnt(wb + o0[j]);
+#pragma unroll
+  for(int j = 0; j < SL; ++j) w[j].c1 = kt_ldnt(wb + o1[j]);
+#pragma unroll
+  for(int j = 0; j < SL; ++j) w[j].hs = sb[os[j]];
+  __builtin_amdgcn_sched_barrier(0);
+  kt_pin<SL>(&stg[0], &sa[0][0]);                                    /* every load above is issued before a write */
+  {
+    const bool in = o < KT_KL * UW;
+    const int lo = (o / UW) * UP + o % UW;
+#pragma unroll
+    for(int j = 0; j < SL; ++j) *(uint4*)(xw + (in ? j * KT_KL * UP + lo : F::XW - 16)) = stg[j];
+  }
+  kt_wave_sync();
+  float acc = 0.0f;
+#pragma unroll
+  for(int j = 0; j < SL; ++j){
+    const int u = (s_lo + j) * KT_KL + c;
+    if(j < ns){                                                      /* wave-uniform */
+      const bool uok = u < NU;
+      const float d = uok ? kt_h2f(w[j].hs) : 0.0f;
+      int v = kt_unit_lds<KT_FMT_TERN>(w[j].c0, w[j].c1, xw + (j * KT_KL + (uok ? c : 0)) * UP) - (int)sa[1][j];
+      v = uok ? v : 0;
+      acc = fmaf((float)v, __uint_as_float(sa[0][j]) * d, acc);
+      if(DBG && uok && row < R) dbg[(long long)row * NU + u] = v;
+    }
+  }
+  const float y = kt_row_sum(acc);
+  if(c == 0) red[ks * 8 + r] = y;
+  __syncthreads();
+  if(ks == 0 && c == 0){
+    float v = red[r];
+    for(int k = 1; k < KS; ++k) v += red[k * 8 + r];
+    if(row < R) m.y[row] = v;
+  }
+}
+
 /* one token a chunk: held to 64 VGPRs (8 waves a SIMD), so three 9-wave blocks fit a CU and the widest products
    run in one round of blocks */
 template <int FMT, int MT, bool DBG, bool GRP>
 __global__ void __launch_bounds__(64 * KT_KSMAX) __attribute__((amdgpu_waves_per_eu(8)))
 k_gemv_flat1(const KtGemvArgs a, const KtGroupedArgs ga, const int8_t* __restrict__ xq, const float* __restrict__ xs,
              const int* __restrict__ xa, int32_t* __restrict__ dbg, int KS){
+  if constexpr(KT_FLAT1_ONE && FMT == KT_FMT_TERN && MT == 1 && !GRP){
+    /* one token with slices of at most KT_SL steps (uniform): activations first */
+    if(a.M == 1 && !a.hp && kt_steps(a.NU) <= KT_SL * KS){ kt_gemv_one_body<DBG>(a, xq, xs, xa, dbg, KS); return; }
+  }
   kt_gemv_flat_body<FMT, MT, DBG, GRP>(a, ga, xq, xs, xa, dbg, KS);
 }
 template <int FMT, int MT, bool DBG, bool GRP>
