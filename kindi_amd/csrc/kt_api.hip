@@ -72,6 +72,9 @@ size_t kt_moe1_down_lds(int k, int KS);
 #ifndef KT_M16Q_WAVES
 #define KT_M16Q_WAVES 16384           /* matrix-core grids of at most this many waves split a slice over 4 waves */
 #endif
+#ifndef KT_STEP2_WAVES
+#define KT_STEP2_WAVES (1ll << 40)    /* one-token k_gemv_step grids of more slice-waves: two row groups a block (never) */
+#endif
 #ifndef KT_PAIR_WAVES
 #define KT_PAIR_WAVES 6144             /* one-token grids of more waves take two row groups a block (k_gemv_pair) */
 #endif
@@ -175,12 +178,14 @@ static int kt_launch_gemv(const KtGemvArgs& a, int ngroups, const int8_t* xq, co
   bool even = true;
   for(int i = 0; i < a.nmat; ++i) even = even && kt_r8(a.mat[i].R) % 2 == 0;
   if(FMT == KT_FMT_TERN && a.M == 1 && kt_steps(a.NU) <= 8){
-    /* one step a wave (rows of up to 8 steps, the same tree), two row groups a block where the one-row-group grid
-       exceeds the wave slots (measured on MI355X, 27B-class one-token launches against two steps a wave: gate/up
-       11.5 -> 10.9 us, q/k/v 5.6 -> 5.1 us, o 5.0 -> 4.7 us; step 1.91 -> 1.81 ms). Wider rows (the 27B down
-       projection: 17 steps) stay on k_gemv_flat1: 16-wave blocks of one step each were slower there */
+    /* one step a wave (rows of up to 8 steps, the same tree; measured on MI355X, 27B-class one-token launches against
+       two steps a wave: gate/up 11.5 -> 10.9 us, q/k/v 5.6 -> 5.1 us, o 5.0 -> 4.7 us; step 1.91 -> 1.81 ms), one
+       row group a block: with the activations loaded before the weights, the 27B gate/up grid (21,760 one-step waves,
+       more than the wave slots) is faster on one row group a block than on two (step 1.755 -> 1.736 ms), where it
+       was slower with the weights first. KT_STEP2_WAVES: grids of more slice-waves take two row groups a block. Wider
+       rows (the 27B down projection: 17 steps) stay on k_gemv_flat1: 16-wave blocks of one step each were slower */
     const int S = kt_steps(a.NU);
-    const bool two = even && (long long)ngroups * ks > KT_PAIR_WAVES;
+    const bool two = even && (long long)ngroups * ks > KT_STEP2_WAVES;
     const size_t lds = (size_t)S * KT_KL * KtFlat<KT_FMT_TERN, 1>::UP + (size_t)(two ? 2 : 1) * S * 64 * 4 * 2;
     const dim3 block(64 * S);
 #define KT_ST(RG) do { const dim3 grid(ngroups / RG); \
