@@ -607,7 +607,7 @@ def main():
     log("config 3, M=1")
     step, nbytes, calls, launches, stages = sweep_step(torch, linear, layers, 1)
     ms_l = timer.run(graphed(torch, step, use_graph), a.steps, a.warmup)
-    ms, nlaunch, kernel = ms_l, len(calls), "k_gemv_step<1> (q/k/v, o) + k_gemv_step<2> (gate/up) + k_gemv_flat1 (down)"
+    ms, nlaunch, kernel = ms_l, len(calls), "k_gemv_step<1> (q/k/v, o, gate/up) + k_gemv_flat1 (down)"
     replay = None
     if a.plan:
         # the same launches as records replayed from the host (no graph): Kindi's HIP plan replay
