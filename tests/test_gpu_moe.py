@@ -55,7 +55,7 @@ def test_q8_gemv(kt, R, C, M):
 
 
 @pytest.mark.parametrize("R", [96, 100])
-@pytest.mark.parametrize("C", [512, 1024, 1536, 2688, 3584, 4096])
+@pytest.mark.parametrize("C", [512, 1024, 1536, 1856, 2688, 3584, 4096])
 def test_grouped_mma_widths(kt, C, R):
     """the grouped matrix-core q8_0 product (16 entries an expert on average) at widths of 1 to 8 K slices: one slice
     a wave (up to 2 slices) and two waves taking the slices in turn (3 to 8, odd counts included). int32 unit values
