@@ -175,6 +175,53 @@ def test_moe_decode_validation(lib):
     assert lib.kt_moe_decode(f, f, 128, 2688, 1856, 6, f, 0, f, 2688, None, f, n, None) == 0       # nothing to do
 
 
+def test_validation_remaining_entries(lib):
+    """the entry points the tests above leave out: each rejects a bad argument (or does nothing for an empty call)
+    before any device call"""
+    f = ctypes.c_void_p(0x1000)
+    odd = ctypes.c_void_p(0x1008)                                  # not 16-byte aligned
+    assert lib.kt_error_string(INVALID)                              # a message for every return code
+    # q8_0 pack: C % 32, the output's alignment, null rows
+    assert lib.kt_q8_pack(f, 64, 48, f, None) == INVALID
+    assert lib.kt_q8_pack(f, 64, 64, odd, None) == INVALID
+    assert lib.kt_q8_pack(None, 64, 64, f, None) == INVALID
+    # the int8 trit copy and the product over it
+    assert lib.kt_tern_expand_bytes(100, 256) == 104 * 256               # rows padded to the kt2 row groups
+    assert lib.kt_tern_expand_bytes(64, 100) == 0
+    assert lib.kt_tern_expand(f, 64, 100, f, None) == INVALID
+    assert lib.kt_tern_expand(f, 64, 256, odd, None) == INVALID
+    assert lib.kt_tern_gemm8(f, f, 64, 256, f, 256, f, 0, f, None, 64, None, None) == 0           # nothing to do
+    assert lib.kt_tern_gemm8(f, f, 64, 256, f, 260, f, 1, f, None, 64, None, None) == INVALID     # ldq % 16
+    assert lib.kt_tern_gemm8(f, f, 64, 256, f, 256, f, 1, None, None, 64, None, None) == INVALID  # no output
+    assert lib.kt_tern_gemm8(f, f, 64, 256, f, 256, f, 1, f, None, 63, None, None) == INVALID     # ldy < R
+    assert lib.kt_tern_gemm8(f, f, 64, 256, f, 1 << 16, f, 1 << 15, f, None, 64, None, None) == INVALID  # 2^31 bytes
+    # three matrices in one launch: C % 128, a null output of a present matrix
+    assert lib.kt_tern_gemv3(f, 64, f, f, 64, f, f, 64, f, 100, f, 112, f, f, 1, None) == INVALID
+    assert lib.kt_tern_gemv3(f, 64, f, f, 64, None, f, 64, f, 256, f, 256, f, f, 1, None) == INVALID
+    assert lib.kt_tern_gemv3(f, 64, f, f, 64, f, f, 64, f, 256, f, 256, f, f, 0, None) == 0
+    # the grouped q8_0 product: C % 32, ldq % 16; no entries is a no-op
+    grouped = [f, 64, 64, 8, f, f, f, f, None, 4, 4, f, 64, f, 2, f, 64, None, None]
+    assert lib.kt_q8_grouped(*(grouped[:2] + [48] + grouped[3:12] + [48] + grouped[13:])) == INVALID
+    assert lib.kt_q8_grouped(*(grouped[:12] + [72] + grouped[13:])) == INVALID
+    assert lib.kt_q8_grouped(*(grouped[:9] + [0] + grouped[10:])) == 0
+    # combine: k > 16, null inputs; M = 0 is a no-op
+    assert lib.kt_moe_combine(f, None, f, f, 0, 6, 64, f, None) == 0
+    assert lib.kt_moe_combine(f, None, f, f, 1, 17, 64, f, None) == INVALID
+    assert lib.kt_moe_combine(None, None, f, f, 1, 6, 64, f, None) == INVALID
+    # the scorings of the routed entry points: sigmoid needs its bias, unknown ones are refused
+    route = [f, 1, 128, 6, 1, None, 1.0] + [f] * 8 + [None, 0, 0, None, 0, None, 0, None]
+    assert lib.kt_moe_route_r(*route) == INVALID
+    assert lib.kt_moe_route_r(*(route[:4] + [2, f] + route[6:])) == INVALID
+    assert lib.kt_moe_decode_r(f, f, 128, 2688, 1856, 6, 1, None, 1.0, f, 1, f, 2688, None, f, 1 << 20, None) == INVALID
+    assert lib.kt_moe_decode_r(f, f, 128, 2688, 1856, 6, 3, f, 1.0, f, 1, f, 2688, None, f, 1 << 20, None) == INVALID
+    # the no-allocation chain: its array's size, shapes past the one-wave route or past the array refused first
+    assert lib.kt_moe_decode_noalloc_max() == 4 << 20
+    assert lib.kt_moe_decode_noalloc(f, f, 128, 2688, 1856, 6, f, 0, f, 2688, None, None) == 0
+    assert lib.kt_moe_decode_noalloc(f, f, 128, 2688, 1856, 6, f, 11, f, 2688, None, None) == INVALID   # M k > 64
+    assert lib.kt_moe_decode_workspace(10, 6, 128, 4096, 16384) > lib.kt_moe_decode_noalloc_max()
+    assert lib.kt_moe_decode_noalloc(f, f, 128, 4096, 16384, 6, f, 10, f, 4096, None, None) == INVALID
+
+
 def test_no_fallback_without_library(tmp_path):
     """with the library absent the product path raises KernelError (no CPU fallback): a child process with
     KINDI_KT_LIB pointing at a missing file builds a TernaryMatrix and calls quantize"""
