@@ -77,7 +77,8 @@ __host__ __device__ __forceinline__ void kt_xcd_tile(int L, int gx, int gy, int&
 __device__ __forceinline__ float kt_h2f(uint16_t h){ return __half2float(__ushort_as_half(h)); }
 
 typedef unsigned int kt_u32x4 __attribute__((ext_vector_type(4)));
-/* a streaming 128-bit load (each weight byte is read once per product: keep it out of the caches' way) */
+/* a streaming 128-bit load (each weight byte is read once per product: keep it out of the caches' way; measured on
+   MI355X against plain loads, 27B-class step at one token 1.791 -> 1.737 ms) */
 __device__ __forceinline__ uint4 kt_ldnt(const uint4* p){
   const kt_u32x4 v = __builtin_nontemporal_load((const kt_u32x4*)p);
   return make_uint4(v.x, v.y, v.z, v.w);
