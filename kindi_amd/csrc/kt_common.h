@@ -78,7 +78,8 @@ __device__ __forceinline__ float kt_h2f(uint16_t h){ return __half2float(__ushor
 
 typedef unsigned int kt_u32x4 __attribute__((ext_vector_type(4)));
 /* a streaming 128-bit load (each weight byte is read once per product: keep it out of the caches' way; measured on
-   MI355X against plain loads, 27B-class step at one token 1.791 -> 1.737 ms) */
+   MI355X against plain loads, 27B-class step at one token 1.791 -> 1.737 ms; buffer loads with the same bit
+   1.733 ms, within the runs' spread, and with the scope bits sc0 / sc1 added no faster) */
 __device__ __forceinline__ uint4 kt_ldnt(const uint4* p){
   const kt_u32x4 v = __builtin_nontemporal_load((const kt_u32x4*)p);
   return make_uint4(v.x, v.y, v.z, v.w);
