@@ -91,6 +91,34 @@ def test_grouped_mma_widths(kt, C, R):
         assert np.array_equal(host(dense).view(np.uint32), y[p].view(np.uint32)), e
 
 
+def test_grouped_mma_odd_experts(kt):
+    """the grouped matrix-core product with an expert count that is not a multiple of 8 (13 experts, 3 picks, 64
+    tokens: about 15 entries an expert, the matrix-core path): every expert's rows bit-identical to the dense
+    product"""
+    lib, moe = kt
+    E, k, M, R, C = 13, 3, 64, 100, 2688
+    say("grouped mma odd E", E, R, C)
+    rows = [q8_case(R, C, 700 + e)[0] for e in range(E)]
+    ups = moe.Q8Experts(rows, R, C)
+    layer = moe.MoE(moe.Q8Experts([q8_case(32, 32, e)[0] for e in range(E)], 32, 32),
+                    moe.Q8Experts([q8_case(32, 32, 90 + e)[0] for e in range(E)], 32, 32), k)
+    r = rng(C + E)
+    ids = np.stack([r.permutation(E)[:k] for _ in range(M)]).astype(np.int32)
+    lists = layer.lists(dev(ids))
+    X = r.normal(0, 1, (M, C)).astype(np.float32)
+    Q, D = moe.q8_quantize(dev(X))
+    n = M * k
+    Y = torch.full((n, R), float("nan"), dtype=torch.float32, device="cuda")
+    ups.grouped(lists, M, Q, D, Y, xrow=True)
+    cnt, off, xrow, where = orc.moe_sort(ids, E)
+    y = host(Y)
+    for e in range(E):
+        p = np.arange(off[e], off[e] + cnt[e])
+        idx = torch.from_numpy(xrow[p]).cuda().long()
+        dense = moe.Q8Matrix(rows[e], R, C).gemv(Q[idx], D[idx])
+        assert np.array_equal(host(dense).view(np.uint32), y[p].view(np.uint32)), e
+
+
 @pytest.mark.parametrize("E,M", [(60, 1), (60, 300), (1024, 200), (1000, 700)])
 def test_sort_wide(kt, E, M):
     """kt_moe_sort at other expert counts (not a power of two, the 1024 maximum), one expert taking half the
