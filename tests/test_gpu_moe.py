@@ -401,7 +401,7 @@ def test_topk_nan_distinct(kt):
 
 
 @pytest.mark.parametrize("E,H,F,M,k", [(128, 2688, 1856, 1, 6), (128, 2688, 1856, 8, 6), (256, 96, 64, 1, 6),
-                                       (32, 96, 64, 40, 4)])
+                                       (32, 96, 64, 40, 4), (1024, 64, 32, 1, 8), (1024, 64, 32, 3, 8)])
 def test_moe_sigmoid_chain(kt, E, H, F, M, k):
     """the MoE layer with Kindi's router: kt_moe_decode_r gives x bit for bit as forward() (route_r / topk_r, sort,
     grouped up, relu^2 quantize, grouped down, combine), whose picks and weights are the oracle's"""
